@@ -1,0 +1,199 @@
+"""BF16 tensor <-> (sign/mantissa bytes, chunked Huffman exponents), with the
+reference's API (afterimage/runtime/compressed_store.py:28-303).
+
+bf16 bit layout, MSB to LSB: [sign:1][exponent:8][mantissa:7]. The stored
+sign/mantissa byte is (sign << 7) | mantissa; the exponent byte is
+entropy-coded. Decompression runs one fused gfx950 kernel per slice: Huffman
+decode of the exponents and the bit recombine
+``((sm & 0x80) << 8) | (e << 7) | (sm & 0x7F)`` write the bf16 output directly,
+so no exponent scratch tensor and no chain of elementwise torch kernels exist.
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import torch
+
+from .device import DeviceTensor, decode_bf16
+from .huffman_chunked import ChunkedEncoded, encode_chunked
+
+EXPONENT_SHIFT = 7
+
+
+@dataclasses.dataclass
+class CompressedLayer:
+    """(compressed_store.py:28-42)"""
+
+    sign_mantissa: torch.Tensor  # uint8, flat, CPU
+    encoded: ChunkedEncoded      # entropy-coded exponent field
+    shape: tuple[int, ...]
+
+    @property
+    def compressed_bytes(self) -> int:
+        return (self.sign_mantissa.numel() + self.encoded.packed.nbytes
+                + self.encoded.sym_lut.nbytes + self.encoded.len_lut.nbytes)
+
+    @property
+    def original_bytes(self) -> int:
+        return self.sign_mantissa.numel() * 2
+
+
+def split_fields(bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """(exponent, sign_mantissa) bytes of bf16 words given as uint16."""
+    exponent = ((bits >> EXPONENT_SHIFT) & 0xFF).astype(np.uint8)
+    sign_mantissa = (((bits >> 8) & 0x80) | (bits & 0x7F)).astype(np.uint8)
+    return exponent, sign_mantissa
+
+
+def compress_layer(W: torch.Tensor, chunk_size: int = 1024, max_bits: int = 16,
+                   work_chunk_elems: int = 1 << 24) -> CompressedLayer:
+    """Field split + chunked encode (compressed_store.py:48-91).
+
+    The split runs in bounded pieces of ``work_chunk_elems`` so no full-size
+    integer temporaries are built for large matrices.
+    """
+    assert W.dtype == torch.bfloat16, f"expected bfloat16, got {W.dtype}"
+    if work_chunk_elems < 1:
+        raise ValueError("work_chunk_elems must be positive")
+    raw = W.detach().contiguous().cpu().view(torch.int16).reshape(-1).numpy().view(np.uint16)
+    n = raw.shape[0]
+    exponent = np.empty(n, dtype=np.uint8)
+    sign_mantissa = np.empty(n, dtype=np.uint8)
+    for start in range(0, n, work_chunk_elems):
+        end = min(start + work_chunk_elems, n)
+        exponent[start:end], sign_mantissa[start:end] = split_fields(raw[start:end])
+    encoded = encode_chunked(exponent, chunk_size=chunk_size, max_bits=max_bits)
+    return CompressedLayer(sign_mantissa=torch.from_numpy(sign_mantissa), encoded=encoded,
+                           shape=tuple(W.shape))
+
+
+def _recombine(exponent: torch.Tensor, sign_mantissa: torch.Tensor,
+               shape: tuple) -> torch.Tensor:
+    """bf16 from decoded exponents and sign/mantissa bytes, in int16 throughout
+    (compressed_store.py:94-114): setting bit 15 of a value below 32768 is
+    subtracting 32768 in two's complement."""
+    e16 = exponent.to(torch.int16)
+    sm16 = sign_mantissa.to(torch.int16)
+    bits = (e16 << EXPONENT_SHIFT) | (sm16 & 0x7F)
+    bits = torch.where(sign_mantissa >= 128, bits - 32768, bits)
+    return bits.view(torch.bfloat16).reshape(shape)
+
+
+def recombine_exponent_and_sign_mantissa(exponent, sign_mantissa, shape: tuple,
+                                         device: str) -> torch.Tensor:
+    """Combine already-decoded exponents with sign/mantissa bytes
+    (compressed_store.py:117-130)."""
+    exp = torch.as_tensor(exponent, device=device)
+    sm = torch.as_tensor(sign_mantissa, device=device)
+    return _recombine(exp, sm, shape)
+
+
+def _slice_encoded(enc: ChunkedEncoded, c0: int, c1: int) -> ChunkedEncoded:
+    """Chunks [c0, c1) as a standalone ChunkedEncoded (compressed_store.py:133-158):
+    the byte range plus up to 8 following bytes, offsets rebased, and
+    ``n_symbols`` counting whole chunks."""
+    byte_start = int(enc.chunk_offsets[c0])
+    nbytes = enc.chunk_nbytes[c0:c1]
+    byte_end = int(enc.chunk_offsets[c1 - 1]) + int(nbytes[-1])
+    byte_end = min(byte_end + 8, enc.packed.shape[0])
+    return ChunkedEncoded(
+        packed=enc.packed[byte_start:byte_end],
+        chunk_offsets=(enc.chunk_offsets[c0:c1] - byte_start),
+        chunk_nbytes=nbytes,
+        sym_lut=enc.sym_lut,
+        len_lut=enc.len_lut,
+        max_bits=enc.max_bits,
+        chunk_size=enc.chunk_size,
+        n_symbols=(c1 - c0) * enc.chunk_size,
+        shape=((c1 - c0) * enc.chunk_size,),
+    )
+
+
+def _gpu_device(device) -> torch.device:
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise RuntimeError(
+            "afterimage_amd decodes on the GPU only (device %r); there is no CPU "
+            "decode path in this package" % (str(device),))
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    return dev
+
+
+def _tables_for(enc: ChunkedEncoded, dev: torch.device):
+    from . import gpu_decode_v2  # attribute looked up at call time
+
+    return gpu_decode_v2.prepare_decode_tables(enc, dev)
+
+
+def _decode_range_into(layer: CompressedLayer, c0: int, c1: int, out_flat: torch.Tensor,
+                       take: int, dev: torch.device, tables) -> None:
+    """Decode chunks [c0, c1) of ``layer`` into ``out_flat[:take]``."""
+    enc = layer.encoded
+    sub = enc if (c0 == 0 and c1 == enc.n_chunks) else _slice_encoded(enc, c0, c1)
+    s0 = c0 * enc.chunk_size
+    sm = layer.sign_mantissa.reshape(-1)[s0: s0 + take]
+    dt = DeviceTensor.from_encoded(sub, sm, dev, tables=tables)
+    dt.n_symbols = take
+    decode_bf16([dt], [out_flat])
+
+
+def decompress_layer_gpu(layer: CompressedLayer, device: str = "cuda",
+                         max_slice_elems: int = 1 << 25, *,
+                         reuse_decode_tables: bool = False) -> torch.Tensor:
+    """The exact original bf16 tensor, decoded on ``device``
+    (compressed_store.py:186-240).
+
+    Tensors above ``max_slice_elems`` elements are processed in chunk-range
+    slices, bounding the staged compressed input to one slice; the output is
+    written in place slice by slice. With ``reuse_decode_tables`` the tables
+    are prepared once for the whole call; otherwise once per slice (both go
+    through the content-keyed table cache). Work is ordered on the current
+    stream of ``device``; nothing here synchronises.
+    """
+    dev = _gpu_device(device)
+    enc = layer.encoded
+    n = enc.n_symbols
+    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    if n == 0:
+        return out.reshape(layer.shape)
+    tables = _tables_for(enc, dev) if reuse_decode_tables else None
+    if n <= max_slice_elems:
+        _decode_range_into(layer, 0, enc.n_chunks, out, n,
+                           dev, tables if tables is not None else _tables_for(enc, dev))
+        return out.reshape(layer.shape)
+    chunks_per_slice = max(1, max_slice_elems // enc.chunk_size)
+    for c0 in range(0, enc.n_chunks, chunks_per_slice):
+        c1 = min(c0 + chunks_per_slice, enc.n_chunks)
+        s0 = c0 * enc.chunk_size
+        s1 = min(c1 * enc.chunk_size, n)
+        _decode_range_into(layer, c0, c1, out[s0:s1], s1 - s0, dev,
+                           tables if tables is not None else _tables_for(enc, dev))
+    return out.reshape(layer.shape)
+
+
+def decompress_rows_gpu(layer: CompressedLayer, row_start: int, row_end: int,
+                        device: str = "cuda") -> torch.Tensor:
+    """Rows [row_start, row_end) of a 2-D compressed tensor
+    (compressed_store.py:254-303): the covering chunk range is decoded and
+    the exact element range returned as a (rows, cols) view."""
+    if len(layer.shape) != 2:
+        raise ValueError("decompress_rows_gpu needs a 2D tensor, got shape %r"
+                         % (layer.shape,))
+    dev = _gpu_device(device)
+    rows, cols = layer.shape
+    row_start = max(0, row_start)
+    row_end = min(rows, row_end)
+    if row_end <= row_start:
+        return torch.empty((0, cols), dtype=torch.bfloat16, device=dev)
+    enc = layer.encoded
+    cs = enc.chunk_size
+    e0, e1 = row_start * cols, row_end * cols
+    c0 = e0 // cs
+    c1 = min(enc.n_chunks, -(-e1 // cs))
+    base = c0 * cs
+    avail = min(enc.n_symbols, c1 * cs) - base
+    flat = torch.empty(avail, dtype=torch.bfloat16, device=dev)
+    _decode_range_into(layer, c0, c1, flat, avail, dev, _tables_for(enc, dev))
+    return flat[e0 - base:e1 - base].reshape(row_end - row_start, cols)

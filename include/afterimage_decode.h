@@ -1,0 +1,134 @@
+/*
+ * afterimage_decode.h -- C ABI of the MI355X (gfx950) lossless BF16 weight decoder.
+ *
+ * The decoder rebuilds BF16 tensors from Afterimage's compressed-store format:
+ *   - a raw sign/mantissa byte per weight: (sign << 7) | mantissa
+ *     (afterimage/runtime/compressed_store.py:78-88);
+ *   - the exponent byte, canonical-Huffman coded in fixed-symbol-count chunks.
+ *     Each chunk is its own MSB-first byte-aligned bitstream, located by
+ *     chunk_offsets / chunk_nbytes (afterimage/runtime/huffman_chunked.py:151-207).
+ *     The code is described by the stored flat LUT: sym_lut[2^max_bits] and
+ *     len_lut[2^max_bits] (afterimage/runtime/huffman.py:128-150).
+ *
+ * The reference has no C layer; its decode API is Python
+ * (afterimage/runtime/gpu_decode_v2.py, afterimage/runtime/compressed_store.py).
+ * Each entry point below names the Python function whose work it replaces.
+ * An FFI binding (ctypes) calls these with plain pointers and sizes.
+ *
+ * Conventions:
+ *   - Every function returns AIMG_OK (0) or a positive AIMG_ERR_* code.
+ *     aimg_last_error() returns the calling thread's last message.
+ *   - Pointers named "device" are HIP device pointers. Streams are hipStream_t
+ *     passed as void* (NULL = the null stream). Launches are asynchronous and
+ *     ordered on the given stream. Nothing here synchronises the device.
+ *   - No entry point allocates device memory.
+ *   - Functions are re-entrant.
+ */
+#ifndef AFTERIMAGE_DECODE_H
+#define AFTERIMAGE_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AIMG_OK 0
+#define AIMG_ERR_INVALID_ARGUMENT 1 /* bad size, null pointer, too many tensors */
+#define AIMG_ERR_BAD_TABLE 2        /* LUT is not a prefix-code table with byte symbols */
+#define AIMG_ERR_HIP 3              /* a HIP runtime call failed */
+#define AIMG_ERR_UNSUPPORTED 4      /* valid request that this build does not serve */
+
+/* Most tensors one aimg_decode_* call accepts (kernel-argument descriptors). */
+#define AIMG_MAX_TENSORS 32
+
+/* Library ABI version (bumped on any signature or table-layout change). */
+int aimg_abi_version(void);
+
+/* Message for the last non-OK status returned on this thread. */
+const char* aimg_last_error(void);
+
+/* ------------------------------------------------------------------------- */
+/* Decode tables.                                                            */
+/* Replaces prepare_decode_tables (afterimage/runtime/gpu_decode_v2.py:71-76), */
+/* which copies sym_lut / len_lut to the device as two int32 tensors. Here    */
+/* the stored LUT is turned on the host into one self-contained table blob:  */
+/* a 4096-entry multi-symbol window table (up to 6 codewords per 12-bit      */
+/* window) plus the stored LUT packed to 16 bits per entry for codewords     */
+/* longer than 12 bits. The caller copies the blob to device memory once per */
+/* codebook and may share it across every tensor with the same codebook.     */
+/* ------------------------------------------------------------------------- */
+
+/* Size in bytes of the table blob for a LUT of 2^max_bits entries (1..16). */
+int aimg_table_nbytes(int max_bits, size_t* nbytes);
+
+/*
+ * Build the table blob into host memory `out` (out_nbytes >= aimg_table_nbytes).
+ * sym_lut: int32[2^max_bits], len_lut: int8[2^max_bits], as stored by
+ * build_decode_lut (afterimage/runtime/huffman.py:128-150).
+ * Fails with AIMG_ERR_BAD_TABLE when a symbol is outside 0..255 (the
+ * reference asserts this, gpu_decode_v2.py:73-74), a length is outside
+ * 0..max_bits, or an entry is not replicated over its whole prefix span.
+ */
+int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, int max_bits,
+                     void* out, size_t out_nbytes);
+
+/* ------------------------------------------------------------------------- */
+/* Decode.                                                                   */
+/* ------------------------------------------------------------------------- */
+
+/* One tensor's device-resident compressed form (a ChunkedEncoded plus its
+ * sign/mantissa stream, huffman_chunked.py:135-148, compressed_store.py:28-42). */
+typedef struct aimg_tensor {
+    const uint8_t* packed;         /* device: chunk bitstreams, as stored       */
+    const int32_t* chunk_offsets;  /* device: byte offset of each chunk         */
+    const int32_t* chunk_nbytes;   /* device: byte length of each chunk         */
+    const uint8_t* sign_mantissa;  /* device: n_symbols bytes (bf16 only)       */
+    void* out;                     /* device: uint16 bf16 bits, or uint8        */
+    const void* table;             /* device: blob from aimg_build_table        */
+    int64_t packed_nbytes;         /* bytes readable at `packed`                */
+    int64_t n_symbols;             /* elements to write                         */
+    int32_t chunk_size;            /* symbols per chunk                         */
+    int32_t n_chunks;              /* chunks described by offsets / nbytes      */
+} aimg_tensor;
+
+/*
+ * Decode n_tensors tensors to BF16 in one launch: the Huffman decode of
+ * decode_gpu_v2 (gpu_decode_v2.py:79-117) fused with _recombine
+ * (compressed_store.py:94-114). out[i] = ((sm[i] & 0x80) << 8) | (exp[i] << 7)
+ * | (sm[i] & 0x7F) for i < n_symbols, where n_symbols <= n_chunks*chunk_size.
+ * Replaces the body of decompress_layer_gpu (compressed_store.py:186-240) for
+ * device-resident inputs; one call covers a whole decoder block of tensors.
+ */
+int aimg_decode_bf16(const aimg_tensor* tensors, int n_tensors, void* stream);
+
+/*
+ * Decode n_tensors exponent streams to uint8 symbols: decode_gpu_v2
+ * (gpu_decode_v2.py:79-117). sign_mantissa is ignored. Positions past a
+ * chunk's coded symbols decode as if the chunk's bytes were followed by zero
+ * bits, as the bounded CPU reader does (huffman_chunked.py:230-235).
+ */
+int aimg_decode_u8(const aimg_tensor* tensors, int n_tensors, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Encoder support (host).                                                   */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Pack symbols[0..n) chunk by chunk into MSB-first byte-aligned bitstreams:
+ * the packer of encode_chunked (huffman_chunked.py:41-78, :101-109).
+ * code_of[256] / len_of[256] give each symbol's canonical code and length
+ * (lengths 1..16; symbols that occur must have len_of > 0).
+ * Writes chunk_nbytes[ceil(n/chunk_size)] and the packed bytes into out
+ * (capacity out_cap); *total receives the packed byte count (no slack tail).
+ */
+int aimg_pack_chunked(const uint8_t* symbols, int64_t n, const uint32_t* code_of,
+                      const uint8_t* len_of, int32_t chunk_size, uint8_t* out,
+                      int64_t out_cap, int32_t* chunk_nbytes, int64_t* total);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AFTERIMAGE_DECODE_H */

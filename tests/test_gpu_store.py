@@ -1,0 +1,193 @@
+"""Full BF16 reconstruction on the GPU (decompress_layer_gpu and friends),
+bit-exact against the original weights and the oracle.
+
+Mirrors the reference's tests/test_compressed_store.py, test_sliced_decompress.py,
+test_decode_table_reuse.py and test_chunked_lm_head_gpu.py decode cases.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from afterimage_amd import workloads
+from afterimage_amd.runtime import device as devmod
+from afterimage_amd.runtime import gpu_decode_v2 as gd
+from afterimage_amd.runtime.compressed_store import (
+    compress_layer,
+    decompress_layer_gpu,
+    decompress_rows_gpu,
+)
+from afterimage_amd.runtime.device import DeviceTensor, decode_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16)
+
+
+def test_full_weight_reconstruction_bit_exact():
+    torch.manual_seed(0)
+    W = (torch.randn(128, 512) * 0.02).to(torch.bfloat16)
+    layer = compress_layer(W, chunk_size=256)
+    out = decompress_layer_gpu(layer)
+    assert out.dtype == torch.bfloat16 and out.shape == W.shape and out.is_cuda
+    assert torch.equal(_bits(out), _bits(W))
+    assert torch.equal(_bits(out), _bits(oracle.decompress_layer_reference(layer)))
+
+
+def test_bounded_work_chunks_preserve_every_bit():
+    torch.manual_seed(40)
+    W = (torch.randn(37, 59) * 0.02).to(torch.bfloat16)
+    layer = compress_layer(W, chunk_size=31, work_chunk_elems=17)
+    assert torch.equal(_bits(decompress_layer_gpu(layer)), _bits(W))
+
+
+@pytest.mark.parametrize("scale", [0.001, 0.02, 0.5, 3.0])
+def test_realistic_weight_scales(scale):
+    torch.manual_seed(1)
+    W = (torch.randn(64, 256) * scale).to(torch.bfloat16)
+    layer = compress_layer(W)
+    assert torch.equal(_bits(decompress_layer_gpu(layer)), _bits(W))
+
+
+def test_zero_negative_and_extreme_values():
+    W = torch.tensor([0.0, -0.0, 1.0, -1.0, 1e-30, -1e-30, 1e30, -1e30, 3.14159],
+                     dtype=torch.bfloat16).reshape(3, 3)
+    layer = compress_layer(W, chunk_size=9)
+    assert torch.equal(_bits(decompress_layer_gpu(layer)), _bits(W))
+
+
+def test_every_bf16_bit_pattern():
+    W = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    layer = compress_layer(W.reshape(256, 256), chunk_size=1024)
+    assert torch.equal(_bits(decompress_layer_gpu(layer)).reshape(-1), W.view(torch.int16))
+
+
+@pytest.mark.parametrize("shape", [(1, 100), (100, 1), (7, 13), (8960, 1536)])
+def test_shapes(shape):
+    torch.manual_seed(3)
+    W = (torch.randn(*shape) * 0.02).to(torch.bfloat16)
+    layer = compress_layer(W, chunk_size=512)
+    out = decompress_layer_gpu(layer)
+    assert out.shape == shape
+    assert torch.equal(_bits(out), _bits(W))
+
+
+def test_sliced_matches_unsliced():
+    torch.manual_seed(1)
+    W = (torch.randn(4096, 512) * 0.02).to(torch.bfloat16)
+    layer = compress_layer(W, chunk_size=1024)
+    big = decompress_layer_gpu(layer, max_slice_elems=1 << 30)
+    small = decompress_layer_gpu(layer, max_slice_elems=1 << 17)
+    assert torch.equal(_bits(big), _bits(small))
+    assert torch.equal(_bits(small), _bits(W))
+
+
+@pytest.mark.parametrize("slice_elems", [97, 1 << 20])
+def test_reused_tables_are_bit_exact_and_built_once_per_call(monkeypatch, slice_elems):
+    original = gd.prepare_decode_tables
+    seen = []
+
+    def prepare(enc, device="cuda"):
+        seen.append(id(enc))
+        return original(enc, device)
+
+    monkeypatch.setattr(gd, "prepare_decode_tables", prepare)
+    keys = []
+    for seed, scale in [(1, .01), (2, 10.)]:
+        torch.manual_seed(seed)
+        weight = (torch.randn(31, 59) * scale).to(torch.bfloat16)
+        layer = compress_layer(weight, chunk_size=31)
+        before = len(seen)
+        out = decompress_layer_gpu(layer, max_slice_elems=slice_elems, reuse_decode_tables=True)
+        assert torch.equal(_bits(out), _bits(weight))
+        assert len(seen) - before == 1
+        keys.append(original(layer.encoded, "cuda").key)
+    # Different codebooks never share a table.
+    assert keys[0] != keys[1]
+
+
+def test_reused_tables_on_nondefault_stream_and_special_bit_patterns():
+    bits = torch.tensor([0, -32768, 32640, -128, 32705, -63, 1, 127, 128,
+                         16256, -16512, 32767], dtype=torch.int16).reshape(3, 4)
+    layer = compress_layer(bits.view(torch.bfloat16), chunk_size=5)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        out = decompress_layer_gpu(layer, max_slice_elems=7, reuse_decode_tables=True)
+    stream.synchronize()
+    assert torch.equal(_bits(out), bits)
+
+
+def test_decompress_rows_matches_full_decode():
+    torch.manual_seed(17)
+    W = torch.randn(300, 64, dtype=torch.float32).to(torch.bfloat16)
+    layer = compress_layer(W, chunk_size=32)
+    full = decompress_layer_gpu(layer, device="cuda")
+    assert torch.equal(full, W.to("cuda"))
+    for step in (300, 128, 64, 7, 1):
+        parts = [decompress_rows_gpu(layer, r0, min(r0 + step, 300), device="cuda")
+                 for r0 in range(0, 300, step)]
+        assert torch.equal(torch.cat(parts, dim=0), full), "step=%d" % step
+    assert decompress_rows_gpu(layer, 5, 5, device="cuda").shape == (0, 64)
+
+
+def test_unaligned_output_view_uses_elementwise_stores():
+    torch.manual_seed(5)
+    W = (torch.randn(64, 96) * 0.02).to(torch.bfloat16)
+    layer = compress_layer(W, chunk_size=256)
+    dt = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, "cuda")
+    buf = torch.zeros(W.numel() + 3, dtype=torch.bfloat16, device="cuda")
+    decode_bf16([dt], [buf[3:]])
+    assert torch.equal(_bits(buf[3:]).reshape(W.shape), _bits(W))
+    assert torch.equal(_bits(buf[:3]), torch.zeros(3, dtype=torch.int16))
+
+
+def test_batched_block_launch_with_shared_codebooks():
+    """Several tensors in one launch; same-role tensors share one codebook
+    (encoded from the pooled histogram) and therefore one device table."""
+    shapes = [(512, 640), (128, 640), (128, 640), (512, 640), (640, 1088), (5120,)]
+    ws = [workloads.bf16_normal(s, 10 + i, 0.02, outlier_frac=1e-3) for i, s in enumerate(shapes)]
+    ws[-1] = workloads.bf16_normal((5120,), 99, 0.05, center=1.0)
+    layers = [compress_layer(w, chunk_size=4096) for w in ws]
+    dts = [DeviceTensor.from_encoded(l.encoded, l.sign_mantissa, "cuda") for l in layers]
+    outs = decode_bf16(dts)
+    for w, o in zip(ws, outs):
+        assert torch.equal(_bits(o), _bits(w).reshape(-1))
+    # Same LUT content -> same cached table object.
+    t0 = devmod.TABLES.get(layers[1].encoded.sym_lut, layers[1].encoded.len_lut,
+                           layers[1].encoded.max_bits, "cuda")
+    t1 = devmod.TABLES.get(layers[1].encoded.sym_lut.copy(), layers[1].encoded.len_lut.copy(),
+                           layers[1].encoded.max_bits, "cuda")
+    assert t0.blob.data_ptr() == t1.blob.data_ptr()
+
+
+def test_cpu_device_is_refused():
+    torch.manual_seed(20)
+    layer = compress_layer((torch.randn(16, 16) * 0.02).to(torch.bfloat16))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        decompress_layer_gpu(layer, device="cpu")
+
+
+def test_small_layer_1024x3072_chunk4096():
+    W, layer = workloads.small_layer()
+    out = decompress_layer_gpu(layer)
+    assert torch.equal(_bits(out), _bits(W))
+    exps = oracle.decode_chunked_reference(layer.encoded)
+    ref = oracle.recombine(exps, layer.sign_mantissa.numpy())
+    assert np.array_equal(_bits(out).numpy().reshape(-1).view(np.uint16), ref)
+
+
+def test_single_layer_5120x17408_chunk65536():
+    """The full-size layer: bit-exact against the seeded original (the
+    reference decoder is lossless, so its output is the original)."""
+    W, layer = workloads.single_layer()
+    assert layer.encoded.n_chunks == 1360
+    dt = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, "cuda")
+    (out,) = decode_bf16([dt])
+    assert torch.equal(_bits(out), _bits(W).reshape(-1))
+    # And the oracle agrees on a sample of chunks (the whole tensor is
+    # checked against W above).
+    exps = oracle.decode_chunks(layer.encoded, 0, 8, n_threads=4)
+    sm = layer.sign_mantissa.numpy()[: exps.size]
+    assert np.array_equal(_bits(out).numpy()[: exps.size].view(np.uint16), oracle.recombine(exps, sm))

@@ -1,0 +1,166 @@
+"""The C ABI library on the CPU: it loads, exports what include/afterimage_decode.h
+declares, and its host functions (table builder, packer) are right. No kernel
+is launched here."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from afterimage_amd import _native
+from afterimage_amd.runtime.device import build_table_blob
+from afterimage_amd.runtime.huffman import build_lengths, canonical_codes, code_arrays
+from afterimage_amd.runtime.huffman_chunked import ChunkedEncoded, pack_chunks
+from tests.golden_data import case, case_names
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "afterimage_decode.h"
+WIN_BITS = 12
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(aimg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    lib = _native.lib()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_native.EXPORTED_SYMBOLS)
+
+
+def test_abi_version_and_error_channel():
+    lib = _native.lib()
+    assert lib.aimg_abi_version() == _native.ABI_VERSION
+    n = ctypes.c_size_t()
+    assert lib.aimg_table_nbytes(17, ctypes.byref(n)) == _native.AIMG_ERR_INVALID_ARGUMENT
+    assert b"max_bits" in lib.aimg_last_error()
+    assert lib.aimg_table_nbytes(16, ctypes.byref(n)) == _native.AIMG_OK
+    assert n.value == 64 + 8 * 4096 + 2 * 65536
+
+
+def test_decode_entry_points_validate_before_launching():
+    lib = _native.lib()
+    arr = (_native.AimgTensor * 1)()
+    arr[0].chunk_size = 0
+    assert lib.aimg_decode_bf16(arr, 1, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    assert b"chunk_size" in lib.aimg_last_error()
+    arr[0].chunk_size = 16
+    arr[0].n_chunks = 1
+    arr[0].n_symbols = 17
+    assert lib.aimg_decode_u8(arr, 1, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    assert lib.aimg_decode_u8(arr, 33, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    arr[0].n_symbols = 16  # null device pointers
+    assert lib.aimg_decode_bf16(arr, 1, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    assert b"null" in lib.aimg_last_error()
+    # Nothing to decode is not an error and launches nothing.
+    arr[0].n_symbols = 0
+    assert lib.aimg_decode_bf16(arr, 1, None) == _native.AIMG_OK
+    assert lib.aimg_decode_bf16(arr, 0, None) == _native.AIMG_OK
+
+
+def test_table_builder_rejects_wide_symbols():
+    sym = np.array([0, 300], np.int32)
+    ln = np.array([1, 1], np.int8)
+    with pytest.raises(_native.NativeError, match="fit in a byte"):
+        build_table_blob(sym, ln, 1)
+
+
+def test_table_builder_rejects_non_prefix_lut():
+    sym = np.array([1, 1, 2, 2], np.int32)
+    ln = np.array([1, 2, 2, 2], np.int8)  # entry 1 claims length 2 inside a length-1 span
+    with pytest.raises(_native.NativeError, match="prefix"):
+        build_table_blob(sym, ln, 2)
+
+
+def _window_expectation(lengths, w):
+    """Codewords read one after another from the 12-bit window w, found by
+    matching each canonical code against the window's bits; kept while they
+    lie wholly inside the window (at most 6)."""
+    _, codes = canonical_codes(lengths)
+    bits = format(w, "012b")
+    out, pos = [], 0
+    while len(out) < 6:
+        hit = [s for s, c in codes.items()
+               if pos + lengths[s] <= WIN_BITS
+               and bits[pos: pos + lengths[s]] == format(c, "0%db" % lengths[s])]
+        assert len(hit) <= 1  # prefix property
+        if not hit:
+            break
+        out.append(hit[0])
+        pos += lengths[hit[0]]
+    return out
+
+
+def test_window_expectation_agrees_with_oracle_reader():
+    """The code-matching expectation and the oracle's LUT reader agree on
+    windows made of whole codewords."""
+    c = case("bf16_outliers_64k")
+    enc = c["encoded"]
+    lengths = {s: int(ln) for s, ln in enumerate(c["lengths"]) if ln > 0}
+    for w in range(0, 4096, 37):
+        want = _window_expectation(lengths, w)
+        body = np.array([(w >> 4) & 0xFF, (w & 0xF) << 4], np.uint8)
+        one = ChunkedEncoded(packed=body, chunk_offsets=np.array([0], np.int32),
+                             chunk_nbytes=np.array([2], np.int32), sym_lut=enc.sym_lut,
+                             len_lut=enc.len_lut, max_bits=enc.max_bits, chunk_size=8,
+                             n_symbols=8, shape=(8,))
+        assert list(oracle.decode_chunks(one)[: len(want)]) == want
+
+
+@pytest.mark.parametrize("name", ["bf16_outliers_64k", "dirichlet_6", "skewed_2sym",
+                                  "single_symbol", "fibonacci40_mb6"])
+def test_window_table_matches_oracle_reader(name):
+    c = case(name)
+    enc = c["encoded"]
+    lengths = {s: int(ln) for s, ln in enumerate(c["lengths"]) if ln > 0}
+    blob = build_table_blob(enc.sym_lut, enc.len_lut, enc.max_bits)
+    hdr = blob[:64].view(np.uint32)
+    assert hdr[0] == 0x474D4941 and hdr[2] == enc.max_bits
+    assert hdr[3] == min(lengths.values())
+    assert hdr[4] == enc.sym_lut[0]
+    win = blob[64: 64 + 8 * 4096].view(np.uint64)
+    glut = blob[64 + 8 * 4096:].view(np.uint16)
+    assert np.array_equal(glut & 0xFF, enc.sym_lut & 0xFF)
+    assert np.array_equal(glut >> 8, enc.len_lut.astype(np.uint16))
+    rng = np.random.default_rng(0)
+    for w in sorted(set(rng.integers(0, 4096, 400).tolist()) | {0, 4095}):
+        want = _window_expectation(lengths, w)
+        ent = int(win[w])
+        mask = ent & 0x1FFF
+        got_n = bin(mask).count("1") - 1
+        assert got_n == len(want), (w, want, hex(ent))
+        got = [(ent >> (16 + 8 * j)) & 0xFF for j in range(got_n)]
+        assert got == want
+        # Boundaries sit at the running code lengths.
+        bounds, pos = [0], 0
+        for s in want:
+            pos += lengths[s]
+            bounds.append(pos)
+        assert mask == sum(1 << b for b in bounds)
+
+
+@pytest.mark.parametrize("name", case_names())
+def test_native_packer_matches_reference(name):
+    c = case(name)
+    counts = np.bincount(c["symbols"], minlength=256)
+    freqs = {int(s): int(k) for s, k in enumerate(counts) if k > 0}
+    lengths = build_lengths(freqs, max_bits=c["max_bits"])
+    _, codes = canonical_codes(lengths)
+    body, nbytes = pack_chunks(c["symbols"], codes, lengths, c["chunk_size"],
+                               c["actual_max_bits"])
+    assert np.array_equal(nbytes, c["chunk_nbytes"])
+    assert np.array_equal(body, c["packed"][: body.size])
+
+
+def test_native_packer_rejects_symbol_without_code():
+    codes, lengths = {0: 0, 1: 1}, {0: 1, 1: 1}
+    with pytest.raises(_native.NativeError, match="no code"):
+        pack_chunks(np.array([0, 1, 5], np.uint8), codes, lengths, 4, 1)
+    with pytest.raises(ValueError):
+        code_arrays({300: 0}, {300: 1})
