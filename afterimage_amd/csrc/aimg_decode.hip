@@ -1,30 +1,44 @@
 // gfx950 kernels of libafterimage_decode: chunked canonical-Huffman exponent
 // decode fused with the BF16 recombine.
 //
-// One workgroup decodes one chunk. The chunk's bitstream is walked in rounds;
-// a round gives each of the 256 threads one segment of S bits (S a multiple
-// of 32, at most 256) and runs four phases:
+// Work layout. A workgroup has 1024 threads (16 waves) and one is resident
+// per CU; the grid is persistent and walks "items". An item is a batch of
+// chunks of one tensor: the workgroup splits into 1024/TPC sub-groups of TPC
+// threads (TPC = 16..1024, chosen per tensor from its chunk size so that a
+// chunk's symbols fill the sub-group's 64-bytes-per-thread staging area), and
+// each sub-group decodes one chunk.
+//
+// A sub-group walks its chunk's bitstream in rounds (one round for chunks of
+// up to TPC*224 bits). A round gives each thread one segment of S bits and
+// runs:
 //   1. stage the round's bytes in LDS as big-endian 32-bit words;
-//   2. count: every thread parses its segment and records where its first
-//      codeword boundary at or after the segment start lies (f) and where the
-//      first boundary at or after the segment end lies (e), plus how many
-//      codewords start in between. Thread 0 starts from the true boundary
-//      carried over from the previous round; every other thread starts
-//      speculatively 32 bits early, which Huffman codes of weight exponents
-//      resynchronise within in practice. Segment t is right iff its f equals
-//      segment t-1's e; any thread for which that fails re-parses from its
-//      predecessor's e until all agree, so the result never depends on
-//      resynchronisation happening;
+//   2. count: each thread parses its segment and records the first codeword
+//      boundary at or after the segment start (f), the first boundary at or
+//      after the segment end (e), and the codewords in between. Thread 0
+//      starts from the boundary carried over from the previous round; every
+//      other thread starts 32 bits early on a guess, which Huffman codes of
+//      weight exponents resynchronise within in practice. Segment t is right
+//      iff its f equals segment t-1's e; threads for which that fails
+//      re-parse from their predecessor's e until all agree, so the result
+//      never depends on resynchronisation happening;
 //   3. a workgroup prefix sum of the counts places each segment's symbols;
-//      threads re-parse from their true starts and write exponent bytes to an
-//      LDS staging buffer;
-//   4. the staged exponents are combined with the sign/mantissa bytes and
+//   4. each thread re-parses its segment and writes the exponents to the LDS
+//      staging area, one unaligned 8-byte store per table lookup. A store may
+//      run up to 7 bytes past the thread's symbols into the next threads'
+//      first 8 bytes; after a barrier every thread rewrites its own first 8
+//      bytes exactly;
+//   5. the staged exponents are combined with the sign/mantissa bytes and
 //      written with 16-byte stores (8 bf16 or 16 uint8 per store).
-// Codewords are read through a 12-bit window table (up to 6 codewords per
-// lookup); codewords longer than 12 bits go to the stored LUT in global memory.
+// If a round has more symbols than the staging area holds, steps 4-5 repeat
+// over windows of whole segments.
+//
+// Codewords are read through a 12-bit window table of up to 6 codewords per
+// lookup (LDS); codewords of 13..16 bits go through 16-entry escape blocks
+// (LDS for the first 64 blocks, global memory beyond).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "afterimage_decode.h"
@@ -33,14 +47,21 @@
 namespace aimg {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
+constexpr int kMinTpc = 16;
+constexpr int kMaxGroups = kThreads / kMinTpc;
 constexpr uint32_t kOverlapBits = 32;
-constexpr uint32_t kMaxSegBits = 256;
-constexpr uint32_t kMinSegBits = 64;
-constexpr uint32_t kStageBody = 32768;  // exponent bytes one round may stage
-constexpr uint32_t kStagePad = 64;      // carried lead (< 16) and slack
-constexpr uint32_t kTileWords = kThreads * kMaxSegBits / 32 + 4;
+constexpr uint32_t kMaxSegBits = 224;
+constexpr uint32_t kMinSegBits = 48;
+constexpr uint32_t kStagePerThread = 64;
+constexpr uint32_t kStageSlack = 32;  // per sub-group: carried lead (< 16) + store overrun
+constexpr uint32_t kTileSlackWords = 4;
+constexpr uint32_t kTileWords = kThreads * kMaxSegBits / 32 + kTileSlackWords * kMaxGroups;
+constexpr uint32_t kStageBytes = kThreads * kStagePerThread + kStageSlack * kMaxGroups;
+constexpr int kLdsEscBlocks = 64;
+constexpr uint32_t kTotalShift = 60;
+constexpr uint64_t kSymMask = 0xFFFFFFFFFFFFull;
 
 struct DevTensor {
     const uint8_t* packed;
@@ -51,19 +72,23 @@ struct DevTensor {
     const uint8_t* table;
     int64_t packed_nbytes;
     int64_t n_symbols;
-    int64_t job_begin;  // index of this tensor's first chunk in the launch
+    int64_t item_begin;  // first item of this tensor in the launch
+    int64_t n_jobs;      // chunks that hold output elements
     int32_t chunk_size;
-    int32_t n_chunks;
+    int32_t tpc;         // threads per chunk (power of two, 16..1024)
 };
 
 struct LaunchArgs {
     DevTensor t[AIMG_MAX_TENSORS];
+    int64_t total_items;
     int32_t n_tensors;
 };
 
-struct Adv {
-    uint32_t p;
-    uint32_t n;
+struct Tables {
+    const uint64_t* win;     // LDS window table
+    const uint16_t* esc;     // LDS escape blocks (first kLdsEscBlocks)
+    const uint16_t* gesc;    // all escape blocks, global memory
+    uint32_t sym0;
 };
 
 // 32 bits of the staged stream starting at bit q (MSB-first).
@@ -73,58 +98,121 @@ __device__ __forceinline__ uint32_t peek32(const uint32_t* tile, uint32_t q) {
     return static_cast<uint32_t>((v << (q & 31)) >> 32);
 }
 
-// Parse codewords from boundary p until the first boundary at or after x.
-// Returns that boundary and the number of codewords that start before x.
-__device__ __forceinline__ Adv advance(const uint32_t* tile, const uint64_t* win,
-                                       const uint16_t* glut, uint32_t gshift, uint32_t p,
+// (symbol, length) of an escape window's first codeword; w holds the window
+// in bits 31..20 and the next four bits in 19..16.
+__device__ __forceinline__ uint32_t escape(const Tables& tb, uint64_t ent, uint32_t w,
+                                           uint32_t* len) {
+    const uint32_t blk = static_cast<uint32_t>(ent) & 0xFFFFu;
+    if (blk == kUnusedBlock) {
+        *len = 1;
+        return tb.sym0;
+    }
+    const uint32_t at = blk * kEscBlockEntries + ((w >> 16) & 15u);
+    const uint32_t v = blk < static_cast<uint32_t>(kLdsEscBlocks) ? tb.esc[at] : tb.gesc[at];
+    const uint32_t l = v >> 8;
+    *len = l ? l : 1u;
+    return v & 0xFFu;
+}
+
+struct Adv {
+    uint32_t p;
+    uint32_t n;
+};
+
+// Parse codewords from boundary p until the first boundary at or after x;
+// returns that boundary and the number of codewords that start before x.
+__device__ __forceinline__ Adv advance(const uint32_t* tile, const Tables& tb, uint32_t p,
                                        uint32_t x) {
     uint32_t n = 0;
-    while (p < x) {
+    // Whole windows while no codeword of the window can reach x.
+    while (p + kWinBits <= x) {
         const uint32_t w = peek32(tile, p);
-        const uint64_t ent = win[w >> (32 - kWinBits)];
-        const uint32_t m = static_cast<uint32_t>(ent) & 0x1FFFu;
-        if (m == 1u) {
-            const uint32_t l = glut[w >> gshift] >> 8;
-            p += l ? l : 1u;
+        const uint64_t ent = tb.win[w >> (32 - kWinBits)];
+        const uint32_t hi = static_cast<uint32_t>(ent >> 32);
+        const uint32_t total = hi >> (kTotalShift - 32);
+        if (total == 0) {
+            uint32_t l;
+            escape(tb, ent, w, &l);
+            p += l;
             n += 1;
             continue;
         }
-        const uint32_t rel = x - p;
-        const uint32_t total = 31u - __clz(m);
-        const uint32_t low = rel > static_cast<uint32_t>(kWinBits) ? 0x1FFFu : ((1u << rel) - 1u);
-        n += __popc(m & low & ~(1u << total));
-        p += total < rel ? total : static_cast<uint32_t>(__ffs(m & ~low) - 1);
+        n += __popc(hi & 0x0FFF0000u);
+        p += total;
+    }
+    while (p < x) {
+        const uint32_t w = peek32(tile, p);
+        const uint64_t ent = tb.win[w >> (32 - kWinBits)];
+        const uint32_t hi = static_cast<uint32_t>(ent >> 32);
+        const uint32_t total = hi >> (kTotalShift - 32);
+        if (total == 0) {
+            uint32_t l;
+            escape(tb, ent, w, &l);
+            p += l;
+            n += 1;
+            continue;
+        }
+        const uint32_t ends = (hi >> 16) & 0xFFFu;  // bit k-1: a codeword ends at offset k
+        const uint32_t rel = x - p;                 // 1..11
+        const uint32_t upto = total < rel ? total : rel;
+        // Codewords starting before rel: the one at offset 0 plus every end
+        // boundary at offset 1..upto-1.
+        n += 1 + __popc(ends & ((1u << (upto - 1)) - 1u));
+        p += total < rel ? total : rel - 1 + __ffs(ends >> (rel - 1));
     }
     return {p, n};
 }
 
-// Parse from true boundary p to true boundary x, writing each codeword's
-// symbol to stage[pos++] while pos < lim.
-__device__ __forceinline__ void emit(const uint32_t* tile, const uint64_t* win,
-                                     const uint16_t* glut, uint32_t gshift, uint32_t p,
-                                     uint32_t x, uint8_t* stage, uint32_t pos, uint32_t lim) {
-    while (p < x) {
+// Re-parse from true boundary p and write `count` symbols to stage[q...],
+// one unaligned 8-byte store per lookup (stores may run 7 bytes past).
+__device__ __forceinline__ void emit_run(const uint32_t* tile, const Tables& tb, uint32_t p,
+                                         uint8_t* stage, uint32_t q, uint32_t count) {
+    const uint32_t q_end = q + count;
+    while (q < q_end) {
         const uint32_t w = peek32(tile, p);
-        const uint64_t ent = win[w >> (32 - kWinBits)];
-        const uint32_t m = static_cast<uint32_t>(ent) & 0x1FFFu;
-        if (m == 1u) {
-            const uint32_t g = glut[w >> gshift];
-            const uint32_t l = g >> 8;
-            if (pos < lim) stage[pos] = static_cast<uint8_t>(g);
-            ++pos;
-            p += l ? l : 1u;
-            continue;
+        const uint64_t ent = tb.win[w >> (32 - kWinBits)];
+        const uint32_t hi = static_cast<uint32_t>(ent >> 32);
+        const uint32_t total = hi >> (kTotalShift - 32);
+        uint64_t syms = ent;
+        uint32_t n = __popc(hi & 0x0FFF0000u);
+        if (total == 0) {
+            uint32_t l;
+            syms = escape(tb, ent, w, &l);
+            n = 1;
+            p += l;
+        } else {
+            p += total;
         }
-        const uint32_t rel = x - p;
-        const uint32_t total = 31u - __clz(m);
-        const uint32_t low = rel > static_cast<uint32_t>(kWinBits) ? 0x1FFFu : ((1u << rel) - 1u);
-        const uint32_t cnt = __popc(m & low & ~(1u << total));
-        const uint64_t syms = ent >> 16;
-#pragma unroll
-        for (uint32_t j = 0; j < static_cast<uint32_t>(kMaxSymsPerWindow); ++j)
-            if (j < cnt && pos + j < lim) stage[pos + j] = static_cast<uint8_t>(syms >> (8 * j));
-        pos += cnt;
-        p += total < rel ? total : rel;
+        __builtin_memcpy(stage + q, &syms, 8);
+        q += n;
+    }
+}
+
+// The first min(8, count) symbols from true boundary p, written exactly.
+__device__ __forceinline__ void write_head(const uint32_t* tile, const Tables& tb, uint32_t p,
+                                           uint8_t* stage, uint32_t q, uint32_t count) {
+    const uint32_t h = count < 8 ? count : 8;
+    uint64_t acc = 0;
+    for (uint32_t k = 0; k < h;) {
+        const uint32_t w = peek32(tile, p);
+        const uint64_t ent = tb.win[w >> (32 - kWinBits)];
+        const uint32_t hi = static_cast<uint32_t>(ent >> 32);
+        const uint32_t total = hi >> (kTotalShift - 32);
+        if (total == 0) {
+            uint32_t l;
+            acc |= static_cast<uint64_t>(escape(tb, ent, w, &l)) << (8 * k);
+            k += 1;
+            p += l;
+        } else {
+            acc |= (ent & kSymMask) << (8 * k);
+            k += __popc(hi & 0x0FFF0000u);
+            p += total;
+        }
+    }
+    if (h == 8) {
+        __builtin_memcpy(stage + q, &acc, 8);
+    } else {
+        for (uint32_t k = 0; k < h; ++k) stage[q + k] = static_cast<uint8_t>(acc >> (8 * k));
     }
 }
 
@@ -142,7 +230,7 @@ __device__ __forceinline__ uint32_t load_be_word(const uint8_t* cbytes, int64_t 
     return __builtin_bswap32(v);
 }
 
-__device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* s_wsum, uint32_t* total) {
+__device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* s_wsum) {
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     uint32_t x = v;
@@ -153,21 +241,15 @@ __device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* s_wsum
     }
     if (lane == 63) s_wsum[w] = x;
     __syncthreads();
-    uint32_t pre = 0, tot = 0;
+    uint32_t pre = 0;
 #pragma unroll
-    for (int i = 0; i < kWaves; ++i) {
-        const uint32_t s = s_wsum[i];
-        pre += i < w ? s : 0u;
-        tot += s;
-    }
-    __syncthreads();
-    *total = tot;
+    for (int i = 0; i < kWaves; ++i) pre += i < w ? s_wsum[i] : 0u;
     return pre + x - v;
 }
 
-// bf16 bits of two elements from two sign/mantissa bytes and two exponents:
-// ((sm & 0x80) << 8) | (e << 7) | (sm & 0x7F), the closed form of _recombine
-// (compressed_store.py:94-114). x holds e<<8|sm in each 16-bit half.
+// bf16 bits of two elements: x holds e<<8|sm in each 16-bit half;
+// ((sm & 0x80) << 8) | (e << 7) | (sm & 0x7F) is the closed form of
+// _recombine (compressed_store.py:94-114).
 __device__ __forceinline__ uint32_t bf16_pair(uint32_t x) {
     return ((x >> 1) & 0x7F807F80u) | (x & 0x007F007Fu) | ((x & 0x00800080u) << 8);
 }
@@ -185,153 +267,229 @@ __device__ __forceinline__ void store_one(const DevTensor& T, int64_t el, uint32
     }
 }
 
-// kGroup: elements per store (8 for bf16 / 16 for uint8 with 16-byte
-// stores, 1 for the element-wise path used when alignment does not allow).
+// Write staged vector group g (kGroup elements) to output element el.
 template <bool kBf16, int kGroup>
-__global__ __launch_bounds__(kThreads) void decode_kernel(LaunchArgs args) {
+__device__ __forceinline__ void store_group(const DevTensor& T, const uint8_t* stage, int64_t el) {
+    if (kGroup == 1) {
+        store_one<kBf16>(T, el, stage[0]);
+    } else if (kBf16) {
+        const uint2 smv = *reinterpret_cast<const uint2*>(T.sm + el);
+        const uint2 ev = *reinterpret_cast<const uint2*>(stage);
+        uint4 o4;
+        o4.x = bf16_pair(__builtin_amdgcn_perm(ev.x, smv.x, 0x05010400u));
+        o4.y = bf16_pair(__builtin_amdgcn_perm(ev.x, smv.x, 0x07030602u));
+        o4.z = bf16_pair(__builtin_amdgcn_perm(ev.y, smv.y, 0x05010400u));
+        o4.w = bf16_pair(__builtin_amdgcn_perm(ev.y, smv.y, 0x07030602u));
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.out) + el) = o4;
+    } else {
+        *reinterpret_cast<uint4*>(static_cast<uint8_t*>(T.out) + el) =
+            *reinterpret_cast<const uint4*>(stage);
+    }
+}
+
+template <bool kBf16, int kGroup>
+__global__ __launch_bounds__(kThreads) void decode_kernel(const LaunchArgs args) {
     __shared__ uint64_t s_win[kWinEntries];
+    __shared__ uint16_t s_esc[kLdsEscBlocks * kEscBlockEntries];
     __shared__ uint32_t s_tile[kTileWords];
-    __shared__ __attribute__((aligned(16))) uint8_t s_stage[kStageBody + kStagePad];
+    __shared__ __attribute__((aligned(16))) uint8_t s_stage[kStageBytes];
     __shared__ uint32_t s_f[kThreads];
     __shared__ uint32_t s_e[kThreads];
     __shared__ uint32_t s_wsum[kWaves];
+    __shared__ uint32_t s_gpre[kMaxGroups + 1];
+    __shared__ uint32_t s_gval[kMaxGroups];
 
-    const int tid = threadIdx.x;
-    const int64_t job = blockIdx.x;
-    int d = 0;
-    while (d + 1 < args.n_tensors && job >= args.t[d + 1].job_begin) ++d;
-    const DevTensor& T = args.t[d];
-    const int64_t c = job - T.job_begin;
+    const uint32_t tid = threadIdx.x;
+    const uint8_t* loaded = nullptr;
+    Tables tb;
+    tb.win = s_win;
+    tb.esc = s_esc;
 
-    const TableHeader* hdr = reinterpret_cast<const TableHeader*>(T.table);
-    const uint32_t gshift = 32u - hdr->max_bits;
-    const uint32_t min_len = hdr->min_len;
-    const uint32_t sym0 = hdr->sym0;
-    const uint16_t* glut = reinterpret_cast<const uint16_t*>(T.table + kGlutOffset);
-    {
-        const uint4* src = reinterpret_cast<const uint4*>(T.table + kWinOffset);
-        uint4* dst = reinterpret_cast<uint4*>(s_win);
-        for (int i = tid; i < kWinEntries / 2; i += kThreads) dst[i] = src[i];
-    }
+    for (int64_t item = blockIdx.x; item < args.total_items; item += gridDim.x) {
+        int d = 0;
+        while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
+        const DevTensor& T = args.t[d];
+        const uint32_t lg = static_cast<uint32_t>(__ffs(T.tpc) - 1);
+        const uint32_t tpc = 1u << lg;
+        const uint32_t g = tid >> lg;
+        const uint32_t i = tid & (tpc - 1);
+        const uint32_t n_groups = kThreads >> lg;
+        const int64_t c = (item - T.item_begin) * n_groups + g;
+        const bool has_chunk = c < T.n_jobs;
 
-    int64_t off = T.offsets[c];
-    int64_t nb = T.nbytes[c];
-    off = off < 0 ? 0 : (off > T.packed_nbytes ? T.packed_nbytes : off);
-    nb = nb < 0 ? 0 : (nb > T.packed_nbytes - off ? T.packed_nbytes - off : nb);
-    const uint8_t* cbytes = T.packed + off;
-    const int64_t chunk_bits = nb * 8;
-    const int64_t chunk_base = c * T.chunk_size;
-    int64_t lim = T.n_symbols - chunk_base;
-    lim = lim < 0 ? 0 : (lim > T.chunk_size ? T.chunk_size : lim);
-
-    uint32_t smax = (kStageBody * min_len) / kThreads;
-    smax = (smax > kMaxSegBits ? kMaxSegBits : smax) & ~31u;
-    const int64_t per_round_max = static_cast<int64_t>(kThreads) * smax;
-    const int64_t nr = (chunk_bits + per_round_max - 1) / per_round_max;
-    uint32_t S = kMinSegBits;
-    if (nr > 0) {
-        const int64_t per_thread = (chunk_bits + kThreads * nr - 1) / (kThreads * nr);
-        S = static_cast<uint32_t>((per_thread + 31) & ~int64_t(31));
-        S = S < kMinSegBits ? kMinSegBits : S;
-    }
-    const uint32_t round_bits = kThreads * S;
-
-    uint32_t p0 = 0;      // true start of the next round, relative to its first bit
-    int64_t ob = 0;       // chunk-local symbols produced so far
-    uint32_t lead = 0;    // staged symbols carried from the previous round
-    uint32_t tail_at = 0; // stage index of those carried symbols after the loop
-    for (int64_t r = 0; r < nr; ++r) {
-        const int64_t R0 = r * round_bits;
-        const int64_t left_bits = chunk_bits - R0;
-        const uint32_t RB = left_bits < round_bits ? static_cast<uint32_t>(left_bits) : round_bits;
-        const uint32_t nw = (RB + 31) / 32 + 2;
-        for (uint32_t j = tid; j < nw; j += kThreads)
-            s_tile[j] = load_be_word(cbytes, nb, R0 / 8 + 4 * static_cast<int64_t>(j));
-        __syncthreads();
-
-        const uint32_t seg_lo = tid * S;
-        const bool active = seg_lo < RB;
-        const uint32_t seg_hi = active ? (seg_lo + S < RB ? seg_lo + S : RB) : 0u;
-        uint32_t f = 0, e = 0, cnt = 0;
-        if (active) {
-            f = tid == 0 ? p0 : advance(s_tile, s_win, glut, gshift, seg_lo - kOverlapBits, seg_lo).p;
-            const Adv a = advance(s_tile, s_win, glut, gshift, f, seg_hi);
-            e = a.p;
-            cnt = a.n;
+        __syncthreads();  // the previous item is done with LDS
+        if (T.table != loaded) {
+            loaded = T.table;
+            const uint4* src = reinterpret_cast<const uint4*>(T.table + kWinOffset);
+            uint4* dst = reinterpret_cast<uint4*>(s_win);
+            for (uint32_t j = tid; j < kWinEntries / 2; j += kThreads) dst[j] = src[j];
+            const TableHeader* hdr = reinterpret_cast<const TableHeader*>(T.table);
+            const uint32_t n_esc = hdr->n_esc_blocks < static_cast<uint32_t>(kLdsEscBlocks)
+                                       ? hdr->n_esc_blocks : kLdsEscBlocks;
+            const uint16_t* gesc = reinterpret_cast<const uint16_t*>(T.table + kEscOffset);
+            for (uint32_t j = tid; j < n_esc * kEscBlockEntries; j += kThreads) s_esc[j] = gesc[j];
         }
-        s_f[tid] = f;
-        s_e[tid] = e;
+        const TableHeader* hdr = reinterpret_cast<const TableHeader*>(T.table);
+        tb.sym0 = hdr->sym0;
+        tb.gesc = reinterpret_cast<const uint16_t*>(T.table + kEscOffset);
+
+        int64_t off = 0, nb = 0, lim = 0;
+        const int64_t chunk_base = c * T.chunk_size;
+        if (has_chunk) {
+            off = T.offsets[c];
+            nb = T.nbytes[c];
+            off = off < 0 ? 0 : (off > T.packed_nbytes ? T.packed_nbytes : off);
+            nb = nb < 0 ? 0 : (nb > T.packed_nbytes - off ? T.packed_nbytes - off : nb);
+            lim = T.n_symbols - chunk_base;
+            lim = lim < 0 ? 0 : (lim > T.chunk_size ? T.chunk_size : lim);
+        }
+        const uint8_t* cbytes = T.packed + off;
+        const int64_t chunk_bits = nb * 8;
+        const int64_t per_round_max = static_cast<int64_t>(tpc) * kMaxSegBits;
+        const int64_t nr = (chunk_bits + per_round_max - 1) / per_round_max;
+        uint32_t S = kMinSegBits;
+        if (nr > 0) {
+            const int64_t per_thread = (chunk_bits + tpc * nr - 1) / (tpc * nr);
+            S = static_cast<uint32_t>((per_thread + 7) & ~int64_t(7));
+            S = S < kMinSegBits ? kMinSegBits : S;
+        }
+        const uint32_t round_bits = tpc * S;
+        uint32_t* tile = s_tile + g * (tpc * kMaxSegBits / 32 + kTileSlackWords);
+        const uint32_t region = tpc * kStagePerThread + kStageSlack;
+        uint8_t* stage = s_stage + g * region;
+
+        if (i == 0) s_gval[g] = static_cast<uint32_t>(nr);
         __syncthreads();
-        for (;;) {
-            const bool bad = active && tid > 0 && s_f[tid] != s_e[tid - 1];
-            const uint32_t nf = bad ? s_e[tid - 1] : 0u;
-            if (!__syncthreads_or(bad)) break;
-            if (bad) {
-                f = nf;
-                const Adv a = advance(s_tile, s_win, glut, gshift, f, seg_hi);
+        uint32_t NR = 0;
+        for (uint32_t k = 0; k < n_groups; ++k) NR = NR > s_gval[k] ? NR : s_gval[k];
+
+        uint32_t p0 = 0;       // true start of the next round, relative to its first bit
+        int64_t ob = 0;        // chunk-local symbols written or staged so far
+        uint32_t lead = 0;     // staged symbols carried into the next window
+        uint32_t tail_at = 0;  // stage index of the symbols carried out of the last round
+        for (uint32_t r = 0; r < NR; ++r) {
+            const bool g_active = r < nr;
+            const int64_t R0 = static_cast<int64_t>(r) * round_bits;
+            uint32_t RB = 0;
+            if (g_active) {
+                const int64_t left = chunk_bits - R0;
+                RB = left < round_bits ? static_cast<uint32_t>(left) : round_bits;
+            }
+            const uint32_t nw = g_active ? (RB + 31) / 32 + 3 : 0;
+            for (uint32_t j = i; j < nw; j += tpc)
+                tile[j] = load_be_word(cbytes, nb, R0 / 8 + 4 * static_cast<int64_t>(j));
+            __syncthreads();
+
+            const uint32_t seg_lo = i * S;
+            const bool active = seg_lo < RB;
+            const uint32_t seg_hi = active ? (seg_lo + S < RB ? seg_lo + S : RB) : 0u;
+            uint32_t f = 0, e = 0, cnt = 0;
+            if (active) {
+                f = i == 0 ? p0 : advance(tile, tb, seg_lo - kOverlapBits, seg_lo).p;
+                const Adv a = advance(tile, tb, f, seg_hi);
                 e = a.p;
                 cnt = a.n;
-                s_f[tid] = f;
-                s_e[tid] = e;
             }
+            s_f[tid] = f;
+            s_e[tid] = e;
             __syncthreads();
+            for (;;) {
+                const bool bad = active && i > 0 && s_f[tid] != s_e[tid - 1];
+                const uint32_t nf = bad ? s_e[tid - 1] : 0u;
+                if (!__syncthreads_or(bad)) break;
+                if (bad) {
+                    f = nf;
+                    const Adv a = advance(tile, tb, f, seg_hi);
+                    e = a.p;
+                    cnt = a.n;
+                    s_f[tid] = f;
+                    s_e[tid] = e;
+                }
+                __syncthreads();
+            }
+
+            const uint32_t excl = block_scan_excl(cnt, s_wsum);
+            if (i == 0) s_gpre[g] = excl;
+            if (tid == kThreads - 1) s_gpre[n_groups] = excl + cnt;
+            const uint32_t n_active = g_active ? (RB + S - 1) / S : 1u;
+            __syncthreads();
+            const uint32_t e_last = s_e[g * tpc + n_active - 1];
+            const uint32_t o = excl - s_gpre[g];
+            const uint32_t gtot = s_gpre[g + 1] - s_gpre[g];
+            const int64_t room = lim - ob;
+            const uint32_t want = g_active ? (gtot < room ? gtot : static_cast<uint32_t>(room)) : 0u;
+            const uint32_t run = (active && o < want) ? (cnt < want - o ? cnt : want - o) : 0u;
+            bool done = run == 0;
+            uint32_t base = 0;  // sub-group symbol index at the start of this window
+            if (i == 0) s_gval[g] = want;
+            __syncthreads();
+            for (;;) {
+                const uint32_t cap = region - 8 - lead;
+                const bool go = !done && o + run - base <= cap;
+                if (go) emit_run(tile, tb, f, stage, lead + o - base, run);
+                if (!done && !go) atomicMin(&s_gval[g], o);
+                __syncthreads();
+                if (go) write_head(tile, tb, f, stage, lead + o - base, run);
+                __syncthreads();
+                const uint32_t wend = s_gval[g];
+                const uint32_t avail = lead + (wend - base);
+                const uint32_t nfull = avail / kGroup;
+                const int64_t a0 = chunk_base + ob - lead;
+                for (uint32_t v = i; v < nfull; v += tpc)
+                    store_group<kBf16, kGroup>(T, stage + v * kGroup,
+                                               a0 + static_cast<int64_t>(v) * kGroup);
+                ob += wend - base;
+                base = wend;
+                done = done || go;
+                const uint32_t rem = avail - nfull * kGroup;
+                const bool more = __syncthreads_or(!done);
+                // Carry the partial vector group to the front of the staging
+                // area when this sub-group has symbols still to come.
+                const bool carry = g_active && (wend < want || r + 1 < nr);
+                const uint8_t keep = (carry && i < rem) ? stage[nfull * kGroup + i] : 0;
+                if (g_active) {
+                    tail_at = carry ? 0u : nfull * kGroup;
+                    lead = rem;
+                }
+                if (i == 0) s_gval[g] = want;
+                __syncthreads();
+                if (carry && i < rem) stage[i] = keep;
+                if (!more) break;
+                __syncthreads();
+            }
+            if (g_active) p0 = e_last - RB;
         }
 
-        uint32_t total;
-        const uint32_t o = block_scan_excl(cnt, s_wsum, &total);
-        const int64_t room = lim - ob;
-        uint32_t take = total < room ? total : static_cast<uint32_t>(room);
-        if (take > kStageBody) take = kStageBody;  // only malformed streams get here
-        if (active && cnt > 0)
-            emit(s_tile, s_win, glut, gshift, f, e, s_stage, lead + o, lead + take);
-        const uint32_t n_active = (RB + S - 1) / S;
-        const uint32_t e_last = s_e[n_active - 1];
+        // Symbols carried out of the last round, then positions no codeword
+        // of the chunk reached: those decode from zero bits, i.e. to sym_lut[0].
         __syncthreads();
-
-        const int64_t a0 = chunk_base + ob - lead;
-        const uint32_t avail = lead + take;
-        const uint32_t nfull = avail / kGroup;
-        for (uint32_t g = tid; g < nfull; g += kThreads) {
-            const int64_t el = a0 + static_cast<int64_t>(g) * kGroup;
-            if (kGroup == 1) {
-                store_one<kBf16>(T, el, s_stage[g]);
-            } else if (kBf16) {
-                const uint2 smv = *reinterpret_cast<const uint2*>(T.sm + el);
-                const uint2 ev = *reinterpret_cast<const uint2*>(s_stage + g * kGroup);
-                uint4 o4;
-                o4.x = bf16_pair(__builtin_amdgcn_perm(ev.x, smv.x, 0x05010400u));
-                o4.y = bf16_pair(__builtin_amdgcn_perm(ev.x, smv.x, 0x07030602u));
-                o4.z = bf16_pair(__builtin_amdgcn_perm(ev.y, smv.y, 0x05010400u));
-                o4.w = bf16_pair(__builtin_amdgcn_perm(ev.y, smv.y, 0x07030602u));
-                *reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.out) + el) = o4;
-            } else {
-                *reinterpret_cast<uint4*>(static_cast<uint8_t*>(T.out) + el) =
-                    *reinterpret_cast<const uint4*>(s_stage + g * kGroup);
-            }
+        const int64_t t0 = chunk_base + ob - lead;
+        const int64_t n_tail = lim - (ob - lead);
+        for (int64_t k = i; k < n_tail; k += tpc) {
+            const uint32_t ex = k < lead ? stage[tail_at + k] : tb.sym0;
+            store_one<kBf16>(T, t0 + k, ex);
         }
-        ob += take;
-        const uint32_t rem = avail - nfull * kGroup;
-        if (r + 1 < nr) {
-            __syncthreads();
-            const uint8_t carry = tid < static_cast<int>(rem) ? s_stage[nfull * kGroup + tid] : 0;
-            __syncthreads();
-            if (tid < static_cast<int>(rem)) s_stage[tid] = carry;
-            tail_at = 0;
-        } else {
-            tail_at = nfull * kGroup;
-        }
-        lead = rem;
-        p0 = e_last - RB;
     }
+}
 
-    // Symbols carried out of the last round, then positions no codeword of
-    // the chunk reached: those decode from zero bits, i.e. to sym_lut[0].
-    const int64_t t0 = chunk_base + ob - lead;
-    const int64_t n_tail = lim - (ob - lead);
-    for (int64_t i = tid; i < n_tail; i += kThreads) {
-        const uint32_t e = i < lead ? s_stage[tail_at + i] : sym0;
-        store_one<kBf16>(T, t0 + i, e);
-    }
+int cu_count() {
+    static std::once_flag once;
+    static int n = 0;
+    std::call_once(once, [] {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 0;
+    });
+    return n > 0 ? n : 256;
+}
+
+uint32_t threads_per_chunk(int32_t chunk_size) {
+    uint32_t t = kMinTpc;
+    while (t < static_cast<uint32_t>(kThreads) &&
+           static_cast<int64_t>(t) * kStagePerThread < chunk_size)
+        t <<= 1;
+    return t;
 }
 
 template <bool kBf16>
@@ -341,7 +499,7 @@ int launch(const aimg_tensor* ts, int n, void* stream) {
         return fail(AIMG_ERR_INVALID_ARGUMENT,
                     "n_tensors must be in 0.." + std::to_string(AIMG_MAX_TENSORS));
     LaunchArgs args{};
-    int64_t jobs = 0;
+    int64_t items = 0;
     bool vec = true;
     const int group = kBf16 ? 8 : 16;
     int m = 0;
@@ -372,20 +530,23 @@ int launch(const aimg_tensor* ts, int n, void* stream) {
         dt.packed_nbytes = t.packed_nbytes;
         dt.n_symbols = t.n_symbols;
         dt.chunk_size = t.chunk_size;
-        dt.n_chunks = t.n_chunks;
-        dt.job_begin = jobs;
+        dt.tpc = static_cast<int32_t>(threads_per_chunk(t.chunk_size));
         // Chunks past the last output element hold nothing to write.
-        jobs += (t.n_symbols + t.chunk_size - 1) / t.chunk_size;
+        dt.n_jobs = (t.n_symbols + t.chunk_size - 1) / t.chunk_size;
+        dt.item_begin = items;
+        const int64_t per_item = kThreads / dt.tpc;
+        items += (dt.n_jobs + per_item - 1) / per_item;
     }
     args.n_tensors = m;
-    if (jobs == 0) return AIMG_OK;
-    if (jobs > 0x7FFFFFFF) return fail(AIMG_ERR_UNSUPPORTED, "more than 2^31-1 chunks in one launch");
+    args.total_items = items;
+    if (items == 0) return AIMG_OK;
+    const int64_t grid = items < cu_count() ? items : cu_count();
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid(static_cast<uint32_t>(jobs)), block(kThreads);
+    const dim3 gdim(static_cast<uint32_t>(grid)), bdim(kThreads);
     if (vec) {
-        hipLaunchKernelGGL((decode_kernel<kBf16, kBf16 ? 8 : 16>), grid, block, 0, s, args);
+        hipLaunchKernelGGL((decode_kernel<kBf16, kBf16 ? 8 : 16>), gdim, bdim, 0, s, args);
     } else {
-        hipLaunchKernelGGL((decode_kernel<kBf16, 1>), grid, block, 0, s, args);
+        hipLaunchKernelGGL((decode_kernel<kBf16, 1>), gdim, bdim, 0, s, args);
     }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess)

@@ -29,7 +29,7 @@ extern "C" int aimg_table_nbytes(int max_bits, size_t* nbytes) {
     if (max_bits < 1 || max_bits > 16)
         return fail(AIMG_ERR_INVALID_ARGUMENT,
                     "max_bits must be in 1..16, got " + std::to_string(max_bits));
-    *nbytes = aimg::table_nbytes(max_bits);
+    *nbytes = aimg::table_nbytes();
     return AIMG_OK;
 }
 
@@ -38,17 +38,13 @@ extern "C" int aimg_table_nbytes(int max_bits, size_t* nbytes) {
 // max_bits-wide window i starts with, replicated over every window sharing
 // that codeword's prefix; windows no codeword covers hold (0, 0).
 //
-// The blob derived here serves the decoder in two levels:
-//  * window table: for each 12-bit window, the codewords that lie wholly
-//    inside it when they are read one after another from bit 0 (at most 6),
-//    as a boundary bitmask (bit k set when a codeword starts or ends at bit
-//    offset k) and the symbols, one byte each. A window whose first codeword
-//    is longer than 12 bits (or unused) has mask 1 and sends the reader to
-//    the second level.
-//  * the stored LUT itself, 16 bits per entry (symbol | length << 8).
-// Reading one codeword through either level gives exactly the (symbol,
-// length) that the stored LUT gives for the same bits, which is what the
-// reference bit reader computes (huffman_chunked.py:237-244).
+// The blob derived here serves the decoder in two levels (layout in
+// aimg_internal.h): a 12-bit window table listing the codewords that lie
+// wholly inside each window, and 16-entry escape blocks for windows whose
+// first codeword is 13..16 bits long. Reading a codeword through either level
+// gives exactly the (symbol, length) that the stored LUT gives for the same
+// bits, which is what the reference bit reader computes
+// (huffman_chunked.py:237-244).
 extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, int max_bits,
                                 void* out, size_t out_nbytes) {
     if (sym_lut == nullptr || len_lut == nullptr || out == nullptr)
@@ -56,14 +52,13 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
     if (max_bits < 1 || max_bits > 16)
         return fail(AIMG_ERR_INVALID_ARGUMENT,
                     "max_bits must be in 1..16, got " + std::to_string(max_bits));
-    const size_t need = aimg::table_nbytes(max_bits);
+    const size_t need = aimg::table_nbytes();
     if (out_nbytes < need)
         return fail(AIMG_ERR_INVALID_ARGUMENT,
                     "table buffer too small: " + std::to_string(out_nbytes) + " < " +
                         std::to_string(need));
     const uint32_t size = 1u << max_bits;
 
-    uint32_t min_len = 0;
     for (uint32_t i = 0; i < size; ++i) {
         const int32_t s = sym_lut[i];
         const int32_t l = len_lut[i];
@@ -77,6 +72,7 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
     }
     // Walk the spans: an entry of length l starts an aligned run of
     // 2^(max_bits - l) identical entries (the windows sharing its prefix).
+    uint32_t min_len = 0;
     for (uint32_t i = 0; i < size;) {
         const uint32_t l = static_cast<uint32_t>(len_lut[i]);
         if (l == 0) {
@@ -100,6 +96,53 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
 
     auto* blob = static_cast<uint8_t*>(out);
     std::memset(blob, 0, need);
+    auto* wt = reinterpret_cast<uint64_t*>(blob + aimg::kWinOffset);
+    auto* esc = reinterpret_cast<uint16_t*>(blob + aimg::kEscOffset);
+    // (symbol, length) of the codeword starting at the first bit of `bits`
+    // (MSB-first, zeros past the window).
+    auto lut_at = [&](uint32_t bits, uint32_t* sym, uint32_t* len) {
+        const uint32_t idx = bits >> (32 - max_bits);
+        *sym = static_cast<uint32_t>(sym_lut[idx]) & 0xFFu;
+        *len = static_cast<uint32_t>(len_lut[idx]);
+    };
+    uint32_t n_blocks = 0;
+    for (uint32_t w = 0; w < static_cast<uint32_t>(aimg::kWinEntries); ++w) {
+        const uint32_t bits = w << (32 - aimg::kWinBits);
+        uint32_t pos = 0, mask = 0, k = 0;
+        uint64_t syms = 0;
+        while (k < static_cast<uint32_t>(aimg::kMaxSymsPerWindow)) {
+            uint32_t s, l;
+            lut_at(bits << pos, &s, &l);
+            if (l == 0 || pos + l > static_cast<uint32_t>(aimg::kWinBits)) break;
+            syms |= static_cast<uint64_t>(s) << (8 * k);
+            ++k;
+            pos += l;
+            mask |= 1u << (pos - 1);
+        }
+        if (k > 0) {
+            wt[w] = syms | (static_cast<uint64_t>(mask) << 48) | (static_cast<uint64_t>(pos) << 60);
+            continue;
+        }
+        // Escape window: one entry per value of the next four bits.
+        uint16_t block[aimg::kEscBlockEntries];
+        bool any = false;
+        for (uint32_t e4 = 0; e4 < static_cast<uint32_t>(aimg::kEscBlockEntries); ++e4) {
+            uint32_t s, l;
+            lut_at(bits | (e4 << (32 - aimg::kWinBits - 4)), &s, &l);
+            block[e4] = static_cast<uint16_t>(s | (l << 8));
+            any = any || l != 0;
+        }
+        if (!any) {
+            wt[w] = aimg::kUnusedBlock;
+            continue;
+        }
+        if (n_blocks >= static_cast<uint32_t>(aimg::kMaxEscBlocks))
+            return fail(AIMG_ERR_BAD_TABLE, "more than 256 windows start with a codeword "
+                                            "longer than 12 bits");
+        std::memcpy(esc + n_blocks * aimg::kEscBlockEntries, block, sizeof(block));
+        wt[w] = n_blocks++;
+    }
+
     aimg::TableHeader hdr{};
     hdr.magic = aimg::kTableMagic;
     hdr.version = aimg::kAbiVersion;
@@ -107,31 +150,8 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
     hdr.min_len = min_len == 0 ? 1 : min_len;
     hdr.sym0 = static_cast<uint32_t>(sym_lut[0]);
     hdr.len0 = static_cast<uint32_t>(len_lut[0]);
-    hdr.glut_entries = size;
+    hdr.n_esc_blocks = n_blocks;
     std::memcpy(blob, &hdr, sizeof(hdr));
-
-    auto* glut = reinterpret_cast<uint16_t*>(blob + aimg::kGlutOffset);
-    for (uint32_t i = 0; i < size; ++i)
-        glut[i] = static_cast<uint16_t>((sym_lut[i] & 0xFF) |
-                                        (static_cast<uint32_t>(len_lut[i]) << 8));
-
-    auto* wt = reinterpret_cast<uint64_t*>(blob + aimg::kWinOffset);
-    for (uint32_t w = 0; w < (1u << aimg::kWinBits); ++w) {
-        // Window bits MSB-first in a 32-bit word, zeros after the window.
-        const uint32_t bits = w << (32 - aimg::kWinBits);
-        uint32_t pos = 0, mask = 1, k = 0;
-        uint64_t syms = 0;
-        while (k < aimg::kMaxSymsPerWindow) {
-            const uint32_t idx = (bits << pos) >> (32 - max_bits);
-            const uint32_t l = static_cast<uint32_t>(len_lut[idx]);
-            if (l == 0 || pos + l > aimg::kWinBits) break;
-            syms |= static_cast<uint64_t>(sym_lut[idx] & 0xFF) << (8 * k);
-            ++k;
-            pos += l;
-            mask |= 1u << pos;
-        }
-        wt[w] = static_cast<uint64_t>(mask) | (syms << 16);
-    }
     return AIMG_OK;
 }
 

@@ -8,15 +8,29 @@
 
 namespace aimg {
 
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 constexpr uint32_t kTableMagic = 0x474D4941u;  // "AIMG"
 
-// Window table: 2^kWinBits entries of 64 bits, each
-//   bits  0..12  boundary mask (bit k: a codeword boundary at bit offset k)
-//   bits 16..63  up to kMaxSymsPerWindow symbols, symbol j in bits 16+8j..23+8j
+// Window table: 2^kWinBits entries of 64 bits. For the codewords that lie
+// wholly inside a 12-bit window, read one after another from its first bit
+// (at most kMaxSymsPerWindow of them):
+//   bits  0..47  the symbols, symbol j in bits 8j..8j+7 (unused bytes zero)
+//   bits 48..59  end mask: bit 48+k-1 set when a codeword ends at offset k
+//   bits 60..63  total bits those codewords take (1..12)
+// Total 0 marks an escape window, whose first codeword is longer than 12
+// bits or unused: bits 0..15 then hold the index of its escape block, or
+// kUnusedBlock when the stored LUT has no codeword there.
 constexpr int kWinBits = 12;
 constexpr int kWinEntries = 1 << kWinBits;
 constexpr int kMaxSymsPerWindow = 6;
+constexpr uint32_t kUnusedBlock = 0xFFFFu;
+
+// Escape blocks: 16 entries of 16 bits (symbol | length << 8), indexed by
+// the 4 bits that follow the 12-bit window (codewords of 13..16 bits).
+constexpr int kEscBlockEntries = 16;
+// A byte alphabet has at most 256 codewords, hence at most 256 windows
+// whose first codeword is longer than 12 bits.
+constexpr int kMaxEscBlocks = 256;
 
 struct TableHeader {
     uint32_t magic;
@@ -25,16 +39,17 @@ struct TableHeader {
     uint32_t min_len;       // shortest code length (>= 1)
     uint32_t sym0;          // sym_lut[0]: what an all-zero window decodes to
     uint32_t len0;          // len_lut[0]
-    uint32_t glut_entries;  // 2^max_bits
+    uint32_t n_esc_blocks;  // escape blocks that follow the window table
     uint32_t reserved[9];
 };
 static_assert(sizeof(TableHeader) == 64, "header is 64 bytes");
 
 constexpr size_t kWinOffset = 64;
-constexpr size_t kGlutOffset = kWinOffset + sizeof(uint64_t) * kWinEntries;
+constexpr size_t kEscOffset = kWinOffset + sizeof(uint64_t) * kWinEntries;
 
-inline size_t table_nbytes(int max_bits) {
-    return kGlutOffset + sizeof(uint16_t) * (size_t(1) << max_bits);
+// Fixed blob size: room for the largest possible escape-block count.
+inline size_t table_nbytes() {
+    return kEscOffset + sizeof(uint16_t) * kEscBlockEntries * kMaxEscBlocks;
 }
 
 int fail(int code, const std::string& msg);

@@ -74,6 +74,27 @@ def _traffic(config_key: str):
     return rec.get("hbm_bytes_per_launch")
 
 
+def _copy_calibration(mib: int, steps: int, warmup: int) -> int:
+    """Copy mib MiB device-to-device `steps` times: each launch reads and
+    writes exactly mib MiB, which calibrates FETCH_SIZE / WRITE_SIZE."""
+    dev = torch.device("cuda", 0)
+    n = mib << 20
+    src = torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize(dev)
+    dt = (time.perf_counter() - t0) / steps
+    print(json.dumps({"copy_bytes_per_launch": n, "steps": steps,
+                      "us_per_copy": round(dt * 1e6, 2),
+                      "gbs_read_plus_write": round(2 * n / dt / 1e9, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -81,16 +102,22 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="instead of decoding, time a plain device copy of this many MiB "
+                         "(the reference kernel for scaling HBM byte counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU only: the decoder has no multi-GPU path in this "
-              "build (chunks shard by range with no exchange; see DESIGN.md). Run with "
-              "--gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU decode path "
+              "(chunks would shard by range with no exchange step). Run with --gpus 1.",
+              file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
+
+    if args.copy_mib:
+        return _copy_calibration(args.copy_mib, args.steps, args.warmup)
 
     from afterimage_amd import _native, workloads
     from afterimage_amd.runtime.device import DeviceTensor, _descriptor

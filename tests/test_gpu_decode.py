@@ -135,3 +135,38 @@ def test_repeat_runs_are_identical_across_streams():
     s.synchronize()
     for a in again:
         assert torch.equal(a, base)
+
+
+@pytest.mark.parametrize("chunk_size", [16, 512, 1024, 2048, 4096, 8192, 16384, 32768, 65536])
+def test_every_subgroup_width(chunk_size):
+    """Chunk sizes that select each threads-per-chunk width (16..1024)."""
+    w = (torch.randn(3 * chunk_size + 77, generator=torch.Generator().manual_seed(chunk_size))
+         * 0.02).to(torch.bfloat16)
+    bits = w.view(torch.int16).to(torch.int32) & 0xFFFF
+    _check((bits >> 7) & 0xFF, chunk_size=chunk_size)
+
+
+def test_round_with_more_symbols_than_the_staging_area():
+    """1-bit codes in 70000-symbol chunks: one round carries more symbols
+    than a sub-group can stage, so the decode runs in several windows."""
+    rng = np.random.default_rng(0)
+    data = rng.choice([5, 9], size=140013, p=[0.7, 0.3])
+    _check(torch.from_numpy(data), chunk_size=70000)
+
+
+def test_chunks_that_need_several_rounds():
+    """8-bit codes in 65536-symbol chunks: 512 Kbit per chunk, several rounds."""
+    rng = np.random.default_rng(1)
+    _check(torch.from_numpy(rng.integers(0, 256, size=65536 + 5000)), chunk_size=65536)
+    c = case("uniform256")
+    gpu = decode_gpu_v2(c["encoded"]).cpu().numpy()
+    assert np.array_equal(gpu, c["symbols"])
+
+
+def test_whole_chunk_decode_with_padding_across_rounds():
+    rng = np.random.default_rng(2)
+    data = rng.integers(0, 256, size=65536 + 5000)
+    enc = encode_chunked(torch.from_numpy(data), chunk_size=65536)
+    sub = _slice_encoded(enc, 0, enc.n_chunks)
+    gpu = decode_gpu_v2(sub).cpu().numpy()
+    assert np.array_equal(gpu, oracle.decode_chunks(sub))

@@ -41,7 +41,7 @@ def test_abi_version_and_error_channel():
     assert lib.aimg_table_nbytes(17, ctypes.byref(n)) == _native.AIMG_ERR_INVALID_ARGUMENT
     assert b"max_bits" in lib.aimg_last_error()
     assert lib.aimg_table_nbytes(16, ctypes.byref(n)) == _native.AIMG_OK
-    assert n.value == 64 + 8 * 4096 + 2 * 65536
+    assert n.value == 64 + 8 * 4096 + 2 * 16 * 256
 
 
 def test_decode_entry_points_validate_before_launching():
@@ -113,9 +113,21 @@ def test_window_expectation_agrees_with_oracle_reader():
         assert list(oracle.decode_chunks(one)[: len(want)]) == want
 
 
+def _first_codeword(lengths, bits16):
+    """(symbol, length) of the canonical codeword that the 16-bit string
+    bits16 starts with, or None."""
+    _, codes = canonical_codes(lengths)
+    for s, c in codes.items():
+        ln = lengths[s]
+        if ln <= 16 and bits16 >> (16 - ln) == c:
+            return s, ln
+    return None
+
+
 @pytest.mark.parametrize("name", ["bf16_outliers_64k", "dirichlet_6", "skewed_2sym",
-                                  "single_symbol", "fibonacci40_mb6"])
-def test_window_table_matches_oracle_reader(name):
+                                  "single_symbol", "fibonacci40_mb6", "uniform256",
+                                  "scales_3p0"])
+def test_window_table_matches_canonical_code(name):
     c = case(name)
     enc = c["encoded"]
     lengths = {s: int(ln) for s, ln in enumerate(c["lengths"]) if ln > 0}
@@ -124,25 +136,45 @@ def test_window_table_matches_oracle_reader(name):
     assert hdr[0] == 0x474D4941 and hdr[2] == enc.max_bits
     assert hdr[3] == min(lengths.values())
     assert hdr[4] == enc.sym_lut[0]
+    n_blocks = int(hdr[6])
     win = blob[64: 64 + 8 * 4096].view(np.uint64)
-    glut = blob[64 + 8 * 4096:].view(np.uint16)
-    assert np.array_equal(glut & 0xFF, enc.sym_lut & 0xFF)
-    assert np.array_equal(glut >> 8, enc.len_lut.astype(np.uint16))
+    esc = blob[64 + 8 * 4096:].view(np.uint16)
+    long_prefixes = {codes_prefix for codes_prefix in range(4096)
+                     if (fc := _first_codeword(lengths, codes_prefix << 4)) is not None
+                     and fc[1] > WIN_BITS}
+    assert n_blocks == len(long_prefixes)
     rng = np.random.default_rng(0)
-    for w in sorted(set(rng.integers(0, 4096, 400).tolist()) | {0, 4095}):
+    windows = set(rng.integers(0, 4096, 400).tolist()) | {0, 4095} | long_prefixes
+    for w in sorted(windows):
         want = _window_expectation(lengths, w)
         ent = int(win[w])
-        mask = ent & 0x1FFF
-        got_n = bin(mask).count("1") - 1
-        assert got_n == len(want), (w, want, hex(ent))
-        got = [(ent >> (16 + 8 * j)) & 0xFF for j in range(got_n)]
+        total = ent >> 60
+        ends = (ent >> 48) & 0xFFF
+        if not want:
+            # Escape window: its block gives the first codeword for every
+            # value of the next four bits.
+            assert total == 0 and ends == 0
+            blk = ent & 0xFFFF
+            if w not in long_prefixes:
+                assert blk == 0xFFFF
+                continue
+            assert blk < n_blocks
+            for e4 in range(16):
+                got = int(esc[blk * 16 + e4])
+                fc = _first_codeword(lengths, (w << 4) | e4)
+                if fc is None:
+                    assert got >> 8 == 0
+                else:
+                    assert (got & 0xFF, got >> 8) == fc
+            continue
+        got = [(ent >> (8 * j)) & 0xFF for j in range(len(want))]
         assert got == want
-        # Boundaries sit at the running code lengths.
-        bounds, pos = [0], 0
+        assert (ent & 0xFFFFFFFFFFFF) >> (8 * len(want)) == 0
+        pos, mask = 0, 0
         for s in want:
             pos += lengths[s]
-            bounds.append(pos)
-        assert mask == sum(1 << b for b in bounds)
+            mask |= 1 << (pos - 1)
+        assert ends == mask and total == pos
 
 
 @pytest.mark.parametrize("name", case_names())
