@@ -1,12 +1,13 @@
 // gfx950 kernels of libafterimage_decode: chunked canonical-Huffman exponent
 // decode fused with the BF16 recombine.
 //
-// Work layout. A workgroup has 1024 threads (16 waves) and one is resident
-// per CU; the grid is persistent and walks "items". An item is a batch of
-// chunks of one tensor: the workgroup splits into 1024/TPC sub-groups of TPC
-// threads (TPC = 16..1024, chosen per tensor from its chunk size so that a
-// chunk's symbols fill the sub-group's 64-bytes-per-thread staging area), and
-// each sub-group decodes one chunk.
+// Work layout. A workgroup has 512 threads (8 waves) and uses under 80 KB
+// of LDS, so two are resident per CU and one's memory phases overlap the
+// other's decoding. The grid is persistent and walks "items". An item is a
+// batch of chunks of one tensor: the workgroup splits into 512/TPC sub-groups
+// of TPC threads (TPC = 16..512, chosen per tensor from its chunk size so that
+// a chunk's symbols fill the sub-group's 64-bytes-per-thread staging area),
+// and each sub-group decodes one chunk.
 //
 // A sub-group walks its chunk's bitstream in rounds (one round for chunks of
 // up to TPC*224 bits). A round gives each thread one segment of S bits and
@@ -23,18 +24,19 @@
 //      never depends on resynchronisation happening;
 //   3. a workgroup prefix sum of the counts places each segment's symbols;
 //   4. each thread re-parses its segment and writes the exponents to the LDS
-//      staging area, one unaligned 8-byte store per table lookup. A store may
-//      run up to 7 bytes past the thread's symbols into the next threads'
-//      first 8 bytes; after a barrier every thread rewrites its own first 8
-//      bytes exactly;
+//      staging area: exact byte stores until it reaches a 4-byte boundary,
+//      then one aligned 8-byte store per table lookup, which may run up to 7
+//      bytes past the thread's symbols into the next threads' first 8 bytes;
+//      after a barrier every thread rewrites its own first 8 bytes exactly;
 //   5. the staged exponents are combined with the sign/mantissa bytes and
 //      written with 16-byte stores (8 bf16 or 16 uint8 per store).
 // If a round has more symbols than the staging area holds, steps 4-5 repeat
 // over windows of whole segments.
 //
-// Codewords are read through a 12-bit window table of up to 6 codewords per
-// lookup (LDS); codewords of 13..16 bits go through 16-entry escape blocks
-// (LDS for the first 64 blocks, global memory beyond).
+// Codewords are read through a 12-bit window table of up to 4 codewords per
+// lookup (LDS; the counting pass reads only its 2-byte length part);
+// codewords of 13..16 bits go through 16-entry escape blocks (LDS for the
+// first 64 blocks, global memory beyond).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -47,7 +49,11 @@
 namespace aimg {
 namespace {
 
-constexpr int kThreads = 1024;
+constexpr int kThreads = 512;
+constexpr int kBlocksPerCu = 2;
+// Waves each SIMD must hold for kBlocksPerCu resident workgroups (4 SIMDs
+// per CU); bounds the registers a thread may use.
+constexpr int kWavesPerSimd = kBlocksPerCu * (kThreads / 64) / 4;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMinTpc = 16;
 constexpr int kMaxGroups = kThreads / kMinTpc;
@@ -59,9 +65,11 @@ constexpr uint32_t kStageSlack = 32;  // per sub-group: carried lead (< 16) + st
 constexpr uint32_t kTileSlackWords = 4;
 constexpr uint32_t kTileWords = kThreads * kMaxSegBits / 32 + kTileSlackWords * kMaxGroups;
 constexpr uint32_t kStageBytes = kThreads * kStagePerThread + kStageSlack * kMaxGroups;
+static_assert(kStageBytes % (16 * kMaxGroups) == 0, "stage regions stay 16-byte aligned");
+static_assert(kTileWords % kMaxGroups == 0, "tile regions split evenly");
 constexpr int kLdsEscBlocks = 64;
-constexpr uint32_t kTotalShift = 60;
-constexpr uint64_t kSymMask = 0xFFFFFFFFFFFFull;
+constexpr uint32_t kTileBatch = 8;   // stream words a thread fetches per batch
+constexpr uint32_t kStoreBatch = 4;  // output vector groups a thread handles per batch
 
 struct DevTensor {
     const uint8_t* packed;
@@ -85,30 +93,64 @@ struct LaunchArgs {
 };
 
 struct Tables {
-    const uint64_t* win;     // LDS window table
+    const uint32_t* syms;    // LDS window table: symbols / escape block
+    const uint16_t* meta;    // LDS window table: end mask | total << 12
     const uint16_t* esc;     // LDS escape blocks (first kLdsEscBlocks)
-    const uint16_t* gesc;    // all escape blocks, global memory
+    const __attribute__((address_space(1))) uint16_t* gesc;  // all escape blocks, global memory
     uint32_t sym0;
 };
 
-// 32 bits of the staged stream starting at bit q (MSB-first).
-__device__ __forceinline__ uint32_t peek32(const uint32_t* tile, uint32_t q) {
-    const uint32_t k = q >> 5;
-    const uint64_t v = (static_cast<uint64_t>(tile[k]) << 32) | tile[k + 1];
-    return static_cast<uint32_t>((v << (q & 31)) >> 32);
+// Bit reader over the staged stream. `pair` holds the two stream words that
+// start at bit `base` (a multiple of 32, base <= p <= base + 47); a step
+// reads at most 16 bits, all inside the pair. While a step's table lookup is
+// in flight, the reader already fetches the pair starting at the word that
+// contains p, which holds the next step's bits, so each step waits for one
+// LDS round trip.
+struct Reader {
+    const uint32_t* tile;
+    uint32_t p;
+    uint32_t base;
+    uint64_t pair;
+};
+
+__device__ __forceinline__ uint64_t load_pair(const uint32_t* tile, uint32_t k) {
+    return (static_cast<uint64_t>(tile[k]) << 32) | tile[k + 1];
+}
+
+__device__ __forceinline__ Reader reader_at(const uint32_t* tile, uint32_t p) {
+    return {tile, p, p & ~31u, load_pair(tile, p >> 5)};
+}
+
+// The 32 bits at the reader's position (bits past the pair read as zero;
+// only the first 16 are used).
+__device__ __forceinline__ uint32_t reader_bits(const Reader& rd) {
+    return static_cast<uint32_t>((rd.pair << (rd.p - rd.base)) >> 32);
+}
+
+// Move the reader forward by n bits (n <= 16), using the pair prefetched at
+// the old position.
+__device__ __forceinline__ void reader_skip(Reader& rd, uint64_t next_pair, uint32_t n) {
+    rd.base = rd.p & ~31u;
+    rd.pair = next_pair;
+    rd.p += n;
 }
 
 // (symbol, length) of an escape window's first codeword; w holds the window
 // in bits 31..20 and the next four bits in 19..16.
-__device__ __forceinline__ uint32_t escape(const Tables& tb, uint64_t ent, uint32_t w,
+__device__ __forceinline__ uint32_t escape(const Tables& tb, uint32_t ent, uint32_t w,
                                            uint32_t* len) {
-    const uint32_t blk = static_cast<uint32_t>(ent) & 0xFFFFu;
+    const uint32_t blk = ent & 0xFFFFu;
     if (blk == kUnusedBlock) {
         *len = 1;
         return tb.sym0;
     }
     const uint32_t at = blk * kEscBlockEntries + ((w >> 16) & 15u);
-    const uint32_t v = blk < static_cast<uint32_t>(kLdsEscBlocks) ? tb.esc[at] : tb.gesc[at];
+    uint32_t v;
+    if (blk < static_cast<uint32_t>(kLdsEscBlocks)) {
+        v = tb.esc[at];
+    } else {
+        v = tb.gesc[at];
+    }
     const uint32_t l = v >> 8;
     *len = l ? l : 1u;
     return v & 0xFFu;
@@ -124,66 +166,97 @@ struct Adv {
 __device__ __forceinline__ Adv advance(const uint32_t* tile, const Tables& tb, uint32_t p,
                                        uint32_t x) {
     uint32_t n = 0;
+    Reader rd = reader_at(tile, p);
     // Whole windows while no codeword of the window can reach x.
-    while (p + kWinBits <= x) {
-        const uint32_t w = peek32(tile, p);
-        const uint64_t ent = tb.win[w >> (32 - kWinBits)];
-        const uint32_t hi = static_cast<uint32_t>(ent >> 32);
-        const uint32_t total = hi >> (kTotalShift - 32);
+    while (rd.p + kWinBits <= x) {
+        const uint32_t w = reader_bits(rd);
+        const uint32_t idx = w >> (32 - kWinBits);
+        const uint32_t meta = tb.meta[idx];
+        const uint64_t next = load_pair(tile, rd.p >> 5);
+        const uint32_t total = meta >> 12;
         if (total == 0) {
             uint32_t l;
-            escape(tb, ent, w, &l);
-            p += l;
+            escape(tb, tb.syms[idx], w, &l);
+            reader_skip(rd, next, l);
             n += 1;
             continue;
         }
-        n += __popc(hi & 0x0FFF0000u);
-        p += total;
+        n += __popc(meta & 0xFFFu);
+        reader_skip(rd, next, total);
     }
-    while (p < x) {
-        const uint32_t w = peek32(tile, p);
-        const uint64_t ent = tb.win[w >> (32 - kWinBits)];
-        const uint32_t hi = static_cast<uint32_t>(ent >> 32);
-        const uint32_t total = hi >> (kTotalShift - 32);
+    while (rd.p < x) {
+        const uint32_t w = reader_bits(rd);
+        const uint32_t idx = w >> (32 - kWinBits);
+        const uint32_t meta = tb.meta[idx];
+        const uint64_t next = load_pair(tile, rd.p >> 5);
+        const uint32_t total = meta >> 12;
         if (total == 0) {
             uint32_t l;
-            escape(tb, ent, w, &l);
-            p += l;
+            escape(tb, tb.syms[idx], w, &l);
+            reader_skip(rd, next, l);
             n += 1;
             continue;
         }
-        const uint32_t ends = (hi >> 16) & 0xFFFu;  // bit k-1: a codeword ends at offset k
-        const uint32_t rel = x - p;                 // 1..11
+        const uint32_t ends = meta & 0xFFFu;  // bit k-1: a codeword ends at offset k
+        const uint32_t rel = x - rd.p;        // 1..11
         const uint32_t upto = total < rel ? total : rel;
         // Codewords starting before rel: the one at offset 0 plus every end
         // boundary at offset 1..upto-1.
         n += 1 + __popc(ends & ((1u << (upto - 1)) - 1u));
-        p += total < rel ? total : rel - 1 + __ffs(ends >> (rel - 1));
+        reader_skip(rd, next, total < rel ? total : rel - 1 + __ffs(ends >> (rel - 1)));
     }
-    return {p, n};
+    return {rd.p, n};
 }
 
-// Re-parse from true boundary p and write `count` symbols to stage[q...],
-// one unaligned 8-byte store per lookup (stores may run 7 bytes past).
+// One table lookup at the reader: up to 4 symbols (one byte each, zero
+// above the n-th) and the bits they take; advances the reader.
+__device__ __forceinline__ uint32_t next_symbols(Reader& rd, const uint32_t* tile,
+                                                 const Tables& tb, uint32_t* n) {
+    const uint32_t w = reader_bits(rd);
+    const uint32_t idx = w >> (32 - kWinBits);
+    const uint32_t meta = tb.meta[idx];
+    uint32_t syms = tb.syms[idx];
+    const uint64_t next = load_pair(tile, rd.p >> 5);
+    uint32_t adv = meta >> 12;
+    *n = __popc(meta & 0xFFFu);
+    if (adv == 0) {
+        syms = escape(tb, syms, w, &adv);
+        *n = 1;
+    }
+    reader_skip(rd, next, adv);
+    return syms;
+}
+
+// Re-parse from true boundary p and write `count` symbols to stage[q...]
+// (stage is 4-byte aligned). Until q reaches a 4-byte boundary the bytes are
+// stored exactly, so the previous thread's bytes in that word are left
+// alone; after that each lookup is one aligned 8-byte store of the current
+// word (`cur` holds this thread's bytes of it) and the next one. Stores may
+// run up to 7 bytes past the last symbol.
 __device__ __forceinline__ void emit_run(const uint32_t* tile, const Tables& tb, uint32_t p,
                                          uint8_t* stage, uint32_t q, uint32_t count) {
     const uint32_t q_end = q + count;
+    Reader rd = reader_at(tile, p);
+    uint32_t cur = 0;
+    bool exact = (q & 3u) != 0;
     while (q < q_end) {
-        const uint32_t w = peek32(tile, p);
-        const uint64_t ent = tb.win[w >> (32 - kWinBits)];
-        const uint32_t hi = static_cast<uint32_t>(ent >> 32);
-        const uint32_t total = hi >> (kTotalShift - 32);
-        uint64_t syms = ent;
-        uint32_t n = __popc(hi & 0x0FFF0000u);
-        if (total == 0) {
-            uint32_t l;
-            syms = escape(tb, ent, w, &l);
-            n = 1;
-            p += l;
+        uint32_t n;
+        const uint32_t syms = next_symbols(rd, tile, tb, &n);
+        const uint32_t r = q & 3u;
+        const uint64_t sh = static_cast<uint64_t>(syms) << (8 * r);
+        const uint32_t lo = cur | static_cast<uint32_t>(sh);
+        const uint32_t hi = static_cast<uint32_t>(sh >> 32);
+        uint32_t* word = reinterpret_cast<uint32_t*>(stage + (q & ~3u));
+        if (exact) {
+            for (uint32_t j = r; j < 4; ++j)
+                if (j < r + n) stage[(q & ~3u) + j] = static_cast<uint8_t>(lo >> (8 * j));
+            word[1] = hi;
+            exact = r + n < 4;
         } else {
-            p += total;
+            word[0] = lo;
+            word[1] = hi;
         }
-        __builtin_memcpy(stage + q, &syms, 8);
+        cur = r + n >= 4 ? hi : lo;
         q += n;
     }
 }
@@ -193,21 +266,12 @@ __device__ __forceinline__ void write_head(const uint32_t* tile, const Tables& t
                                            uint8_t* stage, uint32_t q, uint32_t count) {
     const uint32_t h = count < 8 ? count : 8;
     uint64_t acc = 0;
+    Reader rd = reader_at(tile, p);
     for (uint32_t k = 0; k < h;) {
-        const uint32_t w = peek32(tile, p);
-        const uint64_t ent = tb.win[w >> (32 - kWinBits)];
-        const uint32_t hi = static_cast<uint32_t>(ent >> 32);
-        const uint32_t total = hi >> (kTotalShift - 32);
-        if (total == 0) {
-            uint32_t l;
-            acc |= static_cast<uint64_t>(escape(tb, ent, w, &l)) << (8 * k);
-            k += 1;
-            p += l;
-        } else {
-            acc |= (ent & kSymMask) << (8 * k);
-            k += __popc(hi & 0x0FFF0000u);
-            p += total;
-        }
+        uint32_t n;
+        const uint32_t syms = next_symbols(rd, tile, tb, &n);
+        acc |= static_cast<uint64_t>(syms) << (8 * k);
+        k += n;
     }
     if (h == 8) {
         __builtin_memcpy(stage + q, &acc, 8);
@@ -216,16 +280,31 @@ __device__ __forceinline__ void write_head(const uint32_t* tile, const Tables& t
     }
 }
 
-// 4 stream bytes starting at byte b of a chunk of nb bytes, as a big-endian
-// word; bytes at or past nb read as zero and are never fetched.
-__device__ __forceinline__ uint32_t load_be_word(const uint8_t* cbytes, int64_t nb, int64_t b) {
-    if (b >= nb) return 0u;
-    const uintptr_t addr = reinterpret_cast<uintptr_t>(cbytes + b);
-    const uintptr_t al = addr & ~static_cast<uintptr_t>(3);
-    const uint32_t sh = static_cast<uint32_t>(addr & 3) * 8u;
-    uint32_t v = *reinterpret_cast<const uint32_t*>(al) >> sh;
-    if (sh != 0u && b + (4 - sh / 8) < nb) v |= *reinterpret_cast<const uint32_t*>(al + 4) << (32u - sh);
+// Byte offset to load stream word b from: b itself when the 4 bytes lie in
+// the `room` readable bytes at the chunk start (room >= 4), else the last
+// readable word, so no byte outside the buffer is touched; the word is then
+// shifted into place by stream_word.
+__device__ __forceinline__ int64_t word_at(int64_t room, int64_t b) {
+    return b + 4 <= room ? b : room - 4;
+}
+
+__device__ __forceinline__ uint32_t load_u32(const uint8_t* p) {
+    uint32_t v;
+    __builtin_memcpy(&v, p, 4);  // unaligned 4-byte load
+    return v;
+}
+
+// The same from single bytes, for a buffer of fewer than 4 bytes.
+__device__ __forceinline__ uint32_t load_bytes(const uint8_t* cbytes, int64_t nb, int64_t b) {
+    uint32_t v = 0;
+    for (int64_t k = 0; k < 4 && b + k < nb; ++k) v |= static_cast<uint32_t>(cbytes[b + k]) << (8 * k);
+    return v;
+}
+
+// Big-endian stream word with the bytes at or past the chunk end zeroed.
+__device__ __forceinline__ uint32_t be_word(uint32_t v, int64_t nb, int64_t b) {
     const int64_t left = nb - b;
+    if (left <= 0) return 0u;
     if (left < 4) v &= (1u << (8 * left)) - 1u;
     return __builtin_bswap32(v);
 }
@@ -287,9 +366,47 @@ __device__ __forceinline__ void store_group(const DevTensor& T, const uint8_t* s
     }
 }
 
+// Vector groups [0, nfull) of a staged window to output elements a0...;
+// thread i of a sub-group of tpc takes groups i, i+tpc, ... and requests
+// the sign/mantissa bytes of a whole batch before combining any.
 template <bool kBf16, int kGroup>
-__global__ __launch_bounds__(kThreads) void decode_kernel(const LaunchArgs args) {
-    __shared__ uint64_t s_win[kWinEntries];
+__device__ __forceinline__ void store_window(const DevTensor& T, const uint8_t* stage, int64_t a0,
+                                             uint32_t nfull, uint32_t i, uint32_t tpc) {
+    if (kGroup == 1 || !kBf16) {
+        for (uint32_t v = i; v < nfull; v += tpc)
+            store_group<kBf16, kGroup>(T, stage + v * kGroup, a0 + static_cast<int64_t>(v) * kGroup);
+        return;
+    }
+    for (uint32_t v0 = 0; v0 < nfull; v0 += kStoreBatch * tpc) {
+        // Unconditional loads (indices clamped into the window) so a batch
+        // is issued back to back.
+        uint2 smv[kStoreBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kStoreBatch; ++k) {
+            const uint32_t v = v0 + k * tpc + i;
+            const uint32_t vc = v < nfull ? v : nfull - 1;
+            smv[k] = *reinterpret_cast<const uint2*>(T.sm + a0 + static_cast<int64_t>(vc) * kGroup);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kStoreBatch; ++k) {
+            const uint32_t v = v0 + k * tpc + i;
+            if (v >= nfull) continue;
+            const uint2 ev = *reinterpret_cast<const uint2*>(stage + v * kGroup);
+            uint4 o4;
+            o4.x = bf16_pair(__builtin_amdgcn_perm(ev.x, smv[k].x, 0x05010400u));
+            o4.y = bf16_pair(__builtin_amdgcn_perm(ev.x, smv[k].x, 0x07030602u));
+            o4.z = bf16_pair(__builtin_amdgcn_perm(ev.y, smv[k].y, 0x05010400u));
+            o4.w = bf16_pair(__builtin_amdgcn_perm(ev.y, smv[k].y, 0x07030602u));
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.out) + a0 +
+                                      static_cast<int64_t>(v) * kGroup) = o4;
+        }
+    }
+}
+
+template <bool kBf16, int kGroup>
+__global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const LaunchArgs args) {
+    __shared__ uint32_t s_wsyms[kWinEntries];
+    __shared__ uint16_t s_wmeta[kWinEntries];
     __shared__ uint16_t s_esc[kLdsEscBlocks * kEscBlockEntries];
     __shared__ uint32_t s_tile[kTileWords];
     __shared__ __attribute__((aligned(16))) uint8_t s_stage[kStageBytes];
@@ -302,7 +419,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const LaunchArgs args)
     const uint32_t tid = threadIdx.x;
     const uint8_t* loaded = nullptr;
     Tables tb;
-    tb.win = s_win;
+    tb.syms = s_wsyms;
+    tb.meta = s_wmeta;
     tb.esc = s_esc;
 
     for (int64_t item = blockIdx.x; item < args.total_items; item += gridDim.x) {
@@ -320,9 +438,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const LaunchArgs args)
         __syncthreads();  // the previous item is done with LDS
         if (T.table != loaded) {
             loaded = T.table;
-            const uint4* src = reinterpret_cast<const uint4*>(T.table + kWinOffset);
-            uint4* dst = reinterpret_cast<uint4*>(s_win);
-            for (uint32_t j = tid; j < kWinEntries / 2; j += kThreads) dst[j] = src[j];
+            const uint4* src = reinterpret_cast<const uint4*>(T.table + kSymsOffset);
+            uint4* dst = reinterpret_cast<uint4*>(s_wsyms);
+            for (uint32_t j = tid; j < kWinEntries / 4; j += kThreads) dst[j] = src[j];
+            const uint4* msrc = reinterpret_cast<const uint4*>(T.table + kMetaOffset);
+            uint4* mdst = reinterpret_cast<uint4*>(s_wmeta);
+            for (uint32_t j = tid; j < kWinEntries / 8; j += kThreads) mdst[j] = msrc[j];
             const TableHeader* hdr = reinterpret_cast<const TableHeader*>(T.table);
             const uint32_t n_esc = hdr->n_esc_blocks < static_cast<uint32_t>(kLdsEscBlocks)
                                        ? hdr->n_esc_blocks : kLdsEscBlocks;
@@ -331,7 +452,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const LaunchArgs args)
         }
         const TableHeader* hdr = reinterpret_cast<const TableHeader*>(T.table);
         tb.sym0 = hdr->sym0;
-        tb.gesc = reinterpret_cast<const uint16_t*>(T.table + kEscOffset);
+        tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(T.table + kEscOffset);
 
         int64_t off = 0, nb = 0, lim = 0;
         const int64_t chunk_base = c * T.chunk_size;
@@ -344,6 +465,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const LaunchArgs args)
             lim = lim < 0 ? 0 : (lim > T.chunk_size ? T.chunk_size : lim);
         }
         const uint8_t* cbytes = T.packed + off;
+        const int64_t room = T.packed_nbytes - off;
         const int64_t chunk_bits = nb * 8;
         const int64_t per_round_max = static_cast<int64_t>(tpc) * kMaxSegBits;
         const int64_t nr = (chunk_bits + per_round_max - 1) / per_round_max;
@@ -354,8 +476,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const LaunchArgs args)
             S = S < kMinSegBits ? kMinSegBits : S;
         }
         const uint32_t round_bits = tpc * S;
-        uint32_t* tile = s_tile + g * (tpc * kMaxSegBits / 32 + kTileSlackWords);
-        const uint32_t region = tpc * kStagePerThread + kStageSlack;
+        uint32_t* tile = s_tile + g * (kTileWords >> (__ffs(n_groups) - 1));
+        const uint32_t region = kStageBytes >> (__ffs(n_groups) - 1);
         uint8_t* stage = s_stage + g * region;
 
         if (i == 0) s_gval[g] = static_cast<uint32_t>(nr);
@@ -376,8 +498,35 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const LaunchArgs args)
                 RB = left < round_bits ? static_cast<uint32_t>(left) : round_bits;
             }
             const uint32_t nw = g_active ? (RB + 31) / 32 + 3 : 0;
-            for (uint32_t j = i; j < nw; j += tpc)
-                tile[j] = load_be_word(cbytes, nb, R0 / 8 + 4 * static_cast<int64_t>(j));
+            // All of this thread's words are requested before any is used;
+            // loads past the chunk read a clamped in-buffer word and are zeroed.
+            for (uint32_t j0 = 0; j0 < nw; j0 += kTileBatch * tpc) {
+                uint32_t raw[kTileBatch];
+                if (room >= 4) {
+#pragma unroll
+                    for (uint32_t k = 0; k < kTileBatch; ++k) {
+                        const int64_t b = R0 / 8 + 4 * static_cast<int64_t>(j0 + k * tpc + i);
+                        const int64_t bb = b < nb ? b : 0;
+                        raw[k] = load_u32(cbytes + word_at(room, bb));
+                    }
+#pragma unroll
+                    for (uint32_t k = 0; k < kTileBatch; ++k) {
+                        const int64_t b = R0 / 8 + 4 * static_cast<int64_t>(j0 + k * tpc + i);
+                        const int64_t bb = b < nb ? b : 0;
+                        raw[k] >>= 8 * static_cast<uint32_t>(bb - word_at(room, bb));
+                    }
+                } else {
+#pragma unroll
+                    for (uint32_t k = 0; k < kTileBatch; ++k)
+                        raw[k] = load_bytes(cbytes, nb,
+                                            R0 / 8 + 4 * static_cast<int64_t>(j0 + k * tpc + i));
+                }
+#pragma unroll
+                for (uint32_t k = 0; k < kTileBatch; ++k) {
+                    const uint32_t j = j0 + k * tpc + i;
+                    if (j < nw) tile[j] = be_word(raw[k], nb, R0 / 8 + 4 * static_cast<int64_t>(j));
+                }
+            }
             __syncthreads();
 
             const uint32_t seg_lo = i * S;
@@ -416,8 +565,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const LaunchArgs args)
             const uint32_t e_last = s_e[g * tpc + n_active - 1];
             const uint32_t o = excl - s_gpre[g];
             const uint32_t gtot = s_gpre[g + 1] - s_gpre[g];
-            const int64_t room = lim - ob;
-            const uint32_t want = g_active ? (gtot < room ? gtot : static_cast<uint32_t>(room)) : 0u;
+            const int64_t still = lim - ob;
+            const uint32_t want = g_active ? (gtot < still ? gtot : static_cast<uint32_t>(still)) : 0u;
             const uint32_t run = (active && o < want) ? (cnt < want - o ? cnt : want - o) : 0u;
             bool done = run == 0;
             uint32_t base = 0;  // sub-group symbol index at the start of this window
@@ -435,9 +584,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const LaunchArgs args)
                 const uint32_t avail = lead + (wend - base);
                 const uint32_t nfull = avail / kGroup;
                 const int64_t a0 = chunk_base + ob - lead;
-                for (uint32_t v = i; v < nfull; v += tpc)
-                    store_group<kBf16, kGroup>(T, stage + v * kGroup,
-                                               a0 + static_cast<int64_t>(v) * kGroup);
+                store_window<kBf16, kGroup>(T, stage, a0, nfull, i, tpc);
                 ob += wend - base;
                 base = wend;
                 done = done || go;
@@ -540,7 +687,8 @@ int launch(const aimg_tensor* ts, int n, void* stream) {
     args.n_tensors = m;
     args.total_items = items;
     if (items == 0) return AIMG_OK;
-    const int64_t grid = items < cu_count() ? items : cu_count();
+    const int64_t slots = static_cast<int64_t>(cu_count()) * kBlocksPerCu;
+    const int64_t grid = items < slots ? items : slots;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 gdim(static_cast<uint32_t>(grid)), bdim(kThreads);
     if (vec) {

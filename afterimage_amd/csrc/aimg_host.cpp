@@ -96,7 +96,8 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
 
     auto* blob = static_cast<uint8_t*>(out);
     std::memset(blob, 0, need);
-    auto* wt = reinterpret_cast<uint64_t*>(blob + aimg::kWinOffset);
+    auto* wsyms = reinterpret_cast<uint32_t*>(blob + aimg::kSymsOffset);
+    auto* wmeta = reinterpret_cast<uint16_t*>(blob + aimg::kMetaOffset);
     auto* esc = reinterpret_cast<uint16_t*>(blob + aimg::kEscOffset);
     // (symbol, length) of the codeword starting at the first bit of `bits`
     // (MSB-first, zeros past the window).
@@ -109,18 +110,19 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
     for (uint32_t w = 0; w < static_cast<uint32_t>(aimg::kWinEntries); ++w) {
         const uint32_t bits = w << (32 - aimg::kWinBits);
         uint32_t pos = 0, mask = 0, k = 0;
-        uint64_t syms = 0;
+        uint32_t syms = 0;
         while (k < static_cast<uint32_t>(aimg::kMaxSymsPerWindow)) {
             uint32_t s, l;
             lut_at(bits << pos, &s, &l);
             if (l == 0 || pos + l > static_cast<uint32_t>(aimg::kWinBits)) break;
-            syms |= static_cast<uint64_t>(s) << (8 * k);
+            syms |= s << (8 * k);
             ++k;
             pos += l;
             mask |= 1u << (pos - 1);
         }
         if (k > 0) {
-            wt[w] = syms | (static_cast<uint64_t>(mask) << 48) | (static_cast<uint64_t>(pos) << 60);
+            wsyms[w] = syms;
+            wmeta[w] = static_cast<uint16_t>(mask | (pos << 12));
             continue;
         }
         // Escape window: one entry per value of the next four bits.
@@ -132,15 +134,16 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
             block[e4] = static_cast<uint16_t>(s | (l << 8));
             any = any || l != 0;
         }
+        wmeta[w] = 0;
         if (!any) {
-            wt[w] = aimg::kUnusedBlock;
+            wsyms[w] = aimg::kUnusedBlock;
             continue;
         }
         if (n_blocks >= static_cast<uint32_t>(aimg::kMaxEscBlocks))
             return fail(AIMG_ERR_BAD_TABLE, "more than 256 windows start with a codeword "
                                             "longer than 12 bits");
         std::memcpy(esc + n_blocks * aimg::kEscBlockEntries, block, sizeof(block));
-        wt[w] = n_blocks++;
+        wsyms[w] = n_blocks++;
     }
 
     aimg::TableHeader hdr{};

@@ -8,21 +8,21 @@
 
 namespace aimg {
 
-constexpr int kAbiVersion = 2;
+constexpr int kAbiVersion = 3;
 constexpr uint32_t kTableMagic = 0x474D4941u;  // "AIMG"
 
-// Window table: 2^kWinBits entries of 64 bits. For the codewords that lie
-// wholly inside a 12-bit window, read one after another from its first bit
-// (at most kMaxSymsPerWindow of them):
-//   bits  0..47  the symbols, symbol j in bits 8j..8j+7 (unused bytes zero)
-//   bits 48..59  end mask: bit 48+k-1 set when a codeword ends at offset k
-//   bits 60..63  total bits those codewords take (1..12)
+// Window table: for each 12-bit window, the codewords that lie wholly inside
+// it when read one after another from its first bit (at most
+// kMaxSymsPerWindow), in two arrays:
+//   syms (uint32): the symbols, symbol j in bits 8j..8j+7 (unused bytes zero)
+//   meta (uint16): bits 0..11 end mask (bit k-1 set when a codeword ends at
+//                  offset k), bits 12..15 total bits those codewords take
 // Total 0 marks an escape window, whose first codeword is longer than 12
-// bits or unused: bits 0..15 then hold the index of its escape block, or
-// kUnusedBlock when the stored LUT has no codeword there.
+// bits or unused; its syms entry then holds the index of its escape block,
+// or kUnusedBlock when the stored LUT has no codeword there.
 constexpr int kWinBits = 12;
 constexpr int kWinEntries = 1 << kWinBits;
-constexpr int kMaxSymsPerWindow = 6;
+constexpr int kMaxSymsPerWindow = 4;
 constexpr uint32_t kUnusedBlock = 0xFFFFu;
 
 // Escape blocks: 16 entries of 16 bits (symbol | length << 8), indexed by
@@ -44,8 +44,9 @@ struct TableHeader {
 };
 static_assert(sizeof(TableHeader) == 64, "header is 64 bytes");
 
-constexpr size_t kWinOffset = 64;
-constexpr size_t kEscOffset = kWinOffset + sizeof(uint64_t) * kWinEntries;
+constexpr size_t kSymsOffset = 64;
+constexpr size_t kMetaOffset = kSymsOffset + sizeof(uint32_t) * kWinEntries;
+constexpr size_t kEscOffset = kMetaOffset + sizeof(uint16_t) * kWinEntries;
 
 // Fixed blob size: room for the largest possible escape-block count.
 inline size_t table_nbytes() {

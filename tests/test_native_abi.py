@@ -41,7 +41,7 @@ def test_abi_version_and_error_channel():
     assert lib.aimg_table_nbytes(17, ctypes.byref(n)) == _native.AIMG_ERR_INVALID_ARGUMENT
     assert b"max_bits" in lib.aimg_last_error()
     assert lib.aimg_table_nbytes(16, ctypes.byref(n)) == _native.AIMG_OK
-    assert n.value == 64 + 8 * 4096 + 2 * 16 * 256
+    assert n.value == 64 + 4 * 4096 + 2 * 4096 + 2 * 16 * 256
 
 
 def test_decode_entry_points_validate_before_launching():
@@ -78,14 +78,14 @@ def test_table_builder_rejects_non_prefix_lut():
         build_table_blob(sym, ln, 2)
 
 
-def _window_expectation(lengths, w):
+def _window_expectation(lengths, w, max_syms=4):
     """Codewords read one after another from the 12-bit window w, found by
     matching each canonical code against the window's bits; kept while they
-    lie wholly inside the window (at most 6)."""
+    lie wholly inside the window (at most max_syms)."""
     _, codes = canonical_codes(lengths)
     bits = format(w, "012b")
     out, pos = [], 0
-    while len(out) < 6:
+    while len(out) < max_syms:
         hit = [s for s, c in codes.items()
                if pos + lengths[s] <= WIN_BITS
                and bits[pos: pos + lengths[s]] == format(c, "0%db" % lengths[s])]
@@ -104,7 +104,7 @@ def test_window_expectation_agrees_with_oracle_reader():
     enc = c["encoded"]
     lengths = {s: int(ln) for s, ln in enumerate(c["lengths"]) if ln > 0}
     for w in range(0, 4096, 37):
-        want = _window_expectation(lengths, w)
+        want = _window_expectation(lengths, w, max_syms=6)
         body = np.array([(w >> 4) & 0xFF, (w & 0xF) << 4], np.uint8)
         one = ChunkedEncoded(packed=body, chunk_offsets=np.array([0], np.int32),
                              chunk_nbytes=np.array([2], np.int32), sym_lut=enc.sym_lut,
@@ -137,8 +137,9 @@ def test_window_table_matches_canonical_code(name):
     assert hdr[3] == min(lengths.values())
     assert hdr[4] == enc.sym_lut[0]
     n_blocks = int(hdr[6])
-    win = blob[64: 64 + 8 * 4096].view(np.uint64)
-    esc = blob[64 + 8 * 4096:].view(np.uint16)
+    wsyms = blob[64: 64 + 4 * 4096].view(np.uint32)
+    wmeta = blob[64 + 4 * 4096: 64 + 6 * 4096].view(np.uint16)
+    esc = blob[64 + 6 * 4096:].view(np.uint16)
     long_prefixes = {codes_prefix for codes_prefix in range(4096)
                      if (fc := _first_codeword(lengths, codes_prefix << 4)) is not None
                      and fc[1] > WIN_BITS}
@@ -147,9 +148,9 @@ def test_window_table_matches_canonical_code(name):
     windows = set(rng.integers(0, 4096, 400).tolist()) | {0, 4095} | long_prefixes
     for w in sorted(windows):
         want = _window_expectation(lengths, w)
-        ent = int(win[w])
-        total = ent >> 60
-        ends = (ent >> 48) & 0xFFF
+        ent = int(wsyms[w])
+        total = int(wmeta[w]) >> 12
+        ends = int(wmeta[w]) & 0xFFF
         if not want:
             # Escape window: its block gives the first codeword for every
             # value of the next four bits.
@@ -169,7 +170,7 @@ def test_window_table_matches_canonical_code(name):
             continue
         got = [(ent >> (8 * j)) & 0xFF for j in range(len(want))]
         assert got == want
-        assert (ent & 0xFFFFFFFFFFFF) >> (8 * len(want)) == 0
+        assert ent >> (8 * len(want)) == 0
         pos, mask = 0, 0
         for s in want:
             pos += lengths[s]
