@@ -23,11 +23,9 @@
 //      re-parse from their predecessor's e until all agree, so the result
 //      never depends on resynchronisation happening;
 //   3. a workgroup prefix sum of the counts places each segment's symbols;
-//   4. each thread re-parses its segment and writes the exponents to the LDS
-//      staging area: exact byte stores until it reaches a 4-byte boundary,
-//      then one aligned 8-byte store per table lookup, which may run up to 7
-//      bytes past the thread's symbols into the next threads' first 8 bytes;
-//      after a barrier every thread rewrites its own first 8 bytes exactly;
+//   4. each thread re-parses its segment and ORs the exponents into the
+//      zeroed LDS staging area, one or two word atomics per table lookup, so
+//      every thread sets exactly its own bytes;
 //   5. the staged exponents are combined with the sign/mantissa bytes and
 //      written with 16-byte stores (8 bf16 or 16 uint8 per store).
 // If a round has more symbols than the staging area holds, steps 4-5 repeat
@@ -227,56 +225,24 @@ __device__ __forceinline__ uint32_t next_symbols(Reader& rd, const uint32_t* til
     return syms;
 }
 
-// Re-parse from true boundary p and write `count` symbols to stage[q...]
-// (stage is 4-byte aligned). Until q reaches a 4-byte boundary the bytes are
-// stored exactly, so the previous thread's bytes in that word are left
-// alone; after that each lookup is one aligned 8-byte store of the current
-// word (`cur` holds this thread's bytes of it) and the next one. Stores may
-// run up to 7 bytes past the last symbol.
+// Re-parse from true boundary p and place `count` symbols at stage[q...]
+// (stage is 4-byte aligned and zero where this thread's symbols go). Each
+// lookup ORs its bytes into the one or two words they fall in, so a thread
+// sets exactly its own bytes and threads sharing a word need no ordering.
 __device__ __forceinline__ void emit_run(const uint32_t* tile, const Tables& tb, uint32_t p,
                                          uint8_t* stage, uint32_t q, uint32_t count) {
     const uint32_t q_end = q + count;
     Reader rd = reader_at(tile, p);
-    uint32_t cur = 0;
-    bool exact = (q & 3u) != 0;
     while (q < q_end) {
         uint32_t n;
-        const uint32_t syms = next_symbols(rd, tile, tb, &n);
-        const uint32_t r = q & 3u;
-        const uint64_t sh = static_cast<uint64_t>(syms) << (8 * r);
-        const uint32_t lo = cur | static_cast<uint32_t>(sh);
-        const uint32_t hi = static_cast<uint32_t>(sh >> 32);
+        uint32_t syms = next_symbols(rd, tile, tb, &n);
+        // Only the symbols before q_end belong to this run.
+        if (q + n > q_end) syms &= (1u << (8 * (q_end - q))) - 1u;
+        const uint64_t sh = static_cast<uint64_t>(syms) << (8 * (q & 3u));
         uint32_t* word = reinterpret_cast<uint32_t*>(stage + (q & ~3u));
-        if (exact) {
-            for (uint32_t j = r; j < 4; ++j)
-                if (j < r + n) stage[(q & ~3u) + j] = static_cast<uint8_t>(lo >> (8 * j));
-            word[1] = hi;
-            exact = r + n < 4;
-        } else {
-            word[0] = lo;
-            word[1] = hi;
-        }
-        cur = r + n >= 4 ? hi : lo;
+        atomicOr(word, static_cast<uint32_t>(sh));
+        if ((sh >> 32) != 0) atomicOr(word + 1, static_cast<uint32_t>(sh >> 32));
         q += n;
-    }
-}
-
-// The first min(8, count) symbols from true boundary p, written exactly.
-__device__ __forceinline__ void write_head(const uint32_t* tile, const Tables& tb, uint32_t p,
-                                           uint8_t* stage, uint32_t q, uint32_t count) {
-    const uint32_t h = count < 8 ? count : 8;
-    uint64_t acc = 0;
-    Reader rd = reader_at(tile, p);
-    for (uint32_t k = 0; k < h;) {
-        uint32_t n;
-        const uint32_t syms = next_symbols(rd, tile, tb, &n);
-        acc |= static_cast<uint64_t>(syms) << (8 * k);
-        k += n;
-    }
-    if (h == 8) {
-        __builtin_memcpy(stage + q, &acc, 8);
-    } else {
-        for (uint32_t k = 0; k < h; ++k) stage[q + k] = static_cast<uint8_t>(acc >> (8 * k));
     }
 }
 
@@ -309,6 +275,18 @@ __device__ __forceinline__ uint32_t be_word(uint32_t v, int64_t nb, int64_t b) {
     return __builtin_bswap32(v);
 }
 
+// Zero stage bytes [from, region) (from a multiple of 4, region of 16);
+// thread i of a sub-group of tpc.
+__device__ __forceinline__ void clear_stage(uint8_t* stage, uint32_t from, uint32_t region,
+                                            uint32_t i, uint32_t tpc) {
+    const uint32_t w_end = (from / 4 + 3) & ~3u;  // first word on a 16-byte boundary
+    for (uint32_t w = from / 4 + i; w < w_end && w < region / 4; w += tpc)
+        reinterpret_cast<uint32_t*>(stage)[w] = 0;
+    const uint32_t v0 = w_end / 4;
+    for (uint32_t v = v0 + i; v < region / 16; v += tpc)
+        reinterpret_cast<uint4*>(stage)[v] = make_uint4(0, 0, 0, 0);
+}
+
 __device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* s_wsum) {
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
@@ -326,11 +304,15 @@ __device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* s_wsum
     return pre + x - v;
 }
 
-// bf16 bits of two elements: x holds e<<8|sm in each 16-bit half;
-// ((sm & 0x80) << 8) | (e << 7) | (sm & 0x7F) is the closed form of
-// _recombine (compressed_store.py:94-114).
-__device__ __forceinline__ uint32_t bf16_pair(uint32_t x) {
-    return ((x >> 1) & 0x7F807F80u) | (x & 0x007F007Fu) | ((x & 0x00800080u) << 8);
+// bf16 bits ((sm & 0x80) << 8) | (e << 7) | (sm & 0x7F), the closed form of
+// _recombine (compressed_store.py:94-114), for the two elements whose
+// sign/mantissa and exponent bytes sit at byte `lane2` and lane2+1 of `sm4`
+// and `e4`: sm|sm<<8 supplies bit 15 and bits 6..0, e<<7 bits 14..7.
+template <uint32_t kSmSel, uint32_t kExpSel>
+__device__ __forceinline__ uint32_t bf16_pair(uint32_t sm4, uint32_t e4) {
+    const uint32_t a = __builtin_amdgcn_perm(sm4, sm4, kSmSel);   // s0 s0 s1 s1
+    const uint32_t b = __builtin_amdgcn_perm(e4, e4, kExpSel) >> 1; // e0<<7, e1<<7
+    return (a & 0x807F807Fu) | (b & 0x7F807F80u);
 }
 
 __device__ __forceinline__ uint16_t bf16_one(uint32_t sm, uint32_t e) {
@@ -355,10 +337,10 @@ __device__ __forceinline__ void store_group(const DevTensor& T, const uint8_t* s
         const uint2 smv = *reinterpret_cast<const uint2*>(T.sm + el);
         const uint2 ev = *reinterpret_cast<const uint2*>(stage);
         uint4 o4;
-        o4.x = bf16_pair(__builtin_amdgcn_perm(ev.x, smv.x, 0x05010400u));
-        o4.y = bf16_pair(__builtin_amdgcn_perm(ev.x, smv.x, 0x07030602u));
-        o4.z = bf16_pair(__builtin_amdgcn_perm(ev.y, smv.y, 0x05010400u));
-        o4.w = bf16_pair(__builtin_amdgcn_perm(ev.y, smv.y, 0x07030602u));
+        o4.x = bf16_pair<0x01010000u, 0x010C000Cu>(smv.x, ev.x);
+        o4.y = bf16_pair<0x03030202u, 0x030C020Cu>(smv.x, ev.x);
+        o4.z = bf16_pair<0x01010000u, 0x010C000Cu>(smv.y, ev.y);
+        o4.w = bf16_pair<0x03030202u, 0x030C020Cu>(smv.y, ev.y);
         *reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.out) + el) = o4;
     } else {
         *reinterpret_cast<uint4*>(static_cast<uint8_t*>(T.out) + el) =
@@ -393,10 +375,10 @@ __device__ __forceinline__ void store_window(const DevTensor& T, const uint8_t* 
             if (v >= nfull) continue;
             const uint2 ev = *reinterpret_cast<const uint2*>(stage + v * kGroup);
             uint4 o4;
-            o4.x = bf16_pair(__builtin_amdgcn_perm(ev.x, smv[k].x, 0x05010400u));
-            o4.y = bf16_pair(__builtin_amdgcn_perm(ev.x, smv[k].x, 0x07030602u));
-            o4.z = bf16_pair(__builtin_amdgcn_perm(ev.y, smv[k].y, 0x05010400u));
-            o4.w = bf16_pair(__builtin_amdgcn_perm(ev.y, smv[k].y, 0x07030602u));
+            o4.x = bf16_pair<0x01010000u, 0x010C000Cu>(smv[k].x, ev.x);
+            o4.y = bf16_pair<0x03030202u, 0x030C020Cu>(smv[k].x, ev.x);
+            o4.z = bf16_pair<0x01010000u, 0x010C000Cu>(smv[k].y, ev.y);
+            o4.w = bf16_pair<0x03030202u, 0x030C020Cu>(smv[k].y, ev.y);
             *reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.out) + a0 +
                                       static_cast<int64_t>(v) * kGroup) = o4;
         }
@@ -480,6 +462,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         const uint32_t region = kStageBytes >> (__ffs(n_groups) - 1);
         uint8_t* stage = s_stage + g * region;
 
+        clear_stage(stage, 0, region, i, tpc);
         if (i == 0) s_gval[g] = static_cast<uint32_t>(nr);
         __syncthreads();
         uint32_t NR = 0;
@@ -578,8 +561,6 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 if (go) emit_run(tile, tb, f, stage, lead + o - base, run);
                 if (!done && !go) atomicMin(&s_gval[g], o);
                 __syncthreads();
-                if (go) write_head(tile, tb, f, stage, lead + o - base, run);
-                __syncthreads();
                 const uint32_t wend = s_gval[g];
                 const uint32_t avail = lead + (wend - base);
                 const uint32_t nfull = avail / kGroup;
@@ -600,7 +581,12 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 }
                 if (i == 0) s_gval[g] = want;
                 __syncthreads();
-                if (carry && i < rem) stage[i] = keep;
+                if (carry) {
+                    // Carried bytes (fewer than 16) to the front, everything
+                    // after them zero; a sub-group has at least 16 threads.
+                    if (i < 16) stage[i] = i < rem ? keep : 0;
+                    clear_stage(stage, 16, region, i, tpc);
+                }
                 if (!more) break;
                 __syncthreads();
             }
