@@ -5,36 +5,35 @@
 // of LDS, so two are resident per CU and one's memory phases overlap the
 // other's decoding. The grid is persistent and walks "items". An item is a
 // batch of chunks of one tensor: the workgroup splits into 512/TPC sub-groups
-// of TPC threads (TPC = 16..512, chosen per tensor from its chunk size so that
-// a chunk's symbols fill the sub-group's 64-bytes-per-thread staging area),
-// and each sub-group decodes one chunk.
+// of TPC threads (TPC = 16..512, chosen per tensor from its chunk size), and
+// each sub-group decodes one chunk.
 //
-// A sub-group walks its chunk's bitstream in rounds (one round for chunks of
-// up to TPC*224 bits). A round gives each thread one segment of S bits and
-// runs:
+// A sub-group walks its chunk's bitstream in rounds. A round gives each
+// thread one segment of S bits, with S at most kSlotCap times the shortest
+// code length, so no segment holds more than kSlotCap codeword starts. A
+// round runs:
 //   1. stage the round's bytes in LDS as big-endian 32-bit words;
-//   2. count: each thread parses its segment and records the first codeword
-//      boundary at or after the segment start (f), the first boundary at or
+//   2. decode: each thread parses its segment once, writing the symbols of
+//      every table lookup into its own LDS slot, and records the first
+//      codeword boundary at or after the segment start (f), the first at or
 //      after the segment end (e), and the codewords in between. Thread 0
 //      starts from the boundary carried over from the previous round; every
 //      other thread starts 32 bits early on a guess, which Huffman codes of
 //      weight exponents resynchronise within in practice. Segment t is right
-//      iff its f equals segment t-1's e; threads for which that fails
-//      re-parse from their predecessor's e until all agree, so the result
-//      never depends on resynchronisation happening;
+//      iff its f equals segment t-1's e; threads for which that fails decode
+//      again from their predecessor's e until all agree, so the result never
+//      depends on resynchronisation happening;
 //   3. a workgroup prefix sum of the counts places each segment's symbols;
-//   4. each thread re-parses its segment and ORs the exponents into the
-//      zeroed LDS staging area, one or two word atomics per table lookup, so
-//      every thread sets exactly its own bytes;
+//   4. compaction: each thread reads its slot into registers and, after a
+//      barrier, writes its symbols at their place in the same LDS area
+//      (whole aligned words, single bytes at the two ends);
 //   5. the staged exponents are combined with the sign/mantissa bytes and
-//      written with 16-byte stores (8 bf16 or 16 uint8 per store).
-// If a round has more symbols than the staging area holds, steps 4-5 repeat
-// over windows of whole segments.
+//      written with 16-byte stores (8 bf16 or 16 uint8 per store); the last
+//      partial vector group moves to the front for the next round.
 //
 // Codewords are read through a 12-bit window table of up to 4 codewords per
-// lookup (LDS; the counting pass reads only its 2-byte length part);
-// codewords of 13..16 bits go through 16-entry escape blocks (LDS for the
-// first 64 blocks, global memory beyond).
+// lookup (LDS); codewords of 13..16 bits go through 16-entry escape blocks
+// (LDS for the first 64 blocks, global memory beyond).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -56,18 +55,22 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kMinTpc = 16;
 constexpr int kMaxGroups = kThreads / kMinTpc;
 constexpr uint32_t kOverlapBits = 32;
-constexpr uint32_t kMaxSegBits = 224;
-constexpr uint32_t kMinSegBits = 48;
-constexpr uint32_t kStagePerThread = 64;
-constexpr uint32_t kStageSlack = 32;  // per sub-group: carried lead (< 16) + store overrun
+// Per-thread slot for one segment's symbols: an odd number of words, so the
+// slots of a wave's lanes start in different banks. A lookup writes 4 bytes
+// at the running count, so a slot holds kSlotCap symbols.
+constexpr uint32_t kSlotWords = 19;
+constexpr uint32_t kSlotBytes = 4 * kSlotWords;
+constexpr uint32_t kSlotCap = kSlotBytes - 4;
+constexpr uint32_t kMaxSegBits = 160;
+constexpr uint32_t kLeadBytes = 16;  // room for a carried partial vector group
 constexpr uint32_t kTileSlackWords = 4;
 constexpr uint32_t kTileWords = kThreads * kMaxSegBits / 32 + kTileSlackWords * kMaxGroups;
-constexpr uint32_t kStageBytes = kThreads * kStagePerThread + kStageSlack * kMaxGroups;
+constexpr uint32_t kStageBytes = kThreads * kSlotBytes + kLeadBytes * kMaxGroups;
 static_assert(kStageBytes % (16 * kMaxGroups) == 0, "stage regions stay 16-byte aligned");
 static_assert(kTileWords % kMaxGroups == 0, "tile regions split evenly");
 constexpr int kLdsEscBlocks = 64;
 constexpr uint32_t kTileBatch = 8;   // stream words a thread fetches per batch
-constexpr uint32_t kStoreBatch = 4;  // output vector groups a thread handles per batch
+constexpr uint32_t kStoreBatch = 8;  // output vector groups a thread handles per batch
 
 struct DevTensor {
     const uint8_t* packed;
@@ -96,6 +99,7 @@ struct Tables {
     const uint16_t* esc;     // LDS escape blocks (first kLdsEscBlocks)
     const __attribute__((address_space(1))) uint16_t* gesc;  // all escape blocks, global memory
     uint32_t sym0;
+    uint32_t min_len;  // shortest code length
 };
 
 // Bit reader over the staged stream. `pair` holds the two stream words that
@@ -134,12 +138,15 @@ __device__ __forceinline__ void reader_skip(Reader& rd, uint64_t next_pair, uint
 }
 
 // (symbol, length) of an escape window's first codeword; w holds the window
-// in bits 31..20 and the next four bits in 19..16.
+// in bits 31..20 and the next four bits in 19..16. Bits that start no
+// codeword of the stored LUT (only a malformed stream has them) decode to
+// sym_lut[0] and take the shortest code length, so every lookup consumes
+// at least that many bits per codeword, whatever the input.
 __device__ __forceinline__ uint32_t escape(const Tables& tb, uint32_t ent, uint32_t w,
                                            uint32_t* len) {
     const uint32_t blk = ent & 0xFFFFu;
     if (blk == kUnusedBlock) {
-        *len = 1;
+        *len = tb.min_len;
         return tb.sym0;
     }
     const uint32_t at = blk * kEscBlockEntries + ((w >> 16) & 15u);
@@ -150,8 +157,8 @@ __device__ __forceinline__ uint32_t escape(const Tables& tb, uint32_t ent, uint3
         v = tb.gesc[at];
     }
     const uint32_t l = v >> 8;
-    *len = l ? l : 1u;
-    return v & 0xFFu;
+    *len = l ? l : tb.min_len;
+    return l ? v & 0xFFu : tb.sym0;
 }
 
 struct Adv {
@@ -206,44 +213,80 @@ __device__ __forceinline__ Adv advance(const uint32_t* tile, const Tables& tb, u
     return {rd.p, n};
 }
 
-// One table lookup at the reader: up to 4 symbols (one byte each, zero
-// above the n-th) and the bits they take; advances the reader.
-__device__ __forceinline__ uint32_t next_symbols(Reader& rd, const uint32_t* tile,
-                                                 const Tables& tb, uint32_t* n) {
-    const uint32_t w = reader_bits(rd);
-    const uint32_t idx = w >> (32 - kWinBits);
-    const uint32_t meta = tb.meta[idx];
-    uint32_t syms = tb.syms[idx];
-    const uint64_t next = load_pair(tile, rd.p >> 5);
-    uint32_t adv = meta >> 12;
-    *n = __popc(meta & 0xFFFu);
-    if (adv == 0) {
-        syms = escape(tb, syms, w, &adv);
-        *n = 1;
-    }
-    reader_skip(rd, next, adv);
-    return syms;
+__device__ __forceinline__ uint32_t get_u32(const uint8_t* p) {
+    return *reinterpret_cast<const uint32_t*>(p);  // LDS, any byte alignment
 }
 
-// Re-parse from true boundary p and place `count` symbols at stage[q...]
-// (stage is 4-byte aligned and zero where this thread's symbols go). Each
-// lookup ORs its bytes into the one or two words they fall in, so a thread
-// sets exactly its own bytes and threads sharing a word need no ordering.
-__device__ __forceinline__ void emit_run(const uint32_t* tile, const Tables& tb, uint32_t p,
-                                         uint8_t* stage, uint32_t q, uint32_t count) {
-    const uint32_t q_end = q + count;
+// Writer of a thread's slot: symbols are appended with aligned word stores.
+// `acc` holds the symbols already placed in the current word (bytes below
+// n & 3, zero above); each append stores that word merged with the new
+// symbols and moves on when they cross into the next word.
+struct SlotWriter {
+    uint32_t* word;
+    uint32_t acc;
+    uint32_t n;
+};
+
+// Append c symbols (bytes 0..c-1 of syms; any bytes above are past the
+// count and never read).
+__device__ __forceinline__ void slot_put(SlotWriter& sw, uint32_t syms, uint32_t c) {
+    const uint32_t b = sw.n & 3u;
+    const uint64_t v = static_cast<uint64_t>(syms) << (8 * b);
+    const uint32_t lo = sw.acc | static_cast<uint32_t>(v);
+    *sw.word = lo;
+    const bool cross = b + c >= 4;
+    sw.acc = cross ? static_cast<uint32_t>(v >> 32) : lo;
+    sw.word += cross ? 1 : 0;
+    sw.n += c;
+}
+
+// Parse codewords from true boundary p while they start before x, appending
+// their symbols to the slot. Returns the first boundary at or after x and
+// the number of codewords. Every codeword (or unused window) takes at least
+// min_len bits, so a segment of at most kSlotCap * min_len bits never
+// holds more than kSlotCap codewords.
+__device__ __forceinline__ Adv decode_run(const uint32_t* tile, const Tables& tb, uint32_t p,
+                                          uint32_t x, uint8_t* slot) {
+    SlotWriter sw{reinterpret_cast<uint32_t*>(slot), 0u, 0u};
     Reader rd = reader_at(tile, p);
-    while (q < q_end) {
-        uint32_t n;
-        uint32_t syms = next_symbols(rd, tile, tb, &n);
-        // Only the symbols before q_end belong to this run.
-        if (q + n > q_end) syms &= (1u << (8 * (q_end - q))) - 1u;
-        const uint64_t sh = static_cast<uint64_t>(syms) << (8 * (q & 3u));
-        uint32_t* word = reinterpret_cast<uint32_t*>(stage + (q & ~3u));
-        atomicOr(word, static_cast<uint32_t>(sh));
-        if ((sh >> 32) != 0) atomicOr(word + 1, static_cast<uint32_t>(sh >> 32));
-        q += n;
+    while (rd.p + kWinBits <= x) {
+        const uint32_t w = reader_bits(rd);
+        const uint32_t idx = w >> (32 - kWinBits);
+        const uint32_t meta = tb.meta[idx];
+        uint32_t syms = tb.syms[idx];
+        const uint64_t next = load_pair(tile, rd.p >> 5);
+        uint32_t adv = meta >> 12;
+        uint32_t c = __popc(meta & 0xFFFu);
+        if (adv == 0) {
+            syms = escape(tb, syms, w, &adv);
+            c = 1;
+        }
+        slot_put(sw, syms, c);
+        reader_skip(rd, next, adv);
     }
+    while (rd.p < x) {
+        const uint32_t w = reader_bits(rd);
+        const uint32_t idx = w >> (32 - kWinBits);
+        const uint32_t meta = tb.meta[idx];
+        uint32_t syms = tb.syms[idx];
+        const uint64_t next = load_pair(tile, rd.p >> 5);
+        const uint32_t total = meta >> 12;
+        uint32_t adv, c;
+        if (total == 0) {
+            syms = escape(tb, syms, w, &adv);
+            c = 1;
+        } else {
+            const uint32_t ends = meta & 0xFFFu;
+            const uint32_t rel = x - rd.p;  // 1..11
+            const uint32_t upto = total < rel ? total : rel;
+            c = 1 + __popc(ends & ((1u << (upto - 1)) - 1u));
+            adv = total < rel ? total : rel - 1 + __ffs(ends >> (rel - 1));
+        }
+        slot_put(sw, syms, c);
+        reader_skip(rd, next, adv);
+    }
+    *sw.word = sw.acc;
+    return {rd.p, sw.n};
 }
 
 // Byte offset to load stream word b from: b itself when the 4 bytes lie in
@@ -273,18 +316,6 @@ __device__ __forceinline__ uint32_t be_word(uint32_t v, int64_t nb, int64_t b) {
     if (left <= 0) return 0u;
     if (left < 4) v &= (1u << (8 * left)) - 1u;
     return __builtin_bswap32(v);
-}
-
-// Zero stage bytes [from, region) (from a multiple of 4, region of 16);
-// thread i of a sub-group of tpc.
-__device__ __forceinline__ void clear_stage(uint8_t* stage, uint32_t from, uint32_t region,
-                                            uint32_t i, uint32_t tpc) {
-    const uint32_t w_end = (from / 4 + 3) & ~3u;  // first word on a 16-byte boundary
-    for (uint32_t w = from / 4 + i; w < w_end && w < region / 4; w += tpc)
-        reinterpret_cast<uint32_t*>(stage)[w] = 0;
-    const uint32_t v0 = w_end / 4;
-    for (uint32_t v = v0 + i; v < region / 16; v += tpc)
-        reinterpret_cast<uint4*>(stage)[v] = make_uint4(0, 0, 0, 0);
 }
 
 __device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* s_wsum) {
@@ -392,7 +423,6 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     __shared__ uint16_t s_esc[kLdsEscBlocks * kEscBlockEntries];
     __shared__ uint32_t s_tile[kTileWords];
     __shared__ __attribute__((aligned(16))) uint8_t s_stage[kStageBytes];
-    __shared__ uint32_t s_f[kThreads];
     __shared__ uint32_t s_e[kThreads];
     __shared__ uint32_t s_wsum[kWaves];
     __shared__ uint32_t s_gpre[kMaxGroups + 1];
@@ -434,7 +464,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         }
         const TableHeader* hdr = reinterpret_cast<const TableHeader*>(T.table);
         tb.sym0 = hdr->sym0;
+        tb.min_len = hdr->min_len >= 1 ? hdr->min_len : 1u;
         tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(T.table + kEscOffset);
+        // Segment length: at most kSlotCap codewords of the shortest length.
+        uint32_t S = kSlotCap * tb.min_len;
+        S = (S < kMaxSegBits ? S : kMaxSegBits) & ~7u;
 
         int64_t off = 0, nb = 0, lim = 0;
         const int64_t chunk_base = c * T.chunk_size;
@@ -449,29 +483,21 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         const uint8_t* cbytes = T.packed + off;
         const int64_t room = T.packed_nbytes - off;
         const int64_t chunk_bits = nb * 8;
-        const int64_t per_round_max = static_cast<int64_t>(tpc) * kMaxSegBits;
-        const int64_t nr = (chunk_bits + per_round_max - 1) / per_round_max;
-        uint32_t S = kMinSegBits;
-        if (nr > 0) {
-            const int64_t per_thread = (chunk_bits + tpc * nr - 1) / (tpc * nr);
-            S = static_cast<uint32_t>((per_thread + 7) & ~int64_t(7));
-            S = S < kMinSegBits ? kMinSegBits : S;
-        }
         const uint32_t round_bits = tpc * S;
+        const uint32_t nr = static_cast<uint32_t>((chunk_bits + round_bits - 1) / round_bits);
         uint32_t* tile = s_tile + g * (kTileWords >> (__ffs(n_groups) - 1));
         const uint32_t region = kStageBytes >> (__ffs(n_groups) - 1);
         uint8_t* stage = s_stage + g * region;
+        uint8_t* slot = stage + kLeadBytes + i * kSlotBytes;
 
-        clear_stage(stage, 0, region, i, tpc);
-        if (i == 0) s_gval[g] = static_cast<uint32_t>(nr);
+        if (i == 0) s_gval[g] = nr;
         __syncthreads();
         uint32_t NR = 0;
         for (uint32_t k = 0; k < n_groups; ++k) NR = NR > s_gval[k] ? NR : s_gval[k];
 
-        uint32_t p0 = 0;       // true start of the next round, relative to its first bit
-        int64_t ob = 0;        // chunk-local symbols written or staged so far
-        uint32_t lead = 0;     // staged symbols carried into the next window
-        uint32_t tail_at = 0;  // stage index of the symbols carried out of the last round
+        uint32_t p0 = 0;    // true start of the next round, relative to its first bit
+        int64_t ob = 0;     // chunk-local symbols placed so far
+        uint32_t lead = 0;  // placed symbols still staged at the front of the region
         for (uint32_t r = 0; r < NR; ++r) {
             const bool g_active = r < nr;
             const int64_t R0 = static_cast<int64_t>(r) * round_bits;
@@ -518,23 +544,21 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             uint32_t f = 0, e = 0, cnt = 0;
             if (active) {
                 f = i == 0 ? p0 : advance(tile, tb, seg_lo - kOverlapBits, seg_lo).p;
-                const Adv a = advance(tile, tb, f, seg_hi);
+                const Adv a = decode_run(tile, tb, f, seg_hi, slot);
                 e = a.p;
                 cnt = a.n;
             }
-            s_f[tid] = f;
             s_e[tid] = e;
             __syncthreads();
             for (;;) {
-                const bool bad = active && i > 0 && s_f[tid] != s_e[tid - 1];
+                const bool bad = active && i > 0 && f != s_e[tid - 1];
                 const uint32_t nf = bad ? s_e[tid - 1] : 0u;
                 if (!__syncthreads_or(bad)) break;
                 if (bad) {
                     f = nf;
-                    const Adv a = advance(tile, tb, f, seg_hi);
+                    const Adv a = decode_run(tile, tb, f, seg_hi, slot);
                     e = a.p;
                     cnt = a.n;
-                    s_f[tid] = f;
                     s_e[tid] = e;
                 }
                 __syncthreads();
@@ -550,46 +574,45 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const uint32_t gtot = s_gpre[g + 1] - s_gpre[g];
             const int64_t still = lim - ob;
             const uint32_t want = g_active ? (gtot < still ? gtot : static_cast<uint32_t>(still)) : 0u;
-            const uint32_t run = (active && o < want) ? (cnt < want - o ? cnt : want - o) : 0u;
-            bool done = run == 0;
-            uint32_t base = 0;  // sub-group symbol index at the start of this window
-            if (i == 0) s_gval[g] = want;
+
+            // Compaction. The dense area overlaps the slots, so every slot is
+            // in registers before any symbol moves.
+            const uint32_t m = want > o ? (cnt < want - o ? cnt : want - o) : 0u;
+            const uint32_t dpos = lead + o;
+            const uint32_t head0 = (4u - (dpos & 3u)) & 3u;
+            const uint32_t head = head0 < m ? head0 : m;  // bytes before the first aligned word
+            const uint32_t nbody = (m - head) >> 2;       // whole words
+            const uint32_t ntail = m - head - 4 * nbody;  // bytes after them
+            uint32_t rw[kSlotWords];
+            const uint32_t* slot_w = reinterpret_cast<const uint32_t*>(slot);
+#pragma unroll
+            for (uint32_t j = 0; j < kSlotWords; ++j) rw[j] = slot_w[j];
+            const uint32_t tv = get_u32(slot + head + 4 * nbody);
             __syncthreads();
-            for (;;) {
-                const uint32_t cap = region - 8 - lead;
-                const bool go = !done && o + run - base <= cap;
-                if (go) emit_run(tile, tb, f, stage, lead + o - base, run);
-                if (!done && !go) atomicMin(&s_gval[g], o);
-                __syncthreads();
-                const uint32_t wend = s_gval[g];
-                const uint32_t avail = lead + (wend - base);
-                const uint32_t nfull = avail / kGroup;
-                const int64_t a0 = chunk_base + ob - lead;
-                store_window<kBf16, kGroup>(T, stage, a0, nfull, i, tpc);
-                ob += wend - base;
-                base = wend;
-                done = done || go;
-                const uint32_t rem = avail - nfull * kGroup;
-                const bool more = __syncthreads_or(!done);
-                // Carry the partial vector group to the front of the staging
-                // area when this sub-group has symbols still to come.
-                const bool carry = g_active && (wend < want || r + 1 < nr);
-                const uint8_t keep = (carry && i < rem) ? stage[nfull * kGroup + i] : 0;
-                if (g_active) {
-                    tail_at = carry ? 0u : nfull * kGroup;
-                    lead = rem;
-                }
-                if (i == 0) s_gval[g] = want;
-                __syncthreads();
-                if (carry) {
-                    // Carried bytes (fewer than 16) to the front, everything
-                    // after them zero; a sub-group has at least 16 threads.
-                    if (i < 16) stage[i] = i < rem ? keep : 0;
-                    clear_stage(stage, 16, region, i, tpc);
-                }
-                if (!more) break;
-                __syncthreads();
-            }
+            uint8_t* dst = stage + dpos;
+#pragma unroll
+            for (uint32_t k = 0; k < 3; ++k)
+                if (k < head) dst[k] = static_cast<uint8_t>(rw[0] >> (8 * k));
+            uint32_t* body = reinterpret_cast<uint32_t*>(dst + head);
+#pragma unroll
+            for (uint32_t j = 0; j + 1 < kSlotWords; ++j)
+                if (j < nbody) body[j] = __builtin_amdgcn_alignbyte(rw[j + 1], rw[j], head);
+            uint8_t* tl = dst + head + 4 * nbody;
+#pragma unroll
+            for (uint32_t k = 0; k < 3; ++k)
+                if (k < ntail) tl[k] = static_cast<uint8_t>(tv >> (8 * k));
+            __syncthreads();
+
+            const uint32_t avail = lead + want;
+            const uint32_t nfull = avail / kGroup;
+            store_window<kBf16, kGroup>(T, stage, chunk_base + ob - lead, nfull, i, tpc);
+            ob += want;
+            // The partial vector group moves to the front for the next round.
+            const uint32_t rem = avail - nfull * kGroup;
+            const uint8_t keep = i < rem ? stage[nfull * kGroup + i] : 0;
+            __syncthreads();
+            if (i < rem) stage[i] = keep;
+            lead = rem;
             if (g_active) p0 = e_last - RB;
         }
 
@@ -599,7 +622,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         const int64_t t0 = chunk_base + ob - lead;
         const int64_t n_tail = lim - (ob - lead);
         for (int64_t k = i; k < n_tail; k += tpc) {
-            const uint32_t ex = k < lead ? stage[tail_at + k] : tb.sym0;
+            const uint32_t ex = k < lead ? stage[k] : tb.sym0;
             store_one<kBf16>(T, t0 + k, ex);
         }
     }
@@ -620,7 +643,7 @@ int cu_count() {
 uint32_t threads_per_chunk(int32_t chunk_size) {
     uint32_t t = kMinTpc;
     while (t < static_cast<uint32_t>(kThreads) &&
-           static_cast<int64_t>(t) * kStagePerThread < chunk_size)
+           static_cast<int64_t>(t) * kSlotCap < chunk_size)
         t <<= 1;
     return t;
 }
