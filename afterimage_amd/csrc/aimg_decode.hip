@@ -52,6 +52,8 @@ constexpr int kBlocksPerCu = 2;
 // per CU); bounds the registers a thread may use.
 constexpr int kWavesPerSimd = kBlocksPerCu * (kThreads / 64) / 4;
 constexpr int kWaves = kThreads / 64;
+constexpr uint32_t kLgThreads = 9;
+static_assert(kThreads == 1 << kLgThreads, "kLgThreads");
 constexpr int kMinTpc = 16;
 constexpr int kMaxGroups = kThreads / kMinTpc;
 constexpr uint32_t kOverlapBits = 32;
@@ -69,8 +71,13 @@ constexpr uint32_t kStageBytes = kThreads * kSlotBytes + kLeadBytes * kMaxGroups
 static_assert(kStageBytes % (16 * kMaxGroups) == 0, "stage regions stay 16-byte aligned");
 static_assert(kTileWords % kMaxGroups == 0, "tile regions split evenly");
 constexpr int kLdsEscBlocks = 64;
-constexpr uint32_t kTileBatch = 8;   // stream words a thread fetches per batch
-constexpr uint32_t kStoreBatch = 8;  // output vector groups a thread handles per batch
+// Stream words a thread fetches per round: a round has at most
+// tpc * kMaxSegBits / 32 + 3 words.
+constexpr uint32_t kTileBatch = kMaxSegBits / 32 + 1;
+// Output vector groups a thread stores per round: a round places at most
+// kSlotCap symbols per thread, plus a carried partial group.
+constexpr uint32_t kStoreBatch = (kSlotCap + 7) / 8 + 1;
+static_assert(kStoreBatch * 8 * kMinTpc >= kSlotCap * kMinTpc + 15, "one store batch covers a round");
 
 struct DevTensor {
     const uint8_t* packed;
@@ -84,7 +91,8 @@ struct DevTensor {
     int64_t item_begin;  // first item of this tensor in the launch
     int64_t n_jobs;      // chunks that hold output elements
     int32_t chunk_size;
-    int32_t tpc;         // threads per chunk (power of two, 16..1024)
+    int32_t tpc;         // threads per chunk (power of two, 16..512)
+    uint32_t packed_n32;  // packed_nbytes, capped at 2^32 - 1 (buffer loads)
 };
 
 struct LaunchArgs {
@@ -92,6 +100,27 @@ struct LaunchArgs {
     int64_t total_items;
     int32_t n_tensors;
 };
+
+// Read-only launch data that every thread of a workgroup reads at the same
+// address (table header, a workgroup's own chunk offset and length): loaded
+// through the constant address space, i.e. with scalar loads, which do not
+// queue behind the workgroup's outstanding vector stores.
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T* p) {
+    return *(const __attribute__((address_space(4))) T*)(p);
+}
+
+__device__ __forceinline__ const __attribute__((address_space(4))) TableHeader* header_of(
+    const uint8_t* table) {
+    return (const __attribute__((address_space(4))) TableHeader*)(table);
+}
+
+// Buffer resource over `nbytes` bytes at `base` (raw, stride 0): loads past
+// the end return zero instead of touching memory outside the buffer.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, uint32_t nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(nbytes),
+                                             0x00020000);
+}
 
 struct Tables {
     const uint32_t* syms;    // LDS window table: symbols / escape block
@@ -142,6 +171,11 @@ __device__ __forceinline__ void reader_skip(Reader& rd, uint64_t next_pair, uint
 // codeword of the stored LUT (only a malformed stream has them) decode to
 // sym_lut[0] and take the shortest code length, so every lookup consumes
 // at least that many bits per codeword, whatever the input.
+// kGlobalEsc: the table has escape blocks beyond the ones held in LDS. Only
+// then does the loop carry a global load, whose wait would also wait for
+// every prefetch in flight, so tables without such blocks use loops that
+// have none.
+template <bool kGlobalEsc>
 __device__ __forceinline__ uint32_t escape(const Tables& tb, uint32_t ent, uint32_t w,
                                            uint32_t* len) {
     const uint32_t blk = ent & 0xFFFFu;
@@ -151,7 +185,7 @@ __device__ __forceinline__ uint32_t escape(const Tables& tb, uint32_t ent, uint3
     }
     const uint32_t at = blk * kEscBlockEntries + ((w >> 16) & 15u);
     uint32_t v;
-    if (blk < static_cast<uint32_t>(kLdsEscBlocks)) {
+    if (!kGlobalEsc || blk < static_cast<uint32_t>(kLdsEscBlocks)) {
         v = tb.esc[at];
     } else {
         v = tb.gesc[at];
@@ -168,6 +202,7 @@ struct Adv {
 
 // Parse codewords from boundary p until the first boundary at or after x;
 // returns that boundary and the number of codewords that start before x.
+template <bool kGlobalEsc>
 __device__ __forceinline__ Adv advance(const uint32_t* tile, const Tables& tb, uint32_t p,
                                        uint32_t x) {
     uint32_t n = 0;
@@ -181,7 +216,7 @@ __device__ __forceinline__ Adv advance(const uint32_t* tile, const Tables& tb, u
         const uint32_t total = meta >> 12;
         if (total == 0) {
             uint32_t l;
-            escape(tb, tb.syms[idx], w, &l);
+            escape<kGlobalEsc>(tb, tb.syms[idx], w, &l);
             reader_skip(rd, next, l);
             n += 1;
             continue;
@@ -197,7 +232,7 @@ __device__ __forceinline__ Adv advance(const uint32_t* tile, const Tables& tb, u
         const uint32_t total = meta >> 12;
         if (total == 0) {
             uint32_t l;
-            escape(tb, tb.syms[idx], w, &l);
+            escape<kGlobalEsc>(tb, tb.syms[idx], w, &l);
             reader_skip(rd, next, l);
             n += 1;
             continue;
@@ -245,6 +280,7 @@ __device__ __forceinline__ void slot_put(SlotWriter& sw, uint32_t syms, uint32_t
 // the number of codewords. Every codeword (or unused window) takes at least
 // min_len bits, so a segment of at most kSlotCap * min_len bits never
 // holds more than kSlotCap codewords.
+template <bool kGlobalEsc>
 __device__ __forceinline__ Adv decode_run(const uint32_t* tile, const Tables& tb, uint32_t p,
                                           uint32_t x, uint8_t* slot) {
     SlotWriter sw{reinterpret_cast<uint32_t*>(slot), 0u, 0u};
@@ -258,7 +294,7 @@ __device__ __forceinline__ Adv decode_run(const uint32_t* tile, const Tables& tb
         uint32_t adv = meta >> 12;
         uint32_t c = __popc(meta & 0xFFFu);
         if (adv == 0) {
-            syms = escape(tb, syms, w, &adv);
+            syms = escape<kGlobalEsc>(tb, syms, w, &adv);
             c = 1;
         }
         slot_put(sw, syms, c);
@@ -273,7 +309,7 @@ __device__ __forceinline__ Adv decode_run(const uint32_t* tile, const Tables& tb
         const uint32_t total = meta >> 12;
         uint32_t adv, c;
         if (total == 0) {
-            syms = escape(tb, syms, w, &adv);
+            syms = escape<kGlobalEsc>(tb, syms, w, &adv);
             c = 1;
         } else {
             const uint32_t ends = meta & 0xFFFu;
@@ -289,12 +325,12 @@ __device__ __forceinline__ Adv decode_run(const uint32_t* tile, const Tables& tb
     return {rd.p, sw.n};
 }
 
-// Byte offset to load stream word b from: b itself when the 4 bytes lie in
-// the `room` readable bytes at the chunk start (room >= 4), else the last
-// readable word, so no byte outside the buffer is touched; the word is then
-// shifted into place by stream_word.
-__device__ __forceinline__ int64_t word_at(int64_t room, int64_t b) {
-    return b + 4 <= room ? b : room - 4;
+// Where to load the 4 bytes from packed-buffer byte A (A below the buffer
+// size): A itself, or the last whole word of the buffer (`last` = size - 4)
+// when A is within 3 bytes of its end; the word is then shifted right by
+// A - word_at(A) bytes.
+__device__ __forceinline__ uint32_t word_at(uint32_t A, uint32_t last) {
+    return A < last ? A : last;
 }
 
 __device__ __forceinline__ uint32_t load_u32(const uint8_t* p) {
@@ -303,7 +339,8 @@ __device__ __forceinline__ uint32_t load_u32(const uint8_t* p) {
     return v;
 }
 
-// The same from single bytes, for a buffer of fewer than 4 bytes.
+// Bytes b..b+3 of a chunk read one by one (zero at or past its end), for a
+// packed buffer of fewer than 4 bytes.
 __device__ __forceinline__ uint32_t load_bytes(const uint8_t* cbytes, int64_t nb, int64_t b) {
     uint32_t v = 0;
     for (int64_t k = 0; k < 4 && b + k < nb; ++k) v |= static_cast<uint32_t>(cbytes[b + k]) << (8 * k);
@@ -316,6 +353,137 @@ __device__ __forceinline__ uint32_t be_word(uint32_t v, int64_t nb, int64_t b) {
     if (left <= 0) return 0u;
     if (left < 4) v &= (1u << (8 * left)) - 1u;
     return __builtin_bswap32(v);
+}
+
+// One sub-group's share of an item: which chunk, where its bytes are, how
+// many output symbols it has and in how many rounds it is decoded.
+struct Job {
+    int32_t d;     // tensor; -1 past the last item
+    uint32_t lg;   // log2 of threads per chunk
+    uint32_t S;    // segment bits
+    int64_t c;     // chunk index
+    uint32_t off;  // chunk byte offset in the packed buffer
+    uint32_t nb;   // chunk bytes
+    uint32_t lim;  // output symbols of the chunk
+    uint32_t nr;   // rounds
+};
+
+__device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, uint32_t tid) {
+    Job J{-1, 0u, kMaxSegBits, 0, 0u, 0u, 0u, 0u};
+    if (item >= args.total_items) return J;
+    int d = 0;
+    while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
+    const DevTensor& T = args.t[d];
+    J.d = d;
+    J.lg = static_cast<uint32_t>(__ffs(T.tpc) - 1);
+    const uint32_t n_groups = kThreads >> J.lg;
+    J.c = (item - T.item_begin) * n_groups + (tid >> J.lg);
+    // Segment length: at most kSlotCap codewords of the shortest length.
+    const uint32_t min_len = header_of(T.table)->min_len;
+    const uint32_t S = kSlotCap * (min_len >= 1 ? min_len : 1u);
+    J.S = (S < kMaxSegBits ? S : kMaxSegBits) & ~7u;
+    if (J.c < T.n_jobs) {
+        int64_t off, nb;
+        if (n_groups == 1) {
+            const int64_t cu = item - T.item_begin;  // the same for every thread
+            off = load_uniform(T.offsets + cu);
+            nb = load_uniform(T.nbytes + cu);
+        } else {
+            off = T.offsets[J.c];
+            nb = T.nbytes[J.c];
+        }
+        off = off < 0 ? 0 : (off > T.packed_nbytes ? T.packed_nbytes : off);
+        nb = nb < 0 ? 0 : (nb > T.packed_nbytes - off ? T.packed_nbytes - off : nb);
+        int64_t lim = T.n_symbols - J.c * T.chunk_size;
+        lim = lim < 0 ? 0 : (lim > T.chunk_size ? T.chunk_size : lim);
+        J.off = static_cast<uint32_t>(off);
+        J.nb = static_cast<uint32_t>(nb);
+        J.lim = static_cast<uint32_t>(lim);
+        const int64_t round_bits = static_cast<int64_t>(J.S) << J.lg;
+        J.nr = static_cast<uint32_t>((static_cast<int64_t>(nb) * 8 + round_bits - 1) / round_bits);
+    }
+    return J;
+}
+
+// Bits of round r of a job (0 when the job has no round r).
+__device__ __forceinline__ uint32_t round_len(const Job& J, uint32_t r) {
+    if (r >= J.nr) return 0u;
+    const int64_t round_bits = static_cast<int64_t>(J.S) << J.lg;
+    const int64_t left = static_cast<int64_t>(J.nb) * 8 - r * round_bits;
+    return static_cast<uint32_t>(left < round_bits ? left : round_bits);
+}
+
+// A thread's stream words of one round, in flight in registers until they
+// are written to the LDS tile: words k * tpc + i of the round.
+struct Fetch {
+    uint32_t raw[kTileBatch];
+};
+
+// Packed-buffer byte offsets fit 32 bits: chunk offsets and sizes are int32.
+__device__ __forceinline__ uint32_t last_word(const DevTensor& T) {
+    return T.packed_n32 - 4;  // packed_nbytes >= 4 outside the tiny-buffer kernel
+}
+
+// kTiny: the packed buffer has fewer than 4 bytes, so its words are read
+// byte by byte. Such tensors go to a kernel of their own, which keeps these
+// loads and their waits out of every other kernel's round loop.
+template <bool kTiny>
+__device__ __forceinline__ void fetch_issue(Fetch& F, const LaunchArgs& args, const Job& J,
+                                            uint32_t r, uint32_t tid) {
+    if (round_len(J, r) == 0) return;
+    const DevTensor& T = args.t[J.d];
+    const uint32_t tpc = 1u << J.lg;
+    const uint32_t b0 = ((r * J.S) << J.lg) / 8 + 4 * (tid & (tpc - 1));
+    // All words are requested before any is used; words past the chunk read
+    // an in-buffer word and are zeroed when written.
+    if (!kTiny) {
+        const __amdgpu_buffer_rsrc_t rs = buffer_of(T.packed, T.packed_n32);
+        const uint32_t last = last_word(T);
+        const uint32_t A0 = J.off + b0;
+#pragma unroll
+        for (uint32_t k = 0; k < kTileBatch; ++k)
+            F.raw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, word_at(A0 + 4 * k * tpc, last), 0, 0);
+    } else {
+#pragma unroll
+        for (uint32_t k = 0; k < kTileBatch; ++k)
+            F.raw[k] = load_bytes(T.packed + J.off, J.nb, b0 + 4 * k * tpc);
+    }
+}
+
+// Marks v as used here, so every load into it has completed by this point
+// on every path. The vector-memory counter is in order: a load still pending
+// when its register is loaded again next round would make that round wait
+// for every store issued in between.
+__device__ __forceinline__ void consume(uint32_t v) { asm volatile("" ::"v"(v)); }
+
+template <bool kTiny>
+__device__ __forceinline__ void fetch_commit(const Fetch& F, const LaunchArgs& args, const Job& J,
+                                             uint32_t r, uint32_t tid, uint32_t* s_tile) {
+#pragma unroll
+    for (uint32_t k = 0; k < kTileBatch; ++k) consume(F.raw[k]);
+    const uint32_t RB = round_len(J, r);
+    if (RB == 0) return;
+    const DevTensor& T = args.t[J.d];
+    const uint32_t tpc = 1u << J.lg;
+    const uint32_t i = tid & (tpc - 1);
+    uint32_t* tile = s_tile + (tid >> J.lg) * (kTileWords >> (kLgThreads - J.lg));
+    const uint32_t last = last_word(T);
+    const uint32_t b0 = ((r * J.S) << J.lg) / 8;
+    const uint32_t nw = (RB + 31) / 32 + 3;
+#pragma unroll
+    for (uint32_t k = 0; k < kTileBatch; ++k) {
+        const uint32_t j = k * tpc + i;
+        if (j >= nw) continue;
+        const uint32_t b = b0 + 4 * j;
+        uint32_t v = F.raw[k];
+        if (!kTiny) {
+            // Within the chunk A - word_at(A, last) is 0..3; words at or past
+            // its end are zeroed below, whatever the shift.
+            const uint32_t A = J.off + b;
+            v >>= 8 * ((A - word_at(A, last)) & 3u);
+        }
+        tile[j] = be_word(v, J.nb, b);
+    }
 }
 
 __device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* s_wsum) {
@@ -359,64 +527,87 @@ __device__ __forceinline__ void store_one(const DevTensor& T, int64_t el, uint32
     }
 }
 
-// Write staged vector group g (kGroup elements) to output element el.
+// Sign/mantissa bytes of the vector groups a thread stores in one round
+// (groups k * tpc + i of the round), requested ahead of use.
+template <bool kBf16>
+struct SmBatch {
+    uint2 v[kBf16 ? kStoreBatch : 1];
+};
+
+// Buffer loads (zero past the tensor's last byte), so the batch needs no
+// clamping and is issued back to back; the batch offset is a scalar.
 template <bool kBf16, int kGroup>
-__device__ __forceinline__ void store_group(const DevTensor& T, const uint8_t* stage, int64_t el) {
-    if (kGroup == 1) {
-        store_one<kBf16>(T, el, stage[0]);
-    } else if (kBf16) {
-        const uint2 smv = *reinterpret_cast<const uint2*>(T.sm + el);
-        const uint2 ev = *reinterpret_cast<const uint2*>(stage);
-        uint4 o4;
-        o4.x = bf16_pair<0x01010000u, 0x010C000Cu>(smv.x, ev.x);
-        o4.y = bf16_pair<0x03030202u, 0x030C020Cu>(smv.x, ev.x);
-        o4.z = bf16_pair<0x01010000u, 0x010C000Cu>(smv.y, ev.y);
-        o4.w = bf16_pair<0x03030202u, 0x030C020Cu>(smv.y, ev.y);
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.out) + el) = o4;
-    } else {
-        *reinterpret_cast<uint4*>(static_cast<uint8_t*>(T.out) + el) =
-            *reinterpret_cast<const uint4*>(stage);
+__device__ __forceinline__ void sm_issue(SmBatch<kBf16>& B, const DevTensor& T, int64_t a0,
+                                         uint32_t i, uint32_t tpc) {
+    if (!kBf16 || kGroup == 1) return;
+    const __amdgpu_buffer_rsrc_t rs = buffer_of(T.sm, static_cast<uint32_t>(T.n_symbols));
+    const uint32_t v0 = static_cast<uint32_t>(a0) + i * kGroup;
+#pragma unroll
+    for (uint32_t k = 0; k < kStoreBatch; ++k) {
+        const auto d = __builtin_amdgcn_raw_buffer_load_b64(rs, v0, k * tpc * kGroup, 0);
+        B.v[k] = make_uint2(d[0], d[1]);
     }
 }
 
-// Vector groups [0, nfull) of a staged window to output elements a0...;
-// thread i of a sub-group of tpc takes groups i, i+tpc, ... and requests
-// the sign/mantissa bytes of a whole batch before combining any.
+// Vector groups [0, nfull) of the staged round to output elements a0...;
+// thread i of a sub-group of tpc takes groups i, i + tpc, ...
 template <bool kBf16, int kGroup>
-__device__ __forceinline__ void store_window(const DevTensor& T, const uint8_t* stage, int64_t a0,
-                                             uint32_t nfull, uint32_t i, uint32_t tpc) {
-    if (kGroup == 1 || !kBf16) {
-        for (uint32_t v = i; v < nfull; v += tpc)
-            store_group<kBf16, kGroup>(T, stage + v * kGroup, a0 + static_cast<int64_t>(v) * kGroup);
+__device__ __forceinline__ void store_round(const SmBatch<kBf16>& B, const DevTensor& T,
+                                            const uint8_t* stage, int64_t a0, uint32_t nfull,
+                                            uint32_t i, uint32_t tpc) {
+    if (kGroup == 1) {
+        for (uint32_t v = i; v < nfull; v += tpc) store_one<kBf16>(T, a0 + v, stage[v]);
         return;
     }
-    for (uint32_t v0 = 0; v0 < nfull; v0 += kStoreBatch * tpc) {
-        // Unconditional loads (indices clamped into the window) so a batch
-        // is issued back to back.
-        uint2 smv[kStoreBatch];
+    if (!kBf16) {
+        for (uint32_t v = i; v < nfull; v += tpc)
+            *reinterpret_cast<uint4*>(static_cast<uint8_t*>(T.out) + a0 + static_cast<int64_t>(v) * kGroup) =
+                *reinterpret_cast<const uint4*>(stage + v * kGroup);
+        return;
+    }
 #pragma unroll
-        for (uint32_t k = 0; k < kStoreBatch; ++k) {
-            const uint32_t v = v0 + k * tpc + i;
-            const uint32_t vc = v < nfull ? v : nfull - 1;
-            smv[k] = *reinterpret_cast<const uint2*>(T.sm + a0 + static_cast<int64_t>(vc) * kGroup);
-        }
+    for (uint32_t k = 0; k < kStoreBatch; ++k) {
+        consume(B.v[k].x);
+        consume(B.v[k].y);
+    }
+    // All staged exponents are read (from clamped, always valid offsets)
+    // before any is combined, so the LDS reads overlap.
+    uint2 ev[kStoreBatch];
 #pragma unroll
-        for (uint32_t k = 0; k < kStoreBatch; ++k) {
-            const uint32_t v = v0 + k * tpc + i;
-            if (v >= nfull) continue;
-            const uint2 ev = *reinterpret_cast<const uint2*>(stage + v * kGroup);
-            uint4 o4;
-            o4.x = bf16_pair<0x01010000u, 0x010C000Cu>(smv[k].x, ev.x);
-            o4.y = bf16_pair<0x03030202u, 0x030C020Cu>(smv[k].x, ev.x);
-            o4.z = bf16_pair<0x01010000u, 0x010C000Cu>(smv[k].y, ev.y);
-            o4.w = bf16_pair<0x03030202u, 0x030C020Cu>(smv[k].y, ev.y);
-            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.out) + a0 +
-                                      static_cast<int64_t>(v) * kGroup) = o4;
-        }
+    for (uint32_t k = 0; k < kStoreBatch; ++k) {
+        const uint32_t v = k * tpc + i;
+        ev[k] = *reinterpret_cast<const uint2*>(stage + (v < nfull ? v : 0u) * kGroup);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.out) + a0);
+#pragma unroll
+    for (uint32_t k = 0; k < kStoreBatch; ++k) {
+        const uint32_t v = k * tpc + i;
+        if (v >= nfull) continue;
+        uint4 o4;
+        o4.x = bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].x, ev[k].x);
+        o4.y = bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].x, ev[k].x);
+        o4.z = bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].y, ev[k].y);
+        o4.w = bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].y, ev[k].y);
+        dst[v] = o4;
     }
 }
 
-template <bool kBf16, int kGroup>
+// Window table and the first kLdsEscBlocks escape blocks of a table blob to LDS.
+__device__ __forceinline__ void load_table(const uint8_t* table, uint32_t tid, uint32_t* s_wsyms,
+                                           uint16_t* s_wmeta, uint16_t* s_esc) {
+    const uint4* src = reinterpret_cast<const uint4*>(table + kSymsOffset);
+    uint4* dst = reinterpret_cast<uint4*>(s_wsyms);
+    for (uint32_t j = tid; j < kWinEntries / 4; j += kThreads) dst[j] = src[j];
+    const uint4* msrc = reinterpret_cast<const uint4*>(table + kMetaOffset);
+    uint4* mdst = reinterpret_cast<uint4*>(s_wmeta);
+    for (uint32_t j = tid; j < kWinEntries / 8; j += kThreads) mdst[j] = msrc[j];
+    const uint32_t n_blocks = header_of(table)->n_esc_blocks;
+    const uint32_t n_esc = n_blocks < static_cast<uint32_t>(kLdsEscBlocks) ? n_blocks : kLdsEscBlocks;
+    const uint16_t* gesc = reinterpret_cast<const uint16_t*>(table + kEscOffset);
+    for (uint32_t j = tid; j < n_esc * kEscBlockEntries; j += kThreads) s_esc[j] = gesc[j];
+}
+
+template <bool kBf16, int kGroup, bool kTiny>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const LaunchArgs args) {
     __shared__ uint32_t s_wsyms[kWinEntries];
     __shared__ uint16_t s_wmeta[kWinEntries];
@@ -435,62 +626,45 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     tb.meta = s_wmeta;
     tb.esc = s_esc;
 
+    // Software pipeline: the stream words of the next round (or of the next
+    // item's first round) are in flight while the current round decodes.
+    // The first item's words and table load together.
+    Job cur = make_job(args, blockIdx.x, tid);
+    Fetch F;
+    fetch_issue<kTiny>(F, args, cur, 0, tid);
+    loaded = args.t[cur.d].table;
+    load_table(loaded, tid, s_wsyms, s_wmeta, s_esc);
+    fetch_commit<kTiny>(F, args, cur, 0, tid, s_tile);
+
     for (int64_t item = blockIdx.x; item < args.total_items; item += gridDim.x) {
-        int d = 0;
-        while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
-        const DevTensor& T = args.t[d];
-        const uint32_t lg = static_cast<uint32_t>(__ffs(T.tpc) - 1);
+        const DevTensor& T = args.t[cur.d];
+        const uint32_t lg = cur.lg;
         const uint32_t tpc = 1u << lg;
         const uint32_t g = tid >> lg;
-        const uint32_t i = tid & (tpc - 1);
+        const uint32_t i_item = tid & (tpc - 1);
         const uint32_t n_groups = kThreads >> lg;
-        const int64_t c = (item - T.item_begin) * n_groups + g;
-        const bool has_chunk = c < T.n_jobs;
+        const uint32_t S = cur.S;
+        const Job nxt = make_job(args, item + gridDim.x, tid);
 
-        __syncthreads();  // the previous item is done with LDS
+        __syncthreads();  // the previous item is done with LDS; its tile writes are visible
         if (T.table != loaded) {
             loaded = T.table;
-            const uint4* src = reinterpret_cast<const uint4*>(T.table + kSymsOffset);
-            uint4* dst = reinterpret_cast<uint4*>(s_wsyms);
-            for (uint32_t j = tid; j < kWinEntries / 4; j += kThreads) dst[j] = src[j];
-            const uint4* msrc = reinterpret_cast<const uint4*>(T.table + kMetaOffset);
-            uint4* mdst = reinterpret_cast<uint4*>(s_wmeta);
-            for (uint32_t j = tid; j < kWinEntries / 8; j += kThreads) mdst[j] = msrc[j];
-            const TableHeader* hdr = reinterpret_cast<const TableHeader*>(T.table);
-            const uint32_t n_esc = hdr->n_esc_blocks < static_cast<uint32_t>(kLdsEscBlocks)
-                                       ? hdr->n_esc_blocks : kLdsEscBlocks;
-            const uint16_t* gesc = reinterpret_cast<const uint16_t*>(T.table + kEscOffset);
-            for (uint32_t j = tid; j < n_esc * kEscBlockEntries; j += kThreads) s_esc[j] = gesc[j];
+            load_table(T.table, tid, s_wsyms, s_wmeta, s_esc);
         }
-        const TableHeader* hdr = reinterpret_cast<const TableHeader*>(T.table);
+        const auto* hdr = header_of(T.table);
         tb.sym0 = hdr->sym0;
         tb.min_len = hdr->min_len >= 1 ? hdr->min_len : 1u;
         tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(T.table + kEscOffset);
-        // Segment length: at most kSlotCap codewords of the shortest length.
-        uint32_t S = kSlotCap * tb.min_len;
-        S = (S < kMaxSegBits ? S : kMaxSegBits) & ~7u;
+        const bool global_esc = hdr->n_esc_blocks > static_cast<uint32_t>(kLdsEscBlocks);
 
-        int64_t off = 0, nb = 0, lim = 0;
-        const int64_t chunk_base = c * T.chunk_size;
-        if (has_chunk) {
-            off = T.offsets[c];
-            nb = T.nbytes[c];
-            off = off < 0 ? 0 : (off > T.packed_nbytes ? T.packed_nbytes : off);
-            nb = nb < 0 ? 0 : (nb > T.packed_nbytes - off ? T.packed_nbytes - off : nb);
-            lim = T.n_symbols - chunk_base;
-            lim = lim < 0 ? 0 : (lim > T.chunk_size ? T.chunk_size : lim);
-        }
-        const uint8_t* cbytes = T.packed + off;
-        const int64_t room = T.packed_nbytes - off;
-        const int64_t chunk_bits = nb * 8;
-        const uint32_t round_bits = tpc * S;
-        const uint32_t nr = static_cast<uint32_t>((chunk_bits + round_bits - 1) / round_bits);
-        uint32_t* tile = s_tile + g * (kTileWords >> (__ffs(n_groups) - 1));
-        const uint32_t region = kStageBytes >> (__ffs(n_groups) - 1);
+        const int64_t chunk_base = cur.c * T.chunk_size;
+        const int64_t lim = cur.lim;
+        const uint32_t* tile = s_tile + g * (kTileWords >> (kLgThreads - lg));
+        const uint32_t region = kStageBytes >> (kLgThreads - lg);
         uint8_t* stage = s_stage + g * region;
-        uint8_t* slot = stage + kLeadBytes + i * kSlotBytes;
+        uint8_t* slot = stage + kLeadBytes + i_item * kSlotBytes;
 
-        if (i == 0) s_gval[g] = nr;
+        if (i_item == 0) s_gval[g] = cur.nr;
         __syncthreads();
         uint32_t NR = 0;
         for (uint32_t k = 0; k < n_groups; ++k) NR = NR > s_gval[k] ? NR : s_gval[k];
@@ -499,52 +673,36 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         int64_t ob = 0;     // chunk-local symbols placed so far
         uint32_t lead = 0;  // placed symbols still staged at the front of the region
         for (uint32_t r = 0; r < NR; ++r) {
-            const bool g_active = r < nr;
-            const int64_t R0 = static_cast<int64_t>(r) * round_bits;
-            uint32_t RB = 0;
-            if (g_active) {
-                const int64_t left = chunk_bits - R0;
-                RB = left < round_bits ? static_cast<uint32_t>(left) : round_bits;
-            }
-            const uint32_t nw = g_active ? (RB + 31) / 32 + 3 : 0;
-            // All of this thread's words are requested before any is used;
-            // loads past the chunk read a clamped in-buffer word and are zeroed.
-            for (uint32_t j0 = 0; j0 < nw; j0 += kTileBatch * tpc) {
-                uint32_t raw[kTileBatch];
-                if (room >= 4) {
-#pragma unroll
-                    for (uint32_t k = 0; k < kTileBatch; ++k) {
-                        const int64_t b = R0 / 8 + 4 * static_cast<int64_t>(j0 + k * tpc + i);
-                        const int64_t bb = b < nb ? b : 0;
-                        raw[k] = load_u32(cbytes + word_at(room, bb));
-                    }
-#pragma unroll
-                    for (uint32_t k = 0; k < kTileBatch; ++k) {
-                        const int64_t b = R0 / 8 + 4 * static_cast<int64_t>(j0 + k * tpc + i);
-                        const int64_t bb = b < nb ? b : 0;
-                        raw[k] >>= 8 * static_cast<uint32_t>(bb - word_at(room, bb));
-                    }
-                } else {
-#pragma unroll
-                    for (uint32_t k = 0; k < kTileBatch; ++k)
-                        raw[k] = load_bytes(cbytes, nb,
-                                            R0 / 8 + 4 * static_cast<int64_t>(j0 + k * tpc + i));
-                }
-#pragma unroll
-                for (uint32_t k = 0; k < kTileBatch; ++k) {
-                    const uint32_t j = j0 + k * tpc + i;
-                    if (j < nw) tile[j] = be_word(raw[k], nb, R0 / 8 + 4 * static_cast<int64_t>(j));
-                }
-            }
-            __syncthreads();
+            // Offsets derived from the thread index are cheap to recompute;
+            // keeping them live across the round costs registers.
+            uint32_t i = i_item;
+            asm volatile("" : "+v"(i));
+            // Next words: this item's round r + 1, or the next item's round 0.
+            const bool last = r + 1 == NR;
+            const Job& fj = last ? nxt : cur;
+            const uint32_t fr = last ? 0u : r + 1;
+            fetch_issue<kTiny>(F, args, fj, fr, tid);
+            // Sign/mantissa bytes of every group this round can fill (its
+            // output starts at a known element; its length is known only
+            // after decoding), requested now so the store never waits.
+            SmBatch<kBf16> smb;
+            sm_issue<kBf16, kGroup>(smb, T, chunk_base + ob - lead, i, tpc);
+            const uint32_t RB = round_len(cur, r);
+            const bool g_active = RB != 0;
 
             const uint32_t seg_lo = i * S;
             const bool active = seg_lo < RB;
             const uint32_t seg_hi = active ? (seg_lo + S < RB ? seg_lo + S : RB) : 0u;
             uint32_t f = 0, e = 0, cnt = 0;
             if (active) {
-                f = i == 0 ? p0 : advance(tile, tb, seg_lo - kOverlapBits, seg_lo).p;
-                const Adv a = decode_run(tile, tb, f, seg_hi, slot);
+                Adv a;
+                if (global_esc) {
+                    f = i == 0 ? p0 : advance<true>(tile, tb, seg_lo - kOverlapBits, seg_lo).p;
+                    a = decode_run<true>(tile, tb, f, seg_hi, slot);
+                } else {
+                    f = i == 0 ? p0 : advance<false>(tile, tb, seg_lo - kOverlapBits, seg_lo).p;
+                    a = decode_run<false>(tile, tb, f, seg_hi, slot);
+                }
                 e = a.p;
                 cnt = a.n;
             }
@@ -556,7 +714,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 if (!__syncthreads_or(bad)) break;
                 if (bad) {
                     f = nf;
-                    const Adv a = decode_run(tile, tb, f, seg_hi, slot);
+                    const Adv a = global_esc ? decode_run<true>(tile, tb, f, seg_hi, slot)
+                                             : decode_run<false>(tile, tb, f, seg_hi, slot);
                     e = a.p;
                     cnt = a.n;
                     s_e[tid] = e;
@@ -574,6 +733,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const uint32_t gtot = s_gpre[g + 1] - s_gpre[g];
             const int64_t still = lim - ob;
             const uint32_t want = g_active ? (gtot < still ? gtot : static_cast<uint32_t>(still)) : 0u;
+            const uint32_t avail = lead + want;
+            const uint32_t nfull = avail / kGroup;
+            const int64_t a0 = chunk_base + ob - lead;
 
             // Compaction. The dense area overlaps the slots, so every slot is
             // in registers before any symbol moves.
@@ -601,11 +763,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
 #pragma unroll
             for (uint32_t k = 0; k < 3; ++k)
                 if (k < ntail) tl[k] = static_cast<uint8_t>(tv >> (8 * k));
+            // Every thread is past its decode, so the tile takes the next words.
+            fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
             __syncthreads();
 
-            const uint32_t avail = lead + want;
-            const uint32_t nfull = avail / kGroup;
-            store_window<kBf16, kGroup>(T, stage, chunk_base + ob - lead, nfull, i, tpc);
+            store_round<kBf16, kGroup>(smb, T, stage, a0, nfull, i, tpc);
             ob += want;
             // The partial vector group moves to the front for the next round.
             const uint32_t rem = avail - nfull * kGroup;
@@ -615,16 +777,21 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             lead = rem;
             if (g_active) p0 = e_last - RB;
         }
+        if (NR == 0) {
+            fetch_issue<kTiny>(F, args, nxt, 0, tid);
+            fetch_commit<kTiny>(F, args, nxt, 0, tid, s_tile);
+        }
 
         // Symbols carried out of the last round, then positions no codeword
         // of the chunk reached: those decode from zero bits, i.e. to sym_lut[0].
         __syncthreads();
         const int64_t t0 = chunk_base + ob - lead;
         const int64_t n_tail = lim - (ob - lead);
-        for (int64_t k = i; k < n_tail; k += tpc) {
+        for (int64_t k = i_item; k < n_tail; k += tpc) {
             const uint32_t ex = k < lead ? stage[k] : tb.sym0;
             store_one<kBf16>(T, t0 + k, ex);
         }
+        cur = nxt;
     }
 }
 
@@ -648,17 +815,44 @@ uint32_t threads_per_chunk(int32_t chunk_size) {
     return t;
 }
 
+// Tensors of one launch: those whose packed buffer has fewer than 4 bytes go
+// to a kernel of their own (see fetch_issue).
+struct Batch {
+    LaunchArgs args{};
+    int64_t items = 0;
+    int m = 0;
+    bool vec = true;
+};
+
+template <bool kBf16>
+int launch_batch(Batch& B, hipStream_t s, bool tiny) {
+    B.args.n_tensors = B.m;
+    B.args.total_items = B.items;
+    if (B.items == 0) return AIMG_OK;
+    const int64_t slots = static_cast<int64_t>(cu_count()) * kBlocksPerCu;
+    const int64_t grid = B.items < slots ? B.items : slots;
+    const dim3 gdim(static_cast<uint32_t>(grid)), bdim(kThreads);
+    if (tiny) {
+        hipLaunchKernelGGL((decode_kernel<kBf16, 1, true>), gdim, bdim, 0, s, B.args);
+    } else if (B.vec) {
+        hipLaunchKernelGGL((decode_kernel<kBf16, kBf16 ? 8 : 16, false>), gdim, bdim, 0, s, B.args);
+    } else {
+        hipLaunchKernelGGL((decode_kernel<kBf16, 1, false>), gdim, bdim, 0, s, B.args);
+    }
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+        return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    return AIMG_OK;
+}
+
 template <bool kBf16>
 int launch(const aimg_tensor* ts, int n, void* stream) {
     if (ts == nullptr && n > 0) return fail(AIMG_ERR_INVALID_ARGUMENT, "tensors is null");
     if (n < 0 || n > AIMG_MAX_TENSORS)
         return fail(AIMG_ERR_INVALID_ARGUMENT,
                     "n_tensors must be in 0.." + std::to_string(AIMG_MAX_TENSORS));
-    LaunchArgs args{};
-    int64_t items = 0;
-    bool vec = true;
+    Batch normal, tiny;
     const int group = kBf16 ? 8 : 16;
-    int m = 0;
     for (int i = 0; i < n; ++i) {
         const aimg_tensor& t = ts[i];
         const std::string who = "tensor " + std::to_string(i) + ": ";
@@ -668,15 +862,18 @@ int launch(const aimg_tensor* ts, int n, void* stream) {
         if (t.n_symbols > static_cast<int64_t>(t.n_chunks) * t.chunk_size)
             return fail(AIMG_ERR_INVALID_ARGUMENT, who + "n_symbols exceeds n_chunks * chunk_size");
         if (t.n_symbols == 0) continue;
+        if (t.n_symbols > INT32_MAX)
+            return fail(AIMG_ERR_UNSUPPORTED, who + "more than 2^31 - 1 symbols");
         if (t.packed == nullptr || t.chunk_offsets == nullptr || t.chunk_nbytes == nullptr ||
             t.out == nullptr || t.table == nullptr || (kBf16 && t.sign_mantissa == nullptr))
             return fail(AIMG_ERR_INVALID_ARGUMENT, who + "null device pointer");
         if (reinterpret_cast<uintptr_t>(t.table) % 16 != 0)
             return fail(AIMG_ERR_INVALID_ARGUMENT, who + "table must be 16-byte aligned");
+        Batch& B = t.packed_nbytes < 4 ? tiny : normal;
         if (reinterpret_cast<uintptr_t>(t.out) % 16 != 0 || t.chunk_size % group != 0 ||
             (kBf16 && reinterpret_cast<uintptr_t>(t.sign_mantissa) % 8 != 0))
-            vec = false;
-        DevTensor& dt = args.t[m++];
+            B.vec = false;
+        DevTensor& dt = B.args.t[B.m++];
         dt.packed = t.packed;
         dt.offsets = t.chunk_offsets;
         dt.nbytes = t.chunk_nbytes;
@@ -684,31 +881,21 @@ int launch(const aimg_tensor* ts, int n, void* stream) {
         dt.out = t.out;
         dt.table = static_cast<const uint8_t*>(t.table);
         dt.packed_nbytes = t.packed_nbytes;
+        dt.packed_n32 = t.packed_nbytes > static_cast<int64_t>(UINT32_MAX)
+                            ? UINT32_MAX : static_cast<uint32_t>(t.packed_nbytes);
         dt.n_symbols = t.n_symbols;
         dt.chunk_size = t.chunk_size;
         dt.tpc = static_cast<int32_t>(threads_per_chunk(t.chunk_size));
         // Chunks past the last output element hold nothing to write.
         dt.n_jobs = (t.n_symbols + t.chunk_size - 1) / t.chunk_size;
-        dt.item_begin = items;
+        dt.item_begin = B.items;
         const int64_t per_item = kThreads / dt.tpc;
-        items += (dt.n_jobs + per_item - 1) / per_item;
+        B.items += (dt.n_jobs + per_item - 1) / per_item;
     }
-    args.n_tensors = m;
-    args.total_items = items;
-    if (items == 0) return AIMG_OK;
-    const int64_t slots = static_cast<int64_t>(cu_count()) * kBlocksPerCu;
-    const int64_t grid = items < slots ? items : slots;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 gdim(static_cast<uint32_t>(grid)), bdim(kThreads);
-    if (vec) {
-        hipLaunchKernelGGL((decode_kernel<kBf16, kBf16 ? 8 : 16>), gdim, bdim, 0, s, args);
-    } else {
-        hipLaunchKernelGGL((decode_kernel<kBf16, 1>), gdim, bdim, 0, s, args);
-    }
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess)
-        return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
-    return AIMG_OK;
+    const int rc = launch_batch<kBf16>(normal, s, false);
+    if (rc != AIMG_OK) return rc;
+    return launch_batch<kBf16>(tiny, s, true);
 }
 
 }  // namespace

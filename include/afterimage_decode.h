@@ -54,10 +54,10 @@ const char* aimg_last_error(void);
 /* Replaces prepare_decode_tables (afterimage/runtime/gpu_decode_v2.py:71-76), */
 /* which copies sym_lut / len_lut to the device as two int32 tensors. Here    */
 /* the stored LUT is turned on the host into one self-contained table blob:  */
-/* a 4096-entry multi-symbol window table (up to 6 codewords per 12-bit      */
-/* window) plus the stored LUT packed to 16 bits per entry for codewords     */
-/* longer than 12 bits. The caller copies the blob to device memory once per */
-/* codebook and may share it across every tensor with the same codebook.     */
+/* a 4096-entry multi-symbol window table (up to 4 codewords per 12-bit      */
+/* window) plus 16-entry escape blocks for codewords of 13..16 bits. The     */
+/* caller copies the blob to device memory once per codebook and may share   */
+/* it across every tensor with the same codebook.                            */
 /* ------------------------------------------------------------------------- */
 
 /* Size in bytes of the table blob for a LUT of 2^max_bits entries (1..16). */
@@ -88,7 +88,7 @@ typedef struct aimg_tensor {
     void* out;                     /* device: uint16 bf16 bits, or uint8        */
     const void* table;             /* device: blob from aimg_build_table        */
     int64_t packed_nbytes;         /* bytes readable at `packed`                */
-    int64_t n_symbols;             /* elements to write                         */
+    int64_t n_symbols;             /* elements to write (below 2^31)            */
     int32_t chunk_size;            /* symbols per chunk                         */
     int32_t n_chunks;              /* chunks described by offsets / nbytes      */
 } aimg_tensor;
@@ -100,6 +100,7 @@ typedef struct aimg_tensor {
  * | (sm[i] & 0x7F) for i < n_symbols, where n_symbols <= n_chunks*chunk_size.
  * Replaces the body of decompress_layer_gpu (compressed_store.py:186-240) for
  * device-resident inputs; one call covers a whole decoder block of tensors.
+ * A tensor of 2^31 or more symbols fails with AIMG_ERR_UNSUPPORTED.
  */
 int aimg_decode_bf16(const aimg_tensor* tensors, int n_tensors, void* stream);
 

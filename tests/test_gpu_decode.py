@@ -11,6 +11,7 @@ import oracle
 from afterimage_amd.runtime.compressed_store import _slice_encoded
 from afterimage_amd.runtime.gpu_decode_v2 import decode_gpu_v2
 from afterimage_amd.runtime.huffman_chunked import encode_chunked
+from tests.distributions import many_escape_windows
 from tests.golden_data import case, case_names
 
 pytestmark = pytest.mark.gpu
@@ -83,6 +84,12 @@ def test_block_chunks_values_are_accepted(block_chunks):
 def test_n_chunks_not_multiple_of_block_chunks():
     torch.manual_seed(1)
     _check(torch.randint(0, 256, (7777,)), chunk_size=100, block_chunks=32)
+
+
+@pytest.mark.parametrize("chunk_size", [256, 4096, 65536])
+def test_escape_blocks_beyond_the_lds_share(chunk_size):
+    """Tables with more than 64 escape blocks read the rest from global memory."""
+    _check(torch.from_numpy(many_escape_windows(7, 400_000)), chunk_size=chunk_size)
 
 
 @pytest.mark.parametrize("max_bits", [8, 12, 16])

@@ -4,6 +4,8 @@ bit-exact against the original weights and the oracle.
 Mirrors the reference's tests/test_compressed_store.py, test_sliced_decompress.py,
 test_decode_table_reuse.py and test_chunked_lm_head_gpu.py decode cases.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -141,6 +143,26 @@ def test_unaligned_output_view_uses_elementwise_stores():
     decode_bf16([dt], [buf[3:]])
     assert torch.equal(_bits(buf[3:]).reshape(W.shape), _bits(W))
     assert torch.equal(_bits(buf[:3]), torch.zeros(3, dtype=torch.int16))
+
+
+@pytest.mark.parametrize("shape,chunk,tiny", [((3,), 3, True), ((7, 5), 16, False),
+                                              ((64, 1000), 4096, False)])
+def test_packed_buffer_without_slack_bytes(shape, chunk, tiny):
+    """A packed buffer that ends at the last chunk's last byte: the final
+    words come from the buffer's last whole word, or byte by byte when the
+    whole buffer is shorter than 4 bytes."""
+    W = workloads.bf16_normal(shape, 123, 0.02)
+    layer = compress_layer(W, chunk_size=chunk)
+    enc = layer.encoded
+    used = int(enc.chunk_offsets[-1]) + int(enc.chunk_nbytes[-1])
+    assert (used < 4) == tiny
+    trimmed = dataclasses.replace(enc, packed=enc.packed[:used].copy())
+    dt = DeviceTensor.from_encoded(trimmed, layer.sign_mantissa, "cuda")
+    assert dt.packed.numel() == used
+    (out,) = decode_bf16([dt])
+    assert torch.equal(_bits(out), _bits(W).reshape(-1))
+    exps = gd.decode_gpu_v2(trimmed).cpu().numpy()
+    assert np.array_equal(exps, oracle.decode_chunked_reference(enc))
 
 
 def test_batched_block_launch_with_shared_codebooks():

@@ -7,12 +7,14 @@ from pathlib import Path
 
 import numpy as np
 import pytest
+import torch
 
 import oracle
 from afterimage_amd import _native
 from afterimage_amd.runtime.device import build_table_blob
 from afterimage_amd.runtime.huffman import build_lengths, canonical_codes, code_arrays
-from afterimage_amd.runtime.huffman_chunked import ChunkedEncoded, pack_chunks
+from afterimage_amd.runtime.huffman_chunked import ChunkedEncoded, encode_chunked, pack_chunks
+from tests.distributions import many_escape_windows
 from tests.golden_data import case, case_names
 
 HEADER = Path(__file__).resolve().parent.parent / "include" / "afterimage_decode.h"
@@ -197,3 +199,14 @@ def test_native_packer_rejects_symbol_without_code():
         pack_chunks(np.array([0, 1, 5], np.uint8), codes, lengths, 4, 1)
     with pytest.raises(ValueError):
         code_arrays({300: 0}, {300: 1})
+
+
+def test_escape_blocks_can_exceed_the_lds_share():
+    """The premise of the GPU test of escape blocks held in global memory."""
+    data = many_escape_windows(7, 400_000)
+    enc = encode_chunked(torch.from_numpy(data), chunk_size=4096, max_bits=16)
+    blob = build_table_blob(enc.sym_lut, enc.len_lut, enc.max_bits)
+    hdr = np.frombuffer(blob[:64].tobytes(), dtype=np.uint32)
+    assert hdr[6] > 64  # n_esc_blocks
+    assert int(enc.len_lut.max()) > 12
+
