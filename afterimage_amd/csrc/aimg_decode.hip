@@ -131,37 +131,41 @@ struct Tables {
     uint32_t min_len;  // shortest code length
 };
 
-// Bit reader over the staged stream. `pair` holds the two stream words that
-// start at bit `base` (a multiple of 32, base <= p <= base + 47); a step
-// reads at most 16 bits, all inside the pair. While a step's table lookup is
-// in flight, the reader already fetches the pair starting at the word that
-// contains p, which holds the next step's bits, so each step waits for one
-// LDS round trip.
+// Bit reader over the staged stream. A sub-group's tile holds its round's
+// stream words in reverse order (word j at top[-j]), so one 8-byte LDS read
+// at top - k - 1 returns words k+1 and k as the low and high halves of the
+// 64-bit pair that starts at word k. `pair` holds the words from bit
+// p - sh (a multiple of 32, sh <= 47); a step reads at most 16 bits, all
+// inside the pair. While a step's table lookup is in flight, the reader
+// already fetches the pair starting at the word that contains p, which
+// holds the next step's bits, so each step waits for one LDS round trip.
 struct Reader {
-    const uint32_t* tile;
+    const uint32_t* top;
     uint32_t p;
-    uint32_t base;
+    uint32_t sh;
     uint64_t pair;
 };
 
-__device__ __forceinline__ uint64_t load_pair(const uint32_t* tile, uint32_t k) {
-    return (static_cast<uint64_t>(tile[k]) << 32) | tile[k + 1];
+__device__ __forceinline__ uint64_t load_pair(const uint32_t* top, uint32_t k) {
+    uint64_t v;
+    __builtin_memcpy(&v, top - k - 1, 8);  // 4-byte aligned: two word reads
+    return v;
 }
 
-__device__ __forceinline__ Reader reader_at(const uint32_t* tile, uint32_t p) {
-    return {tile, p, p & ~31u, load_pair(tile, p >> 5)};
+__device__ __forceinline__ Reader reader_at(const uint32_t* top, uint32_t p) {
+    return {top, p, p & 31u, load_pair(top, p >> 5)};
 }
 
 // The 32 bits at the reader's position (bits past the pair read as zero;
 // only the first 16 are used).
 __device__ __forceinline__ uint32_t reader_bits(const Reader& rd) {
-    return static_cast<uint32_t>((rd.pair << (rd.p - rd.base)) >> 32);
+    return static_cast<uint32_t>((rd.pair << rd.sh) >> 32);
 }
 
 // Move the reader forward by n bits (n <= 16), using the pair prefetched at
 // the old position.
 __device__ __forceinline__ void reader_skip(Reader& rd, uint64_t next_pair, uint32_t n) {
-    rd.base = rd.p & ~31u;
+    rd.sh = (rd.p & 31u) + n;
     rd.pair = next_pair;
     rd.p += n;
 }
@@ -195,6 +199,10 @@ __device__ __forceinline__ uint32_t escape(const Tables& tb, uint32_t ent, uint3
     return l ? v & 0xFFu : tb.sym0;
 }
 
+// Escape windows are rare: the wave branches to them only when one of its
+// lanes has one.
+__device__ __forceinline__ bool any_lane(bool v) { return __builtin_amdgcn_ballot_w64(v) != 0; }
+
 struct Adv {
     uint32_t p;
     uint32_t n;
@@ -203,32 +211,33 @@ struct Adv {
 // Parse codewords from boundary p until the first boundary at or after x;
 // returns that boundary and the number of codewords that start before x.
 template <bool kGlobalEsc>
-__device__ __forceinline__ Adv advance(const uint32_t* tile, const Tables& tb, uint32_t p,
+__device__ __forceinline__ Adv advance(const uint32_t* top, const Tables& tb, uint32_t p,
                                        uint32_t x) {
     uint32_t n = 0;
-    Reader rd = reader_at(tile, p);
+    Reader rd = reader_at(top, p);
     // Whole windows while no codeword of the window can reach x.
-    while (rd.p + kWinBits <= x) {
+    const int32_t x12 = static_cast<int32_t>(x) - kWinBits;
+    while (static_cast<int32_t>(rd.p) <= x12) {
         const uint32_t w = reader_bits(rd);
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
-        const uint64_t next = load_pair(tile, rd.p >> 5);
-        const uint32_t total = meta >> 12;
-        if (total == 0) {
-            uint32_t l;
-            escape<kGlobalEsc>(tb, tb.syms[idx], w, &l);
-            reader_skip(rd, next, l);
-            n += 1;
-            continue;
+        const uint64_t next = load_pair(top, rd.p >> 5);
+        uint32_t adv = meta >> 12;
+        uint32_t c = __popc(meta & 0xFFFu);
+        if (__builtin_expect(any_lane(adv == 0), 0)) {
+            if (adv == 0) {
+                escape<kGlobalEsc>(tb, tb.syms[idx], w, &adv);
+                c = 1;
+            }
         }
-        n += __popc(meta & 0xFFFu);
-        reader_skip(rd, next, total);
+        n += c;
+        reader_skip(rd, next, adv);
     }
     while (rd.p < x) {
         const uint32_t w = reader_bits(rd);
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
-        const uint64_t next = load_pair(tile, rd.p >> 5);
+        const uint64_t next = load_pair(top, rd.p >> 5);
         const uint32_t total = meta >> 12;
         if (total == 0) {
             uint32_t l;
@@ -252,52 +261,53 @@ __device__ __forceinline__ uint32_t get_u32(const uint8_t* p) {
     return *reinterpret_cast<const uint32_t*>(p);  // LDS, any byte alignment
 }
 
-// Writer of a thread's slot: symbols are appended with aligned word stores.
-// `acc` holds the symbols already placed in the current word (bytes below
-// n & 3, zero above); each append stores that word merged with the new
-// symbols and moves on when they cross into the next word.
-struct SlotWriter {
-    uint32_t* word;
-    uint32_t acc;
-    uint32_t n;
-};
-
-// Append c symbols (bytes 0..c-1 of syms; any bytes above are past the
-// count and never read).
-__device__ __forceinline__ void slot_put(SlotWriter& sw, uint32_t syms, uint32_t c) {
-    const uint32_t b = sw.n & 3u;
-    const uint64_t v = static_cast<uint64_t>(syms) << (8 * b);
-    const uint32_t lo = sw.acc | static_cast<uint32_t>(v);
-    *sw.word = lo;
-    const bool cross = b + c >= 4;
-    sw.acc = cross ? static_cast<uint32_t>(v >> 32) : lo;
-    sw.word += cross ? 1 : 0;
-    sw.n += c;
+// A thread's slot is zero before its segment is decoded into it.
+__device__ __forceinline__ void clear_slot(uint8_t* slot) {
+    uint32_t* w = reinterpret_cast<uint32_t*>(slot);
+#pragma unroll
+    for (uint32_t j = 0; j < kSlotWords; ++j) w[j] = 0;
 }
 
-// Parse codewords from true boundary p while they start before x, appending
-// their symbols to the slot. Returns the first boundary at or after x and
-// the number of codewords. Every codeword (or unused window) takes at least
-// min_len bits, so a segment of at most kSlotCap * min_len bits never
-// holds more than kSlotCap codewords.
+// Place the symbols of one lookup (bytes of syms, zero above the lookup's
+// count) at slot[n...]: OR them into the one or two words they fall in,
+// so no word needs reading or merging first.
+__device__ __forceinline__ void slot_or(uint8_t* slot, uint32_t n, uint32_t syms) {
+    const uint64_t v = static_cast<uint64_t>(syms) << (8 * (n & 3u));
+    uint32_t* w = reinterpret_cast<uint32_t*>(slot + (n & ~3u));
+    __hip_atomic_fetch_or(w, static_cast<uint32_t>(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_fetch_or(w + 1, static_cast<uint32_t>(v >> 32), __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Parse codewords from true boundary p while they start before x, placing
+// their symbols in the (zeroed) slot. Returns the first boundary at or
+// after x and the number of codewords. Every codeword (or unused window)
+// takes at least min_len bits, so a segment of at most kSlotCap * min_len
+// bits never holds more than kSlotCap codewords, and every word written
+// lies inside the slot. The last lookup may leave symbols that start at or
+// after x past the count; they are never read.
 template <bool kGlobalEsc>
-__device__ __forceinline__ Adv decode_run(const uint32_t* tile, const Tables& tb, uint32_t p,
+__device__ __forceinline__ Adv decode_run(const uint32_t* top, const Tables& tb, uint32_t p,
                                           uint32_t x, uint8_t* slot) {
-    SlotWriter sw{reinterpret_cast<uint32_t*>(slot), 0u, 0u};
-    Reader rd = reader_at(tile, p);
-    while (rd.p + kWinBits <= x) {
+    uint32_t n = 0;
+    Reader rd = reader_at(top, p);
+    const int32_t x12 = static_cast<int32_t>(x) - kWinBits;
+    while (static_cast<int32_t>(rd.p) <= x12) {
         const uint32_t w = reader_bits(rd);
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
         uint32_t syms = tb.syms[idx];
-        const uint64_t next = load_pair(tile, rd.p >> 5);
+        const uint64_t next = load_pair(top, rd.p >> 5);
         uint32_t adv = meta >> 12;
         uint32_t c = __popc(meta & 0xFFFu);
-        if (adv == 0) {
-            syms = escape<kGlobalEsc>(tb, syms, w, &adv);
-            c = 1;
+        if (__builtin_expect(any_lane(adv == 0), 0)) {
+            if (adv == 0) {
+                syms = escape<kGlobalEsc>(tb, syms, w, &adv);
+                c = 1;
+            }
         }
-        slot_put(sw, syms, c);
+        slot_or(slot, n, syms);
+        n += c;
         reader_skip(rd, next, adv);
     }
     while (rd.p < x) {
@@ -305,7 +315,7 @@ __device__ __forceinline__ Adv decode_run(const uint32_t* tile, const Tables& tb
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
         uint32_t syms = tb.syms[idx];
-        const uint64_t next = load_pair(tile, rd.p >> 5);
+        const uint64_t next = load_pair(top, rd.p >> 5);
         const uint32_t total = meta >> 12;
         uint32_t adv, c;
         if (total == 0) {
@@ -318,11 +328,11 @@ __device__ __forceinline__ Adv decode_run(const uint32_t* tile, const Tables& tb
             c = 1 + __popc(ends & ((1u << (upto - 1)) - 1u));
             adv = total < rel ? total : rel - 1 + __ffs(ends >> (rel - 1));
         }
-        slot_put(sw, syms, c);
+        slot_or(slot, n, syms);
+        n += c;
         reader_skip(rd, next, adv);
     }
-    *sw.word = sw.acc;
-    return {rd.p, sw.n};
+    return {rd.p, n};
 }
 
 // Where to load the 4 bytes from packed-buffer byte A (A below the buffer
@@ -419,6 +429,12 @@ struct Fetch {
     uint32_t raw[kTileBatch];
 };
 
+// Word 0 of sub-group g's tile (the tile is filled downwards, see Reader).
+__device__ __forceinline__ uint32_t* tile_top(uint32_t* s_tile, uint32_t g, uint32_t lg) {
+    const uint32_t words = kTileWords >> (kLgThreads - lg);
+    return s_tile + g * words + words - 1;
+}
+
 // Packed-buffer byte offsets fit 32 bits: chunk offsets and sizes are int32.
 __device__ __forceinline__ uint32_t last_word(const DevTensor& T) {
     return T.packed_n32 - 4;  // packed_nbytes >= 4 outside the tiny-buffer kernel
@@ -466,7 +482,7 @@ __device__ __forceinline__ void fetch_commit(const Fetch& F, const LaunchArgs& a
     const DevTensor& T = args.t[J.d];
     const uint32_t tpc = 1u << J.lg;
     const uint32_t i = tid & (tpc - 1);
-    uint32_t* tile = s_tile + (tid >> J.lg) * (kTileWords >> (kLgThreads - J.lg));
+    uint32_t* top = tile_top(s_tile, tid >> J.lg, J.lg);
     const uint32_t last = last_word(T);
     const uint32_t b0 = ((r * J.S) << J.lg) / 8;
     const uint32_t nw = (RB + 31) / 32 + 3;
@@ -482,7 +498,7 @@ __device__ __forceinline__ void fetch_commit(const Fetch& F, const LaunchArgs& a
             const uint32_t A = J.off + b;
             v >>= 8 * ((A - word_at(A, last)) & 3u);
         }
-        tile[j] = be_word(v, J.nb, b);
+        *(top - j) = be_word(v, J.nb, b);
     }
 }
 
@@ -659,7 +675,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
 
         const int64_t chunk_base = cur.c * T.chunk_size;
         const int64_t lim = cur.lim;
-        const uint32_t* tile = s_tile + g * (kTileWords >> (kLgThreads - lg));
+        const uint32_t* top = tile_top(s_tile, g, lg);
         const uint32_t region = kStageBytes >> (kLgThreads - lg);
         uint8_t* stage = s_stage + g * region;
         uint8_t* slot = stage + kLeadBytes + i_item * kSlotBytes;
@@ -695,13 +711,14 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const uint32_t seg_hi = active ? (seg_lo + S < RB ? seg_lo + S : RB) : 0u;
             uint32_t f = 0, e = 0, cnt = 0;
             if (active) {
+                clear_slot(slot);
                 Adv a;
                 if (global_esc) {
-                    f = i == 0 ? p0 : advance<true>(tile, tb, seg_lo - kOverlapBits, seg_lo).p;
-                    a = decode_run<true>(tile, tb, f, seg_hi, slot);
+                    f = i == 0 ? p0 : advance<true>(top, tb, seg_lo - kOverlapBits, seg_lo).p;
+                    a = decode_run<true>(top, tb, f, seg_hi, slot);
                 } else {
-                    f = i == 0 ? p0 : advance<false>(tile, tb, seg_lo - kOverlapBits, seg_lo).p;
-                    a = decode_run<false>(tile, tb, f, seg_hi, slot);
+                    f = i == 0 ? p0 : advance<false>(top, tb, seg_lo - kOverlapBits, seg_lo).p;
+                    a = decode_run<false>(top, tb, f, seg_hi, slot);
                 }
                 e = a.p;
                 cnt = a.n;
@@ -714,8 +731,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 if (!__syncthreads_or(bad)) break;
                 if (bad) {
                     f = nf;
-                    const Adv a = global_esc ? decode_run<true>(tile, tb, f, seg_hi, slot)
-                                             : decode_run<false>(tile, tb, f, seg_hi, slot);
+                    clear_slot(slot);
+                    const Adv a = global_esc ? decode_run<true>(top, tb, f, seg_hi, slot)
+                                             : decode_run<false>(top, tb, f, seg_hi, slot);
                     e = a.p;
                     cnt = a.n;
                     s_e[tid] = e;
