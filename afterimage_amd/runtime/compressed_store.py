@@ -16,7 +16,7 @@ import numpy as np
 import torch
 
 from .device import DeviceTensor, decode_bf16
-from .huffman_chunked import ChunkedEncoded, encode_chunked
+from .huffman_chunked import ChunkedEncoded, encode_chunked, lengths_from_counts, symbol_counts
 
 EXPONENT_SHIFT = 7
 
@@ -46,13 +46,7 @@ def split_fields(bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return exponent, sign_mantissa
 
 
-def compress_layer(W: torch.Tensor, chunk_size: int = 1024, max_bits: int = 16,
-                   work_chunk_elems: int = 1 << 24) -> CompressedLayer:
-    """Field split + chunked encode (compressed_store.py:48-91).
-
-    The split runs in bounded pieces of ``work_chunk_elems`` so no full-size
-    integer temporaries are built for large matrices.
-    """
+def _split_weight(W: torch.Tensor, work_chunk_elems: int) -> tuple[np.ndarray, np.ndarray]:
     assert W.dtype == torch.bfloat16, f"expected bfloat16, got {W.dtype}"
     if work_chunk_elems < 1:
         raise ValueError("work_chunk_elems must be positive")
@@ -63,9 +57,42 @@ def compress_layer(W: torch.Tensor, chunk_size: int = 1024, max_bits: int = 16,
     for start in range(0, n, work_chunk_elems):
         end = min(start + work_chunk_elems, n)
         exponent[start:end], sign_mantissa[start:end] = split_fields(raw[start:end])
-    encoded = encode_chunked(exponent, chunk_size=chunk_size, max_bits=max_bits)
+    return exponent, sign_mantissa
+
+
+def compress_layer(W: torch.Tensor, chunk_size: int = 1024, max_bits: int = 16,
+                   work_chunk_elems: int = 1 << 24, *,
+                   lengths: dict[int, int] | None = None) -> CompressedLayer:
+    """Field split + chunked encode (compressed_store.py:48-91).
+
+    The split runs in bounded pieces of ``work_chunk_elems`` so no full-size
+    integer temporaries are built for large matrices. ``lengths``
+    (keyword-only, not in the reference) encodes with a given codebook; see
+    compress_group.
+    """
+    exponent, sign_mantissa = _split_weight(W, work_chunk_elems)
+    encoded = encode_chunked(exponent, chunk_size=chunk_size, max_bits=max_bits,
+                             lengths=lengths)
     return CompressedLayer(sign_mantissa=torch.from_numpy(sign_mantissa), encoded=encoded,
                            shape=tuple(W.shape))
+
+
+def compress_group(weights: list[torch.Tensor], chunk_size: int = 1024, max_bits: int = 16,
+                   work_chunk_elems: int = 1 << 24) -> list[CompressedLayer]:
+    """Compress several tensors with one exponent codebook built from their
+    pooled histogram (for example all tensors of one role in a decoder block),
+    so they share one stored LUT and one device decode table. Each tensor's
+    stream decodes exactly as if it had been encoded alone with that LUT."""
+    split = [_split_weight(W, work_chunk_elems) for W in weights]
+    counts = np.zeros(256, dtype=np.int64)
+    for exponent, _ in split:
+        counts += symbol_counts(exponent)
+    lengths = lengths_from_counts(counts, max_bits)
+    return [CompressedLayer(sign_mantissa=torch.from_numpy(sm),
+                            encoded=encode_chunked(e, chunk_size=chunk_size, max_bits=max_bits,
+                                                   lengths=lengths),
+                            shape=tuple(W.shape))
+            for W, (e, sm) in zip(weights, split)]
 
 
 def _recombine(exponent: torch.Tensor, sign_mantissa: torch.Tensor,

@@ -71,16 +71,37 @@ def pack_chunks(flat: np.ndarray, codes: dict[int, int], lengths: dict[int, int]
     return out[: total.value].copy(), nbytes
 
 
-def encode_chunked(exponents, chunk_size: int = 512, max_bits: int = 16) -> ChunkedEncoded:
-    """Chunked encode of a symbol tensor/array (huffman_chunked.py:151-207)."""
+def symbol_counts(exponents) -> np.ndarray:
+    """Histogram of a symbol tensor/array over 0..255 (int64[256])."""
+    return np.bincount(_as_symbols(exponents), minlength=256).astype(np.int64)
+
+
+def lengths_from_counts(counts: np.ndarray, max_bits: int = 16) -> dict[int, int]:
+    """Code lengths for a histogram, as encode_chunked builds them."""
+    freqs = {int(s): int(c) for s, c in enumerate(counts) if c > 0}
+    return build_lengths(freqs, max_bits=max_bits)
+
+
+def encode_chunked(exponents, chunk_size: int = 512, max_bits: int = 16, *,
+                   lengths: dict[int, int] | None = None) -> ChunkedEncoded:
+    """Chunked encode of a symbol tensor/array (huffman_chunked.py:151-207).
+
+    ``lengths`` (keyword-only, not in the reference) encodes with a given
+    codebook instead of one built from this array's histogram, so several
+    tensors can share one codebook and one decode table; every symbol that
+    occurs must have a length."""
     if chunk_size < 1:
         raise ValueError("chunk_size must be >= 1, got %d" % chunk_size)
     shape = tuple(exponents.shape)
     flat = _as_symbols(exponents)
     n = int(flat.shape[0])
-    counts = np.bincount(flat, minlength=256)
-    freqs = {int(s): int(c) for s, c in enumerate(counts) if c > 0}
-    lengths = build_lengths(freqs, max_bits=max_bits)
+    if lengths is None:
+        lengths = lengths_from_counts(np.bincount(flat, minlength=256), max_bits)
+    else:
+        present = np.flatnonzero(np.bincount(flat, minlength=256))
+        missing = [int(s) for s in present if int(s) not in lengths]
+        if missing:
+            raise ValueError("symbols %s occur but have no code" % missing[:8])
     table, codes = canonical_codes(lengths)
     sym_lut, len_lut = build_decode_lut(table, codes)
     # The LUT is indexed at the code's real width, which can be below the cap.

@@ -9,7 +9,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from .runtime.compressed_store import CompressedLayer, compress_layer
+from .runtime.compressed_store import CompressedLayer, compress_group, compress_layer
 
 
 def bf16_normal(shape, seed: int, scale: float = 0.02, outlier_frac: float = 0.0,
@@ -55,3 +55,28 @@ def small_layer(seed: int = 1, rows: int = 1024, cols: int = 3072,
     """The 1024x3072 MLP up-projection of a 0.6B model, N(0, 0.02)."""
     w = bf16_normal((rows, cols), seed, 0.02)
     return w, compress_layer(w, chunk_size=chunk_size)
+
+
+def block_14b(seed: int = 3, chunk_size: int = 65536, scale: float = 1.0
+              ) -> list[tuple[str, torch.Tensor, CompressedLayer]]:
+    """One 14B-class decoder block: weights N(0, 0.02), RMSNorm weights
+    N(1.0, 0.05), tensor i seeded with seed * 100 + i. Tensors of one role
+    share one codebook built from their pooled exponent histogram. ``scale``
+    < 1 shrinks every row count (for quick checks); 1.0 is the real block."""
+    weights = []
+    for i, (name, shape, role) in enumerate(BLOCK_14B):
+        if scale != 1.0:
+            shape = (max(1, int(round(shape[0] * scale))),) + tuple(shape[1:])
+        if role == "norm":
+            w = bf16_normal(shape, seed * 100 + i, 0.05, center=1.0)
+        else:
+            w = bf16_normal(shape, seed * 100 + i, 0.02)
+        weights.append((name, w, role))
+    layers: dict[str, CompressedLayer] = {}
+    for role in dict.fromkeys(r for _, _, r in weights):
+        group = [(name, w) for name, w, r in weights if r == role]
+        for (name, _), layer in zip(group, compress_group([w for _, w in group],
+                                                          chunk_size=chunk_size)):
+            layers[name] = layer
+    return [(name, w, layers[name]) for name, w, _ in weights]
+

@@ -1,13 +1,16 @@
 """Decode throughput of the gfx950 BF16 weight decoder on one MI355X.
 
-Workload: one 5120x17408 bf16 weight (N(0, 0.02) with 0.1% N(0, 0.5)
-outliers, seed 2), compressed with a per-tensor canonical-Huffman exponent
-codebook in chunks of 65536 symbols (1360 chunks). Its compressed form
-(bitstreams, chunk offsets/lengths, sign/mantissa bytes, decode table) is
-resident in HBM before timing starts. One step = one kernel launch that
-rebuilds the whole bf16 tensor in HBM. Prints one JSON line.
+Default workload (the headline): one 5120x17408 bf16 weight (N(0, 0.02) with
+0.1% N(0, 0.5) outliers, seed 2), compressed with a per-tensor
+canonical-Huffman exponent codebook in chunks of 65536 symbols (1360 chunks).
+Its compressed form (bitstreams, chunk offsets/lengths, sign/mantissa bytes,
+decode table) is resident in HBM before timing starts. One step = one kernel
+launch that rebuilds the whole bf16 tensor in HBM. --workload block does the
+same for a whole 14B-class decoder block (9 tensors, one codebook per role)
+in one launch. Prints one JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload layer|block]
+                    [--no-cpu-baseline]
 """
 from __future__ import annotations
 
@@ -32,33 +35,43 @@ def _log(msg: str) -> None:
     print("[bench] " + msg, file=sys.stderr, flush=True)
 
 
-def _cpu_baseline(layer, max_threads: int) -> dict:
+def _cpu_baseline(layers, max_threads: int, what: str) -> dict:
     """The reference's CPU decode path (chunk decode + recombine), restated in
     C/OpenMP in oracle/, timed on this host's cores on a bounded sample."""
     import oracle
 
     oracle.build()
     threads = max(1, min(max_threads, oracle.max_threads()))
-    sm = layer.sign_mantissa.numpy()
-    enc = layer.encoded
-    # Sample: the whole tensor, repeated until ~10 s of work at `threads`.
-    res = oracle.time_cpu_decode(enc, sm, threads, min_seconds=10.0, max_reps=40)
-    n = enc.n_symbols
-    # One thread on a 40-chunk slice of the same tensor (reported as context).
+    total_s = 0.0
+    reps = []
+    n = 0
+    # Sample: every tensor of the workload, each repeated until ~10 s of work
+    # in all at `threads`.
+    per_tensor = 10.0 / len(layers)
+    for layer in layers:
+        res = oracle.time_cpu_decode(layer.encoded, layer.sign_mantissa.numpy(), threads,
+                                     min_seconds=per_tensor, max_reps=40)
+        total_s += res["median_s"]
+        reps.append(res["reps"])
+        n += layer.encoded.n_symbols
+    # One thread on a 40-chunk slice of the largest tensor (reported as context).
     from afterimage_amd.runtime.compressed_store import _slice_encoded
 
-    sub = _slice_encoded(enc, 0, 40)
-    one = oracle.time_cpu_decode(sub, sm[: sub.n_symbols], 1, min_seconds=2.0, max_reps=5)
+    big = max(layers, key=lambda l: l.encoded.n_symbols)
+    sub = _slice_encoded(big.encoded, 0, min(40, big.encoded.n_chunks))
+    one = oracle.time_cpu_decode(sub, big.sign_mantissa.numpy()[: sub.n_symbols], 1,
+                                 min_seconds=2.0, max_reps=5)
     return {
-        "value": round(2 * n / res["median_s"] / 1e9, 3),
+        "value": round(2 * n / total_s / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": "whole 5120x17408 tensor x%d reps, chunk decode + recombine, median rep"
-                  % res["reps"],
-        "exponent_bytes_gbs": round(n / res["median_s"] / 1e9, 3),
+        "sample": "%s: each tensor decoded whole (chunk decode + recombine), %s reps, "
+                  "median rep per tensor" % (what, "/".join(str(r) for r in reps)),
+        "exponent_bytes_gbs": round(n / total_s / 1e9, 3),
         "one_thread_gbs": round(2 * sub.n_symbols / one["median_s"] / 1e9, 3),
-        "one_thread_sample": "chunks 0..39 of the same tensor (2.6M symbols)",
+        "one_thread_sample": "first %d chunks of the largest tensor (%d symbols)"
+                             % (sub.n_chunks, sub.n_symbols),
     }
 
 
@@ -100,6 +113,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", choices=["layer", "block"], default="layer",
+                    help="layer: one 5120x17408 weight (the headline); block: a whole "
+                         "14B-class decoder block in one launch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -124,32 +140,50 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    seed = 2
     t0 = time.perf_counter()
-    W, layer = workloads.single_layer(seed=seed)
-    enc = layer.encoded
-    _log("workload built in %.1fs: %d chunks, packed %.2f MB"
-         % (time.perf_counter() - t0, enc.n_chunks, enc.packed.nbytes / 1e6))
-    dt = DeviceTensor.from_encoded(enc, layer.sign_mantissa, dev)
-    n = enc.n_symbols
-    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
-    desc = (_native.AimgTensor * 1)()
-    desc[0] = _descriptor(dt, out, n)
+    if args.workload == "layer":
+        seed = 2
+        W, layer = workloads.single_layer(seed=seed)
+        items = [("layer", W, layer)]
+        config_key = "5120x17408/seed%d/chunk65536/outliers1e-3" % seed
+        description = ("bf16 5120x17408 weight decode, N(0,0.02) + 0.1% N(0,0.5) outliers "
+                       "(seed 2), per-tensor Huffman exponent codebook, 65536-symbol chunks "
+                       "(1360), inputs resident in HBM, one launch per step")
+    else:
+        seed = 3
+        items = workloads.block_14b(seed=seed)
+        config_key = "block14b/seed%d/chunk65536/per-role" % seed
+        description = ("bf16 14B-class decoder block (q,o 5120x5120; k,v 1024x5120; gate,up "
+                       "17408x5120; down 5120x17408; 2 RMSNorm 5120), N(0,0.02) weights, "
+                       "norms N(1,0.05) (seed 3), one exponent codebook per role, "
+                       "65536-symbol chunks (5042), inputs resident in HBM, all 9 tensors "
+                       "in one launch per step")
+    layers = [layer for _, _, layer in items]
+    _log("workload built in %.1fs: %d tensors, %d chunks, packed %.2f MB"
+         % (time.perf_counter() - t0, len(items), sum(l.encoded.n_chunks for l in layers),
+            sum(l.encoded.packed.nbytes for l in layers) / 1e6))
+    dts = [DeviceTensor.from_encoded(l.encoded, l.sign_mantissa, dev) for l in layers]
+    outs = [torch.empty(l.encoded.n_symbols, dtype=torch.bfloat16, device=dev) for l in layers]
+    desc = (_native.AimgTensor * len(dts))()
+    for j, (dt, o) in enumerate(zip(dts, outs)):
+        desc[j] = _descriptor(dt, o, o.numel())
     lib = _native.lib()
     stream = torch.cuda.current_stream(dev)
     handle = ctypes.c_void_p(stream.cuda_stream)
     decode = lib.aimg_decode_bf16
+    n_desc = len(dts)
 
     def step():
-        rc = decode(desc, 1, handle)
+        rc = decode(desc, n_desc, handle)
         if rc:
             _native.check(rc)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize(dev)
-    # Bit-exactness of the benchmarked output (outside the timed region).
-    ok = torch.equal(out.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
+    # Bit-exactness of the benchmarked outputs (outside the timed region).
+    ok = all(torch.equal(o.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
+             for (_, W, _), o in zip(items, outs))
     if not ok:
         print("decoded output differs from the original weights", file=sys.stderr)
         return 1
@@ -169,12 +203,14 @@ def main() -> int:
     _log("timed %d steps: wall %.3f ms/step, events %.1f us/launch"
          % (args.steps, wall * 1e3 / args.steps, kernel_s * 1e6))
 
-    chunk_bytes = int(enc.chunk_nbytes.astype(np.int64).sum())
-    # bitstreams + offsets and lengths + sign/mantissa + window table + bf16 write
-    algo_bytes = chunk_bytes + 8 * enc.n_chunks + n + 6 * 4096 + 2 * n
+    n = sum(l.encoded.n_symbols for l in layers)
+    n_chunks = sum(l.encoded.n_chunks for l in layers)
+    chunk_bytes = sum(int(l.encoded.chunk_nbytes.astype(np.int64).sum()) for l in layers)
+    n_tables = len({dt.tables.key for dt in dts})
+    # bitstreams + offsets and lengths + sign/mantissa + window tables + bf16 write
+    algo_bytes = chunk_bytes + 8 * n_chunks + n + 6 * 4096 * n_tables + 2 * n
     achieved = algo_bytes / kernel_s / 1e9
     value = 2 * n * args.steps / wall / 1e9
-    config_key = "5120x17408/seed%d/chunk65536/outliers1e-3" % seed
     traffic = _traffic(config_key)
     rec = {
         "metric": METRIC,
@@ -190,11 +226,12 @@ def main() -> int:
         "dtype": "u8",
         "data": "synthetic",
         "config": {
-            "workload": "bf16 5120x17408 weight decode, N(0,0.02) + 0.1% N(0,0.5) outliers "
-                        "(seed 2), per-tensor Huffman exponent codebook, 65536-symbol "
-                        "chunks (1360), inputs resident in HBM, one launch per step",
+            "workload": description,
             "config_key": config_key,
+            "n_tensors": len(items),
             "n_weights": n,
+            "n_chunks": n_chunks,
+            "decode_tables": n_tables,
             "packed_exponent_bytes": chunk_bytes,
             "bits_per_exponent": round(8 * chunk_bytes / n, 4),
             "bit_exact": ok,
@@ -213,7 +250,8 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         _log("timing the CPU baseline (~15 s)")
-        rec["cpu_baseline"] = _cpu_baseline(layer, args.cpu_threads)
+        rec["cpu_baseline"] = _cpu_baseline(layers, args.cpu_threads,
+                                            "the whole " + args.workload)
     print(json.dumps(rec), flush=True)
     return 0
 

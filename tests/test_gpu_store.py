@@ -213,3 +213,23 @@ def test_single_layer_5120x17408_chunk65536():
     exps = oracle.decode_chunks(layer.encoded, 0, 8, n_threads=4)
     sm = layer.sign_mantissa.numpy()[: exps.size]
     assert np.array_equal(_bits(out).numpy()[: exps.size].view(np.uint16), oracle.recombine(exps, sm))
+
+
+@pytest.fixture(scope="module")
+def block14b():
+    return workloads.block_14b()
+
+
+def test_block_14b_decodes_in_one_launch_with_shared_tables(block14b):
+    """The full 14B-class block (330M weights, 9 tensors) in one decode call:
+    same-role tensors share one device table; every tensor bit-exact."""
+    dts = [DeviceTensor.from_encoded(l.encoded, l.sign_mantissa, "cuda") for _, _, l in block14b]
+    assert len(dts) <= devmod.MAX_TENSORS  # decode_bf16 issues a single launch
+    tables = {}
+    for dt, (_, _, role) in zip(dts, workloads.BLOCK_14B):
+        tables.setdefault(role, set()).add(dt.tables.blob.data_ptr())
+    assert len(tables) == 5 and all(len(v) == 1 for v in tables.values())
+    outs = decode_bf16(dts)
+    for (name, w, _), o in zip(block14b, outs):
+        assert torch.equal(_bits(o), _bits(w).reshape(-1)), name
+
