@@ -95,10 +95,27 @@ struct DevTensor {
     uint32_t packed_n32;  // packed_nbytes, capped at 2^32 - 1 (buffer loads)
 };
 
+// What a launch makes of the decoded exponents.
+enum Mode : int {
+    kModeU8 = 0,    // the exponent bytes themselves
+    kModeBf16 = 1,  // bf16 weights
+    kModeGemv = 2,  // y += W x with W decoded on the fly and never written
+};
+constexpr int kGemvMaxBatch = 4;
+
+struct GemvArgs {
+    const uint16_t* x;  // bf16 [batch][cols]
+    float* y;           // fp32 [batch][rows], accumulated
+    uint32_t rows;
+    uint32_t cols;
+    int32_t batch;
+};
+
 struct LaunchArgs {
     DevTensor t[AIMG_MAX_TENSORS];
     int64_t total_items;
     int32_t n_tensors;
+    GemvArgs gemv;  // kModeGemv only (one tensor)
 };
 
 // Read-only launch data that every thread of a workgroup reads at the same
@@ -534,28 +551,41 @@ __device__ __forceinline__ uint16_t bf16_one(uint32_t sm, uint32_t e) {
     return static_cast<uint16_t>(((sm & 0x80u) << 8) | (e << 7) | (sm & 0x7Fu));
 }
 
-template <bool kBf16>
-__device__ __forceinline__ void store_one(const DevTensor& T, int64_t el, uint32_t e) {
-    if (kBf16) {
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+// Output element el from its exponent e.
+template <int kMode>
+__device__ __forceinline__ void store_one(const DevTensor& T, const GemvArgs& G, int64_t el,
+                                          uint32_t e) {
+    if (kMode == kModeU8) {
+        static_cast<uint8_t*>(T.out)[el] = static_cast<uint8_t>(e);
+    } else if (kMode == kModeBf16) {
         static_cast<uint16_t*>(T.out)[el] = bf16_one(T.sm[el], e);
     } else {
-        static_cast<uint8_t*>(T.out)[el] = static_cast<uint8_t>(e);
+        const float w = bf16_to_f32(bf16_one(T.sm[el], e));
+        const uint32_t row = static_cast<uint32_t>(el / G.cols);
+        const uint32_t col = static_cast<uint32_t>(el - static_cast<int64_t>(row) * G.cols);
+        for (int b = 0; b < G.batch; ++b)
+            atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + row,
+                      w * bf16_to_f32(G.x[static_cast<int64_t>(b) * G.cols + col]));
     }
 }
 
 // Sign/mantissa bytes of the vector groups a thread stores in one round
 // (groups k * tpc + i of the round), requested ahead of use.
-template <bool kBf16>
+template <int kMode>
 struct SmBatch {
-    uint2 v[kBf16 ? kStoreBatch : 1];
+    uint2 v[kMode != kModeU8 ? kStoreBatch : 1];
 };
 
 // Buffer loads (zero past the tensor's last byte), so the batch needs no
 // clamping and is issued back to back; the batch offset is a scalar.
-template <bool kBf16, int kGroup>
-__device__ __forceinline__ void sm_issue(SmBatch<kBf16>& B, const DevTensor& T, int64_t a0,
+template <int kMode, int kGroup>
+__device__ __forceinline__ void sm_issue(SmBatch<kMode>& B, const DevTensor& T, int64_t a0,
                                          uint32_t i, uint32_t tpc) {
-    if (!kBf16 || kGroup == 1) return;
+    if (kMode == kModeU8 || kGroup == 1) return;
     const __amdgpu_buffer_rsrc_t rs = buffer_of(T.sm, static_cast<uint32_t>(T.n_symbols));
     const uint32_t v0 = static_cast<uint32_t>(a0) + i * kGroup;
 #pragma unroll
@@ -565,17 +595,38 @@ __device__ __forceinline__ void sm_issue(SmBatch<kBf16>& B, const DevTensor& T, 
     }
 }
 
+// Sum of v over the wave (every lane active).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+// Add the wave's per-row sums in acc to y[b][row] (one atomic per batch row,
+// from lane 0) and clear them.
+__device__ __forceinline__ void gemv_flush(const GemvArgs& G, float (&acc)[kGemvMaxBatch],
+                                           uint32_t row) {
+#pragma unroll
+    for (int b = 0; b < kGemvMaxBatch; ++b) {
+        if (b >= G.batch) break;
+        const float s = wave_sum(acc[b]);
+        if ((threadIdx.x & 63) == 0 && s != 0.0f)
+            atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + row, s);
+        acc[b] = 0.0f;
+    }
+}
+
 // Vector groups [0, nfull) of the staged round to output elements a0...;
 // thread i of a sub-group of tpc takes groups i, i + tpc, ...
-template <bool kBf16, int kGroup>
-__device__ __forceinline__ void store_round(const SmBatch<kBf16>& B, const DevTensor& T,
-                                            const uint8_t* stage, int64_t a0, uint32_t nfull,
-                                            uint32_t i, uint32_t tpc) {
+template <int kMode, int kGroup>
+__device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTensor& T,
+                                            const GemvArgs& G, const uint8_t* stage, int64_t a0,
+                                            uint32_t nfull, uint32_t i, uint32_t tpc) {
     if (kGroup == 1) {
-        for (uint32_t v = i; v < nfull; v += tpc) store_one<kBf16>(T, a0 + v, stage[v]);
+        for (uint32_t v = i; v < nfull; v += tpc) store_one<kMode>(T, G, a0 + v, stage[v]);
         return;
     }
-    if (!kBf16) {
+    if (kMode == kModeU8) {
         for (uint32_t v = i; v < nfull; v += tpc)
             *reinterpret_cast<uint4*>(static_cast<uint8_t*>(T.out) + a0 + static_cast<int64_t>(v) * kGroup) =
                 *reinterpret_cast<const uint4*>(stage + v * kGroup);
@@ -594,18 +645,81 @@ __device__ __forceinline__ void store_round(const SmBatch<kBf16>& B, const DevTe
         const uint32_t v = k * tpc + i;
         ev[k] = *reinterpret_cast<const uint2*>(stage + (v < nfull ? v : 0u) * kGroup);
     }
-    uint4* dst = reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.out) + a0);
+    if (kMode == kModeBf16) {
+        uint4* dst = reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.out) + a0);
+#pragma unroll
+        for (uint32_t k = 0; k < kStoreBatch; ++k) {
+            const uint32_t v = k * tpc + i;
+            if (v >= nfull) continue;
+            uint4 o4;
+            o4.x = bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].x, ev[k].x);
+            o4.y = bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].x, ev[k].x);
+            o4.z = bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].y, ev[k].y);
+            o4.w = bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].y, ev[k].y);
+            dst[v] = o4;
+        }
+        return;
+    }
+    // Fused GEMV: each group's 8 weights (one matrix row, as cols % 8 == 0)
+    // are multiplied by x in registers. A wave's groups at one k usually lie
+    // in one row: their products are summed per lane and reduced over the
+    // wave when the row changes; a wave that straddles a row boundary adds
+    // that group's products with per-lane atomics.
+    const uint32_t cols = G.cols;
+    uint32_t el = static_cast<uint32_t>(a0) + i * kGroup;  // element of group k = 0
+    uint32_t row = el / cols;
+    uint32_t col = el - row * cols;
+    const uint32_t step = tpc * kGroup;
+    float acc[kGemvMaxBatch] = {0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t acc_row = 0xFFFFFFFFu;
 #pragma unroll
     for (uint32_t k = 0; k < kStoreBatch; ++k) {
+        if (k > 0) {
+            col += step;
+            while (col >= cols) {
+                col -= cols;
+                ++row;
+            }
+        }
         const uint32_t v = k * tpc + i;
-        if (v >= nfull) continue;
-        uint4 o4;
-        o4.x = bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].x, ev[k].x);
-        o4.y = bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].x, ev[k].x);
-        o4.z = bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].y, ev[k].y);
-        o4.w = bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].y, ev[k].y);
-        dst[v] = o4;
+        const bool live = v < nfull;
+        float p[kGemvMaxBatch] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (live) {
+            const uint32_t o[4] = {bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].x, ev[k].x),
+                                   bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].x, ev[k].x),
+                                   bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].y, ev[k].y),
+                                   bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].y, ev[k].y)};
+#pragma unroll
+            for (int b = 0; b < kGemvMaxBatch; ++b) {
+                if (b >= G.batch) break;
+                const uint4 xv = *reinterpret_cast<const uint4*>(
+                    G.x + static_cast<int64_t>(b) * cols + col);
+                const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+                float s = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    s += __uint_as_float(o[q] << 16) * __uint_as_float(xw[q] << 16);
+                    s += __uint_as_float(o[q] & 0xFFFF0000u) * __uint_as_float(xw[q] & 0xFFFF0000u);
+                }
+                p[b] = s;
+            }
+        }
+        const uint64_t lm = __builtin_amdgcn_ballot_w64(live);
+        if (lm == 0) continue;
+        const uint32_t r0 = __builtin_amdgcn_readlane(row, __builtin_ctzll(lm));
+        if (__builtin_amdgcn_ballot_w64(live && row != r0) == 0) {
+            if (r0 != acc_row) {
+                if (acc_row != 0xFFFFFFFFu) gemv_flush(G, acc, acc_row);
+                acc_row = r0;
+            }
+#pragma unroll
+            for (int b = 0; b < kGemvMaxBatch; ++b) acc[b] += p[b];
+        } else if (live) {
+            for (int b = 0; b < G.batch; ++b)
+                atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + row, p[b]);
+        }
     }
+    if (acc_row != 0xFFFFFFFFu) gemv_flush(G, acc, acc_row);
 }
 
 // Window table and the first kLdsEscBlocks escape blocks of a table blob to LDS.
@@ -623,7 +737,7 @@ __device__ __forceinline__ void load_table(const uint8_t* table, uint32_t tid, u
     for (uint32_t j = tid; j < n_esc * kEscBlockEntries; j += kThreads) s_esc[j] = gesc[j];
 }
 
-template <bool kBf16, int kGroup, bool kTiny>
+template <int kMode, int kGroup, bool kTiny>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const LaunchArgs args) {
     __shared__ uint32_t s_wsyms[kWinEntries];
     __shared__ uint16_t s_wmeta[kWinEntries];
@@ -701,8 +815,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             // Sign/mantissa bytes of every group this round can fill (its
             // output starts at a known element; its length is known only
             // after decoding), requested now so the store never waits.
-            SmBatch<kBf16> smb;
-            sm_issue<kBf16, kGroup>(smb, T, chunk_base + ob - lead, i, tpc);
+            SmBatch<kMode> smb;
+            sm_issue<kMode, kGroup>(smb, T, chunk_base + ob - lead, i, tpc);
             const uint32_t RB = round_len(cur, r);
             const bool g_active = RB != 0;
 
@@ -785,7 +899,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
             __syncthreads();
 
-            store_round<kBf16, kGroup>(smb, T, stage, a0, nfull, i, tpc);
+            store_round<kMode, kGroup>(smb, T, args.gemv, stage, a0, nfull, i, tpc);
             ob += want;
             // The partial vector group moves to the front for the next round.
             const uint32_t rem = avail - nfull * kGroup;
@@ -807,7 +921,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         const int64_t n_tail = lim - (ob - lead);
         for (int64_t k = i_item; k < n_tail; k += tpc) {
             const uint32_t ex = k < lead ? stage[k] : tb.sym0;
-            store_one<kBf16>(T, t0 + k, ex);
+            store_one<kMode>(T, args.gemv, t0 + k, ex);
         }
         cur = nxt;
     }
@@ -842,7 +956,7 @@ struct Batch {
     bool vec = true;
 };
 
-template <bool kBf16>
+template <int kMode>
 int launch_batch(Batch& B, hipStream_t s, bool tiny) {
     B.args.n_tensors = B.m;
     B.args.total_items = B.items;
@@ -850,12 +964,13 @@ int launch_batch(Batch& B, hipStream_t s, bool tiny) {
     const int64_t slots = static_cast<int64_t>(cu_count()) * kBlocksPerCu;
     const int64_t grid = B.items < slots ? B.items : slots;
     const dim3 gdim(static_cast<uint32_t>(grid)), bdim(kThreads);
+    constexpr int kVecGroup = kMode == kModeU8 ? 16 : 8;
     if (tiny) {
-        hipLaunchKernelGGL((decode_kernel<kBf16, 1, true>), gdim, bdim, 0, s, B.args);
+        hipLaunchKernelGGL((decode_kernel<kMode, 1, true>), gdim, bdim, 0, s, B.args);
     } else if (B.vec) {
-        hipLaunchKernelGGL((decode_kernel<kBf16, kBf16 ? 8 : 16, false>), gdim, bdim, 0, s, B.args);
+        hipLaunchKernelGGL((decode_kernel<kMode, kVecGroup, false>), gdim, bdim, 0, s, B.args);
     } else {
-        hipLaunchKernelGGL((decode_kernel<kBf16, 1, false>), gdim, bdim, 0, s, B.args);
+        hipLaunchKernelGGL((decode_kernel<kMode, 1, false>), gdim, bdim, 0, s, B.args);
     }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess)
@@ -863,66 +978,99 @@ int launch_batch(Batch& B, hipStream_t s, bool tiny) {
     return AIMG_OK;
 }
 
-template <bool kBf16>
-int launch(const aimg_tensor* ts, int n, void* stream) {
+// Validate tensor i and add it to the normal or the tiny-buffer batch.
+template <int kMode>
+int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny) {
+    const std::string who = "tensor " + std::to_string(i) + ": ";
+    if (t.chunk_size < 1) return fail(AIMG_ERR_INVALID_ARGUMENT, who + "chunk_size must be >= 1");
+    if (t.n_chunks < 0 || t.n_symbols < 0 || t.packed_nbytes < 0)
+        return fail(AIMG_ERR_INVALID_ARGUMENT, who + "negative size");
+    if (t.n_symbols > static_cast<int64_t>(t.n_chunks) * t.chunk_size)
+        return fail(AIMG_ERR_INVALID_ARGUMENT, who + "n_symbols exceeds n_chunks * chunk_size");
+    if (t.n_symbols == 0) return AIMG_OK;
+    if (t.n_symbols > INT32_MAX)
+        return fail(AIMG_ERR_UNSUPPORTED, who + "more than 2^31 - 1 symbols");
+    const bool need_sm = kMode != kModeU8;
+    const bool need_out = kMode != kModeGemv;
+    if (t.packed == nullptr || t.chunk_offsets == nullptr || t.chunk_nbytes == nullptr ||
+        (need_out && t.out == nullptr) || t.table == nullptr ||
+        (need_sm && t.sign_mantissa == nullptr))
+        return fail(AIMG_ERR_INVALID_ARGUMENT, who + "null device pointer");
+    if (reinterpret_cast<uintptr_t>(t.table) % 16 != 0)
+        return fail(AIMG_ERR_INVALID_ARGUMENT, who + "table must be 16-byte aligned");
+    Batch& B = t.packed_nbytes < 4 ? tiny : normal;
+    const int group = kMode == kModeU8 ? 16 : 8;
+    if ((need_out && reinterpret_cast<uintptr_t>(t.out) % 16 != 0) || t.chunk_size % group != 0 ||
+        (need_sm && reinterpret_cast<uintptr_t>(t.sign_mantissa) % 8 != 0))
+        B.vec = false;
+    DevTensor& dt = B.args.t[B.m++];
+    dt.packed = t.packed;
+    dt.offsets = t.chunk_offsets;
+    dt.nbytes = t.chunk_nbytes;
+    dt.sm = t.sign_mantissa;
+    dt.out = t.out;
+    dt.table = static_cast<const uint8_t*>(t.table);
+    dt.packed_nbytes = t.packed_nbytes;
+    dt.packed_n32 = t.packed_nbytes > static_cast<int64_t>(UINT32_MAX)
+                        ? UINT32_MAX : static_cast<uint32_t>(t.packed_nbytes);
+    dt.n_symbols = t.n_symbols;
+    dt.chunk_size = t.chunk_size;
+    dt.tpc = static_cast<int32_t>(threads_per_chunk(t.chunk_size));
+    // Chunks past the last output element hold nothing to write.
+    dt.n_jobs = (t.n_symbols + t.chunk_size - 1) / t.chunk_size;
+    dt.item_begin = B.items;
+    const int64_t per_item = kThreads / dt.tpc;
+    B.items += (dt.n_jobs + per_item - 1) / per_item;
+    return AIMG_OK;
+}
+
+// vec_ok false selects the element-wise kernel whatever the tensors' layout.
+template <int kMode>
+int launch(const aimg_tensor* ts, int n, const GemvArgs& gemv, bool vec_ok, void* stream) {
     if (ts == nullptr && n > 0) return fail(AIMG_ERR_INVALID_ARGUMENT, "tensors is null");
     if (n < 0 || n > AIMG_MAX_TENSORS)
         return fail(AIMG_ERR_INVALID_ARGUMENT,
                     "n_tensors must be in 0.." + std::to_string(AIMG_MAX_TENSORS));
     Batch normal, tiny;
-    const int group = kBf16 ? 8 : 16;
+    normal.args.gemv = gemv;
+    tiny.args.gemv = gemv;
+    normal.vec = vec_ok;
     for (int i = 0; i < n; ++i) {
-        const aimg_tensor& t = ts[i];
-        const std::string who = "tensor " + std::to_string(i) + ": ";
-        if (t.chunk_size < 1) return fail(AIMG_ERR_INVALID_ARGUMENT, who + "chunk_size must be >= 1");
-        if (t.n_chunks < 0 || t.n_symbols < 0 || t.packed_nbytes < 0)
-            return fail(AIMG_ERR_INVALID_ARGUMENT, who + "negative size");
-        if (t.n_symbols > static_cast<int64_t>(t.n_chunks) * t.chunk_size)
-            return fail(AIMG_ERR_INVALID_ARGUMENT, who + "n_symbols exceeds n_chunks * chunk_size");
-        if (t.n_symbols == 0) continue;
-        if (t.n_symbols > INT32_MAX)
-            return fail(AIMG_ERR_UNSUPPORTED, who + "more than 2^31 - 1 symbols");
-        if (t.packed == nullptr || t.chunk_offsets == nullptr || t.chunk_nbytes == nullptr ||
-            t.out == nullptr || t.table == nullptr || (kBf16 && t.sign_mantissa == nullptr))
-            return fail(AIMG_ERR_INVALID_ARGUMENT, who + "null device pointer");
-        if (reinterpret_cast<uintptr_t>(t.table) % 16 != 0)
-            return fail(AIMG_ERR_INVALID_ARGUMENT, who + "table must be 16-byte aligned");
-        Batch& B = t.packed_nbytes < 4 ? tiny : normal;
-        if (reinterpret_cast<uintptr_t>(t.out) % 16 != 0 || t.chunk_size % group != 0 ||
-            (kBf16 && reinterpret_cast<uintptr_t>(t.sign_mantissa) % 8 != 0))
-            B.vec = false;
-        DevTensor& dt = B.args.t[B.m++];
-        dt.packed = t.packed;
-        dt.offsets = t.chunk_offsets;
-        dt.nbytes = t.chunk_nbytes;
-        dt.sm = t.sign_mantissa;
-        dt.out = t.out;
-        dt.table = static_cast<const uint8_t*>(t.table);
-        dt.packed_nbytes = t.packed_nbytes;
-        dt.packed_n32 = t.packed_nbytes > static_cast<int64_t>(UINT32_MAX)
-                            ? UINT32_MAX : static_cast<uint32_t>(t.packed_nbytes);
-        dt.n_symbols = t.n_symbols;
-        dt.chunk_size = t.chunk_size;
-        dt.tpc = static_cast<int32_t>(threads_per_chunk(t.chunk_size));
-        // Chunks past the last output element hold nothing to write.
-        dt.n_jobs = (t.n_symbols + t.chunk_size - 1) / t.chunk_size;
-        dt.item_begin = B.items;
-        const int64_t per_item = kThreads / dt.tpc;
-        B.items += (dt.n_jobs + per_item - 1) / per_item;
+        const int rc = add_tensor<kMode>(ts[i], i, normal, tiny);
+        if (rc != AIMG_OK) return rc;
     }
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const int rc = launch_batch<kBf16>(normal, s, false);
+    const int rc = launch_batch<kMode>(normal, s, false);
     if (rc != AIMG_OK) return rc;
-    return launch_batch<kBf16>(tiny, s, true);
+    return launch_batch<kMode>(tiny, s, true);
 }
 
 }  // namespace
 }  // namespace aimg
 
 extern "C" int aimg_decode_bf16(const aimg_tensor* tensors, int n_tensors, void* stream) {
-    return aimg::launch<true>(tensors, n_tensors, stream);
+    return aimg::launch<aimg::kModeBf16>(tensors, n_tensors, aimg::GemvArgs{}, true, stream);
 }
 
 extern "C" int aimg_decode_u8(const aimg_tensor* tensors, int n_tensors, void* stream) {
-    return aimg::launch<false>(tensors, n_tensors, stream);
+    return aimg::launch<aimg::kModeU8>(tensors, n_tensors, aimg::GemvArgs{}, true, stream);
+}
+
+extern "C" int aimg_decode_gemv_bf16(const aimg_tensor* t, int64_t rows, int64_t cols,
+                                     const void* x, int batch, float* y, void* stream) {
+    using aimg::fail;
+    if (t == nullptr) return fail(AIMG_ERR_INVALID_ARGUMENT, "tensor is null");
+    if (rows < 1 || cols < 1 || rows > INT32_MAX || cols > INT32_MAX ||
+        rows * cols != t->n_symbols)
+        return fail(AIMG_ERR_INVALID_ARGUMENT, "rows * cols must equal n_symbols (both >= 1)");
+    if (batch < 1 || batch > aimg::kGemvMaxBatch)
+        return fail(AIMG_ERR_INVALID_ARGUMENT,
+                    "batch must be in 1.." + std::to_string(aimg::kGemvMaxBatch));
+    if (x == nullptr || y == nullptr) return fail(AIMG_ERR_INVALID_ARGUMENT, "null x or y");
+    const aimg::GemvArgs g{static_cast<const uint16_t*>(x), y, static_cast<uint32_t>(rows),
+                           static_cast<uint32_t>(cols), batch};
+    // The 8-weight groups take 16-byte x loads: they must lie inside one row
+    // (cols % 8 == 0) and x must be 16-byte aligned.
+    const bool vec_ok = cols % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    return aimg::launch<aimg::kModeGemv>(t, 1, g, vec_ok, stream);
 }

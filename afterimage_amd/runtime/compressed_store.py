@@ -15,7 +15,7 @@ import dataclasses
 import numpy as np
 import torch
 
-from .device import DeviceTensor, decode_bf16
+from .device import DeviceTensor, decode_bf16, decode_gemv
 from .huffman_chunked import ChunkedEncoded, encode_chunked, lengths_from_counts, symbol_counts
 
 EXPONENT_SHIFT = 7
@@ -224,3 +224,26 @@ def decompress_rows_gpu(layer: CompressedLayer, row_start: int, row_end: int,
     flat = torch.empty(avail, dtype=torch.bfloat16, device=dev)
     _decode_range_into(layer, c0, c1, flat, avail, dev, _tables_for(enc, dev))
     return flat[e0 - base:e1 - base].reshape(row_end - row_start, cols)
+
+
+def decompress_matvec_gpu(layer: CompressedLayer, x: torch.Tensor,
+                          device: str | torch.device = "cuda") -> torch.Tensor:
+    """x @ W.T for the layer's 2-D bf16 weight W [rows, cols] without
+    materialising W: the exponents are decoded and multiplied in one kernel
+    (fp32 accumulation, bf16 result). x: [cols] or [b, cols] with b <= 4
+    (a speculative-verify width), any float dtype; it is rounded to bf16.
+    Returns [b, rows] (or [rows] for a 1-D x) in bf16. The reference forms
+    the same product as decompress_rows_gpu (compressed_store.py:254-303)
+    followed by a matmul (streaming_engine.py:2271-2335)."""
+    dev = _gpu_device(device)
+    if len(layer.shape) != 2:
+        raise ValueError("decompress_matvec_gpu needs a 2-D layer, got shape %s" % (layer.shape,))
+    rows, cols = (int(v) for v in layer.shape)
+    squeeze = x.dim() == 1
+    xb = x.reshape(1, -1) if squeeze else x
+    xb = xb.to(device=dev, dtype=torch.bfloat16).contiguous()
+    t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, dev,
+                                  tables=_tables_for(layer.encoded, dev))
+    y = decode_gemv(t, xb, rows, cols).to(torch.bfloat16)
+    return y.reshape(rows) if squeeze else y
+

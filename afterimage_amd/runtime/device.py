@@ -234,3 +234,40 @@ def decode_u8(tensors: list[DeviceTensor], n_out: list[int] | None = None,
         with torch.cuda.device(gouts[0].device):
             _native.check(lib.aimg_decode_u8(arr, len(group), _stream_handle(gouts[0].device)))
     return outs
+
+
+GEMV_MAX_BATCH = 4
+
+
+def decode_gemv(t: DeviceTensor, x: torch.Tensor, rows: int, cols: int,
+                y: torch.Tensor | None = None) -> torch.Tensor:
+    """y += x @ W.T in fp32 for the rows x cols bf16 matrix W held by ``t``,
+    decoded inside the kernel and never written. x: bf16 [b, cols] on the
+    GPU (b <= GEMV_MAX_BATCH); y: fp32 [b, rows], zeros when not given.
+    Returns y. The fp32 sums are added with atomics, so their order (and
+    the last bits of y) can vary between calls."""
+    dev = x.device
+    if dev.type != "cuda":
+        raise RuntimeError("the decoder runs on the GPU only; got x on %s" % dev)
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or x.shape[1] != cols or not x.is_contiguous():
+        raise ValueError("x must be a contiguous bf16 [batch, %d] tensor" % cols)
+    b = int(x.shape[0])
+    if not 1 <= b <= GEMV_MAX_BATCH:
+        raise ValueError("batch must be in 1..%d, got %d" % (GEMV_MAX_BATCH, b))
+    if rows * cols != t.n_symbols:
+        raise ValueError("rows * cols = %d, the tensor has %d weights" % (rows * cols, t.n_symbols))
+    if y is None:
+        y = torch.zeros((b, rows), dtype=torch.float32, device=dev)
+    elif y.dtype != torch.float32 or tuple(y.shape) != (b, rows) or not y.is_contiguous():
+        raise ValueError("y must be a contiguous fp32 [%d, %d] tensor" % (b, rows))
+    if t.sign_mantissa is None or t.sign_mantissa.device != dev:
+        raise ValueError("the tensor needs sign_mantissa bytes on %s" % dev)
+    _check_device(t, y)
+    d = (_native.AimgTensor * 1)()
+    d[0] = _descriptor(t, y, t.n_symbols)
+    d[0].out = None
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().aimg_decode_gemv_bf16(
+            d, rows, cols, x.data_ptr(), b, y.data_ptr(), _stream_handle(dev)))
+    return y
+

@@ -108,14 +108,92 @@ def _copy_calibration(mib: int, steps: int, warmup: int) -> int:
     return 0
 
 
+def _bench_gemv(args) -> int:
+    """Fused decode->GEMV: y[b] = W x[b] for the 5120x17408 weight, W decoded
+    in the kernel and never written. One step = zero y + one launch."""
+    from afterimage_amd import workloads
+    from afterimage_amd.runtime.device import DeviceTensor, decode_gemv
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    W, layer = workloads.single_layer(seed=2)
+    rows, cols = W.shape
+    b = args.batch
+    g = np.random.default_rng(23)
+    x = torch.from_numpy(g.standard_normal((b, cols), dtype=np.float32)).to(torch.bfloat16).to(dev)
+    t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, dev)
+    y = torch.zeros((b, rows), dtype=torch.float32, device=dev)
+
+    def step():
+        y.zero_()
+        decode_gemv(t, x, rows, cols, y)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    ref = torch.matmul(x.float(), W.to(dev).float().t().contiguous())
+    yb = y.to(torch.bfloat16).float()
+    ok = bool(((yb - ref).abs() <= 1e-3 + 1e-2 * ref.abs()).all())
+    if not ok:
+        print("fused GEMV differs from decode-then-matmul beyond rel 1e-2 / abs 1e-3",
+              file=sys.stderr)
+        return 1
+    stream = torch.cuda.current_stream(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    t_start = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t_start
+    step_s = ev0.elapsed_time(ev1) / 1e3 / args.steps
+    enc = layer.encoded
+    n = enc.n_symbols
+    chunk_bytes = int(enc.chunk_nbytes.astype(np.int64).sum())
+    # bitstreams + offsets/lengths + sign/mantissa + table + x read + y read/write
+    algo_bytes = chunk_bytes + 8 * enc.n_chunks + n + 6 * 4096 + 2 * b * cols + 8 * b * rows
+    rec = {
+        "metric": "fused decode->GEMV weight GB/s (bf16 bytes consumed per second)",
+        "value": round(2 * n * args.steps / wall / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {"workload": "fused decode->GEMV, 5120x17408 bf16 weight (seed 2, 0.1% "
+                               "outliers) x bf16 activation [%d, 17408] N(0,1) (seed 23), fp32 "
+                               "accumulate -> bf16" % b,
+                   "batch": b, "within_tolerance": ok, "tolerance": "rel 1e-2, abs 1e-3",
+                   "flops_per_step": 2 * n * b},
+        "roofline": {"bound": "hbm", "achieved": round(algo_bytes / step_s / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(algo_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "algorithmic_bytes_per_launch": algo_bytes,
+                     "kernel_us": round(step_s * 1e6, 2)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=["layer", "block"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "block", "gemv"], default="layer",
                     help="layer: one 5120x17408 weight (the headline); block: a whole "
-                         "14B-class decoder block in one launch")
+                         "14B-class decoder block in one launch; gemv: fused decode->GEMV "
+                         "of the 5120x17408 weight with a [batch, 17408] activation")
+    ap.add_argument("--batch", type=int, default=1, help="gemv batch (1..4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -134,6 +212,8 @@ def main() -> int:
 
     if args.copy_mib:
         return _copy_calibration(args.copy_mib, args.steps, args.warmup)
+    if args.workload == "gemv":
+        return _bench_gemv(args)
 
     from afterimage_amd import _native, workloads
     from afterimage_amd.runtime.device import DeviceTensor, _descriptor

@@ -112,6 +112,21 @@ int aimg_decode_bf16(const aimg_tensor* tensors, int n_tensors, void* stream);
  */
 int aimg_decode_u8(const aimg_tensor* tensors, int n_tensors, void* stream);
 
+/*
+ * Fused decode -> GEMV: y[b][r] += sum_c W[r][c] * x[b][c] in fp32 for the
+ * rows x cols row-major bf16 matrix W held compressed in *t
+ * (t->n_symbols == rows * cols) and b < batch (1..4). W is never written;
+ * t->out is ignored. x: bf16 [batch][cols] (device). y: float [batch][rows]
+ * (device), which the caller zeroes first: the kernel adds to it with
+ * atomics, so the order of the fp32 additions is not fixed. The reference
+ * computes this as decompress_rows_gpu (compressed_store.py:254-303) followed
+ * by a matmul in its chunked lm_head (streaming_engine.py:2271-2335).
+ * cols % 8 == 0 with a 16-byte-aligned x takes the vector path; other
+ * shapes are correct but add every product with its own atomic.
+ */
+int aimg_decode_gemv_bf16(const aimg_tensor* t, int64_t rows, int64_t cols, const void* x,
+                          int batch, float* y, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Encoder support (host).                                                   */
 /* ------------------------------------------------------------------------- */

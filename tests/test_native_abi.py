@@ -66,6 +66,28 @@ def test_decode_entry_points_validate_before_launching():
     assert lib.aimg_decode_bf16(arr, 0, None) == _native.AIMG_OK
 
 
+def test_gemv_entry_point_validates_before_launching():
+    lib = _native.lib()
+    arr = (_native.AimgTensor * 1)()
+    arr[0].chunk_size = 16
+    arr[0].n_chunks = 1
+    arr[0].n_symbols = 16
+    x = ctypes.c_void_p(16)
+    y = ctypes.c_void_p(16)
+    assert lib.aimg_decode_gemv_bf16(None, 4, 4, x, 1, y, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    assert lib.aimg_decode_gemv_bf16(arr, 4, 5, x, 1, y, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    assert b"rows * cols" in lib.aimg_last_error()
+    assert lib.aimg_decode_gemv_bf16(arr, 4, 4, x, 5, y, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    assert b"batch" in lib.aimg_last_error()
+    assert lib.aimg_decode_gemv_bf16(arr, 4, 4, None, 1, y, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    # A tensor without device pointers fails in the shared checks.
+    assert lib.aimg_decode_gemv_bf16(arr, 4, 4, x, 1, y, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    assert b"null" in lib.aimg_last_error()
+    arr[0].n_symbols = 1 << 31
+    arr[0].n_chunks = 1 << 27
+    assert lib.aimg_decode_bf16(arr, 1, None) == _native.AIMG_ERR_UNSUPPORTED
+
+
 def test_table_builder_rejects_wide_symbols():
     sym = np.array([0, 300], np.int32)
     ln = np.array([1, 1], np.int8)
