@@ -108,6 +108,87 @@ def _copy_calibration(mib: int, steps: int, warmup: int) -> int:
     return 0
 
 
+def _bench_ring(args) -> int:
+    """Streamed 14B-class blocks: two distinct compressed blocks in pinned host
+    memory, cycled through `--layers` layers per step; H2D on a side stream,
+    decode on the compute stream, 2-slot ring under a 4 GiB device budget."""
+    from afterimage_amd import workloads
+    from afterimage_amd.runtime.stream_ring import HostBlock, LayerRing
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    t0 = time.perf_counter()
+    blocks = [workloads.block_14b(seed=s) for s in (3, 4)]
+    hbs = [HostBlock([l for _, _, l in blk]) for blk in blocks]
+    _log("2 blocks built and pinned in %.1fs: %.1f MB compressed each"
+         % (time.perf_counter() - t0, hbs[0].nbytes / 1e6))
+    ring = LayerRing(hbs, device=dev, slots=2, vram_budget=4 << 30)
+    refs = [[w.reshape(-1).view(torch.int16) for _, w, _ in blk] for blk in blocks]
+    # Warmup pass, with a bit-exact check of each distinct block.
+    ok = True
+    for k, tensors in ring.stream(max(2, min(args.warmup, args.layers))):
+        if k < 2:
+            ok = ok and all(torch.equal(t.reshape(-1).view(torch.int16).cpu(), r)
+                            for t, r in zip(tensors, refs[k % 2]))
+    torch.cuda.synchronize(dev)
+    if not ok:
+        print("streamed decode differs from the original weights", file=sys.stderr)
+        return 1
+    ring.timing = True
+    walls = []
+    dec_s = []
+    for _ in range(args.steps):
+        torch.cuda.synchronize(dev)
+        t_start = time.perf_counter()
+        for _k, _t in ring.stream(args.layers):
+            pass
+        torch.cuda.synchronize(dev)
+        walls.append(time.perf_counter() - t_start)
+        dec_s.append(sum(a.elapsed_time(b) for a, b in ring.decode_events) / 1e3)
+    wall = sorted(walls)[len(walls) // 2]
+    decode = sorted(dec_s)[len(dec_s) // 2]
+    # Pinned H2D alone, for context.
+    s = torch.cuda.Stream(dev)
+    slot = torch.empty(hbs[0].nbytes, dtype=torch.uint8, device=dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        e0.record(s)
+        for _ in range(4):
+            slot.copy_(hbs[0].buf, non_blocking=True)
+        e1.record(s)
+    torch.cuda.synchronize(dev)
+    h2d_gbs = 4 * hbs[0].nbytes / (e0.elapsed_time(e1) / 1e3) / 1e9
+    decoded = sum(hb.decoded_nbytes for hb in hbs) / len(hbs)
+    rec = {
+        "metric": "streamed 14B-class blocks: end-to-end layers/s (H2D + decode)",
+        "value": round(args.layers / wall, 2),
+        "unit": "layers/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {"workload": "%d layers of the 14B-class block (2 distinct blocks, seeds 3/4, "
+                               "cycled), compressed in pinned host memory, H2D on a side stream, "
+                               "2-slot ring" % args.layers,
+                   "ring_device_bytes": ring.ring_bytes, "vram_budget": 4 << 30,
+                   "compressed_bytes_per_layer": hbs[0].nbytes,
+                   "decoded_bytes_per_layer": int(decoded), "bit_exact": ok},
+        "decode_only_gbs": round(args.layers * decoded / decode / 1e9, 1),
+        "h2d_pinned_gbs": round(h2d_gbs, 1),
+        "h2d_bound_layers_per_s": round(h2d_gbs * 1e9 / hbs[0].nbytes, 2),
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
 def _bench_gemv(args) -> int:
     """Fused decode->GEMV: y[b] = W x[b] for the 5120x17408 weight, W decoded
     in the kernel and never written. One step = zero y + one launch."""
@@ -168,7 +249,7 @@ def _bench_gemv(args) -> int:
         "vs_baseline": None,
         "dtype": "u8",
         "data": "synthetic",
-        "config": {"workload": "fused decode->GEMV, 5120x17408 bf16 weight (seed 2, 0.1% "
+        "config": {"workload": "fused decode->GEMV, 5120x17408 bf16 weight (seed 2, 0.1%% "
                                "outliers) x bf16 activation [%d, 17408] N(0,1) (seed 23), fp32 "
                                "accumulate -> bf16" % b,
                    "batch": b, "within_tolerance": ok, "tolerance": "rel 1e-2, abs 1e-3",
@@ -189,10 +270,12 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=["layer", "block", "gemv"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "block", "gemv", "ring"], default="layer",
                     help="layer: one 5120x17408 weight (the headline); block: a whole "
                          "14B-class decoder block in one launch; gemv: fused decode->GEMV "
-                         "of the 5120x17408 weight with a [batch, 17408] activation")
+                         "of the 5120x17408 weight with a [batch, 17408] activation; ring: 40 "
+                         "streamed blocks from pinned host memory through a 2-slot ring")
+    ap.add_argument("--layers", type=int, default=40, help="ring: layers streamed per step")
     ap.add_argument("--batch", type=int, default=1, help="gemv batch (1..4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=16)
@@ -214,6 +297,8 @@ def main() -> int:
         return _copy_calibration(args.copy_mib, args.steps, args.warmup)
     if args.workload == "gemv":
         return _bench_gemv(args)
+    if args.workload == "ring":
+        return _bench_ring(args)
 
     from afterimage_amd import _native, workloads
     from afterimage_amd.runtime.device import DeviceTensor, _descriptor
