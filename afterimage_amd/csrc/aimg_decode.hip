@@ -57,13 +57,16 @@ static_assert(kThreads == 1 << kLgThreads, "kLgThreads");
 constexpr int kMinTpc = 16;
 constexpr int kMaxGroups = kThreads / kMinTpc;
 constexpr uint32_t kOverlapBits = 32;
-// Per-thread slot for one segment's symbols: an odd number of words, so the
-// slots of a wave's lanes start in different banks. A lookup writes 4 bytes
-// at the running count, so a slot holds kSlotCap symbols.
-constexpr uint32_t kSlotWords = 19;
-constexpr uint32_t kSlotBytes = 4 * kSlotWords;
-constexpr uint32_t kSlotCap = kSlotBytes - 4;
-constexpr uint32_t kMaxSegBits = 160;
+// Per-thread slot for one segment's symbols, kSlotCap bytes. Slots are an
+// odd number of words apart, so the lanes of a wave writing at similar counts
+// hit different LDS banks. 168-bit segments at the 2-bit shortest code of
+// bf16 weights make a 64Ki-symbol chunk (about 171K bits) two rounds of 512
+// segments.
+constexpr uint32_t kSlotCap = 84;
+constexpr uint32_t kSlotBytes = kSlotCap;
+constexpr uint32_t kSlotWords = kSlotBytes / 4;
+static_assert(kSlotBytes % 4 == 0 && kSlotWords % 2 == 1, "slot stride: an odd number of words");
+constexpr uint32_t kMaxSegBits = 168;
 constexpr uint32_t kLeadBytes = 16;  // room for a carried partial vector group
 constexpr uint32_t kTileSlackWords = 4;
 constexpr uint32_t kTileWords = kThreads * kMaxSegBits / 32 + kTileSlackWords * kMaxGroups;
@@ -76,8 +79,13 @@ constexpr int kLdsEscBlocks = 64;
 constexpr uint32_t kTileBatch = kMaxSegBits / 32 + 1;
 // Output vector groups a thread stores per round: a round places at most
 // kSlotCap symbols per thread, plus a carried partial group.
-constexpr uint32_t kStoreBatch = (kSlotCap + 7) / 8 + 1;
+constexpr uint32_t kStoreBatch = (kSlotCap * kMinTpc + 15 + 8 * kMinTpc - 1) / (8 * kMinTpc);
 static_assert(kStoreBatch * 8 * kMinTpc >= kSlotCap * kMinTpc + 15, "one store batch covers a round");
+// Of those, the groups whose sign/mantissa bytes are requested while the round
+// decodes. A round of bf16 weights fills about 8 groups per thread; the rest
+// are loaded at the store, by waves that need them.
+constexpr uint32_t kSmAhead = 9;
+static_assert(kSmAhead <= kStoreBatch, "kSmAhead");
 
 struct DevTensor {
     const uint8_t* packed;
@@ -127,6 +135,23 @@ __device__ __forceinline__ T load_uniform(const T* p) {
     return *(const __attribute__((address_space(4))) T*)(p);
 }
 
+// Values the same in every lane, moved to scalar registers: the compiler
+// cannot always prove it, and loads through a pointer it takes for divergent
+// become vector loads, whose waits also wait for the stores issued before.
+// The builtin takes and returns int: each half goes back through uint32_t so
+// that a low word with its top bit set is not sign-extended into the high one.
+__device__ __forceinline__ uint32_t uniform(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+
+template <typename P>
+__device__ __forceinline__ P* uniform(P* p) {
+    const uint64_t v = reinterpret_cast<uintptr_t>(p);
+    const uint64_t lo = uniform(static_cast<uint32_t>(v));
+    const uint64_t hi = uniform(static_cast<uint32_t>(v >> 32));
+    return reinterpret_cast<P*>((hi << 32) | lo);
+}
+
 __device__ __forceinline__ const __attribute__((address_space(4))) TableHeader* header_of(
     const uint8_t* table) {
     return (const __attribute__((address_space(4))) TableHeader*)(table);
@@ -141,7 +166,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, ui
 
 struct Tables {
     const uint32_t* syms;    // LDS window table: symbols / escape block
-    const uint16_t* meta;    // LDS window table: end mask | total << 12
+    const uint8_t* meta;     // LDS window table: total | count << 4
+    const uint8_t* len;      // LDS code length of each symbol
     const uint16_t* esc;     // LDS escape blocks (first kLdsEscBlocks)
     const __attribute__((address_space(1))) uint16_t* gesc;  // all escape blocks, global memory
     uint32_t sym0;
@@ -149,28 +175,29 @@ struct Tables {
 };
 
 // Bit reader over the staged stream. A sub-group's tile holds its round's
-// stream words in reverse order (word j at top[-j]), so one 8-byte LDS read
-// at top - k - 1 returns words k+1 and k as the low and high halves of the
+// stream words in reverse order (word j at below[-j]), so one 8-byte LDS read
+// at below - k - 1 returns words k+1 and k as the low and high halves of the
 // 64-bit pair that starts at word k. `pair` holds the words from bit
 // p - sh (a multiple of 32, sh <= 47); a step reads at most 16 bits, all
 // inside the pair. While a step's table lookup is in flight, the reader
 // already fetches the pair starting at the word that contains p, which
 // holds the next step's bits, so each step waits for one LDS round trip.
 struct Reader {
-    const uint32_t* top;
+    const uint32_t* below;
     uint32_t p;
     uint32_t sh;
     uint64_t pair;
 };
 
-__device__ __forceinline__ uint64_t load_pair(const uint32_t* top, uint32_t k) {
+// `below` is below - 1: the pair starting at word k is read at below - k.
+__device__ __forceinline__ uint64_t load_pair(const uint32_t* below, uint32_t k) {
     uint64_t v;
-    __builtin_memcpy(&v, top - k - 1, 8);  // 4-byte aligned: two word reads
+    __builtin_memcpy(&v, below - k, 8);  // 4-byte aligned: two word reads
     return v;
 }
 
-__device__ __forceinline__ Reader reader_at(const uint32_t* top, uint32_t p) {
-    return {top, p, p & 31u, load_pair(top, p >> 5)};
+__device__ __forceinline__ Reader reader_at(const uint32_t* below, uint32_t p) {
+    return {below, p, p & 31u, load_pair(below, p >> 5)};
 }
 
 // The 32 bits at the reader's position (bits past the pair read as zero;
@@ -225,53 +252,66 @@ struct Adv {
     uint32_t n;
 };
 
-// Parse codewords from boundary p until the first boundary at or after x;
-// returns that boundary and the number of codewords that start before x.
+// A window that ends at or past x, starting at P < x with c codewords
+// (symbols: the bytes of syms): its codewords that start at or after x are
+// cut off. Returns the first codeword boundary at or after x (`end`, the
+// window's end, if none starts inside) and sets *kept to the codewords that
+// start before x. Boundaries come from the symbols' code lengths.
+__device__ __forceinline__ uint32_t cut_window(const Tables& tb, uint32_t P, uint32_t end,
+                                               uint32_t syms, uint32_t c, uint32_t x,
+                                               uint32_t* kept) {
+    uint32_t st = P, e = end, k = c;
+#pragma unroll
+    for (uint32_t j = 0; j + 1 < static_cast<uint32_t>(kMaxSymsPerWindow); ++j) {
+        if (j + 1 < c) {
+            st += tb.len[(syms >> (8 * j)) & 0xFFu];
+            if (st >= x && k == c) {
+                e = st;
+                k = j + 1;
+            }
+        }
+    }
+    *kept = k;
+    return e;
+}
+
+// The first codeword boundary at or after x, parsing from boundary p.
 template <bool kGlobalEsc>
-__device__ __forceinline__ Adv advance(const uint32_t* top, const Tables& tb, uint32_t p,
-                                       uint32_t x) {
-    uint32_t n = 0;
-    Reader rd = reader_at(top, p);
+__device__ __forceinline__ uint32_t advance(const uint32_t* below, const Tables& tb, uint32_t p,
+                                            uint32_t x) {
+    Reader rd = reader_at(below, p);
     // Whole windows while no codeword of the window can reach x.
     const int32_t x12 = static_cast<int32_t>(x) - kWinBits;
     while (static_cast<int32_t>(rd.p) <= x12) {
         const uint32_t w = reader_bits(rd);
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
-        const uint64_t next = load_pair(top, rd.p >> 5);
-        uint32_t adv = meta >> 12;
-        uint32_t c = __popc(meta & 0xFFFu);
+        const uint64_t next = load_pair(below, rd.p >> 5);
+        uint32_t adv = meta & 15u;
         if (__builtin_expect(any_lane(adv == 0), 0)) {
-            if (adv == 0) {
-                escape<kGlobalEsc>(tb, tb.syms[idx], w, &adv);
-                c = 1;
-            }
+            if (adv == 0) escape<kGlobalEsc>(tb, tb.syms[idx], w, &adv);
         }
-        n += c;
         reader_skip(rd, next, adv);
     }
     while (rd.p < x) {
         const uint32_t w = reader_bits(rd);
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
-        const uint64_t next = load_pair(top, rd.p >> 5);
-        const uint32_t total = meta >> 12;
-        if (total == 0) {
-            uint32_t l;
-            escape<kGlobalEsc>(tb, tb.syms[idx], w, &l);
-            reader_skip(rd, next, l);
-            n += 1;
-            continue;
+        uint32_t syms = tb.syms[idx];
+        const uint64_t next = load_pair(below, rd.p >> 5);
+        uint32_t adv = meta & 15u;
+        uint32_t c = meta >> 4;
+        if (adv == 0) {
+            escape<kGlobalEsc>(tb, syms, w, &adv);
+            c = 1;
         }
-        const uint32_t ends = meta & 0xFFFu;  // bit k-1: a codeword ends at offset k
-        const uint32_t rel = x - rd.p;        // 1..11
-        const uint32_t upto = total < rel ? total : rel;
-        // Codewords starting before rel: the one at offset 0 plus every end
-        // boundary at offset 1..upto-1.
-        n += 1 + __popc(ends & ((1u << (upto - 1)) - 1u));
-        reader_skip(rd, next, total < rel ? total : rel - 1 + __ffs(ends >> (rel - 1)));
+        if (rd.p + adv >= x) {
+            uint32_t kept;
+            return cut_window(tb, rd.p, rd.p + adv, syms, c, x, &kept);
+        }
+        reader_skip(rd, next, adv);
     }
-    return {rd.p, n};
+    return rd.p;
 }
 
 __device__ __forceinline__ uint32_t get_u32(const uint8_t* p) {
@@ -287,7 +327,8 @@ __device__ __forceinline__ void clear_slot(uint8_t* slot) {
 
 // Place the symbols of one lookup (bytes of syms, zero above the lookup's
 // count) at slot[n...]: OR them into the one or two words they fall in,
-// so no word needs reading or merging first.
+// so no word needs reading or merging first. For n near kSlotCap the second
+// word is the next slot's first: only zero bits go there.
 __device__ __forceinline__ void slot_or(uint8_t* slot, uint32_t n, uint32_t syms) {
     const uint64_t v = static_cast<uint64_t>(syms) << (8 * (n & 3u));
     uint32_t* w = reinterpret_cast<uint32_t*>(slot + (n & ~3u));
@@ -300,23 +341,23 @@ __device__ __forceinline__ void slot_or(uint8_t* slot, uint32_t n, uint32_t syms
 // their symbols in the (zeroed) slot. Returns the first boundary at or
 // after x and the number of codewords. Every codeword (or unused window)
 // takes at least min_len bits, so a segment of at most kSlotCap * min_len
-// bits never holds more than kSlotCap codewords, and every word written
-// lies inside the slot. The last lookup may leave symbols that start at or
-// after x past the count; they are never read.
+// bits never holds more than kSlotCap codewords: every nonzero byte written
+// lies inside the slot. The last lookup's symbols that start at or after x
+// are masked off before it is placed.
 template <bool kGlobalEsc>
-__device__ __forceinline__ Adv decode_run(const uint32_t* top, const Tables& tb, uint32_t p,
+__device__ __forceinline__ Adv decode_run(const uint32_t* below, const Tables& tb, uint32_t p,
                                           uint32_t x, uint8_t* slot) {
     uint32_t n = 0;
-    Reader rd = reader_at(top, p);
+    Reader rd = reader_at(below, p);
     const int32_t x12 = static_cast<int32_t>(x) - kWinBits;
     while (static_cast<int32_t>(rd.p) <= x12) {
         const uint32_t w = reader_bits(rd);
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
         uint32_t syms = tb.syms[idx];
-        const uint64_t next = load_pair(top, rd.p >> 5);
-        uint32_t adv = meta >> 12;
-        uint32_t c = __popc(meta & 0xFFFu);
+        const uint64_t next = load_pair(below, rd.p >> 5);
+        uint32_t adv = meta & 15u;
+        uint32_t c = meta >> 4;
         if (__builtin_expect(any_lane(adv == 0), 0)) {
             if (adv == 0) {
                 syms = escape<kGlobalEsc>(tb, syms, w, &adv);
@@ -332,18 +373,18 @@ __device__ __forceinline__ Adv decode_run(const uint32_t* top, const Tables& tb,
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
         uint32_t syms = tb.syms[idx];
-        const uint64_t next = load_pair(top, rd.p >> 5);
-        const uint32_t total = meta >> 12;
-        uint32_t adv, c;
-        if (total == 0) {
+        const uint64_t next = load_pair(below, rd.p >> 5);
+        uint32_t adv = meta & 15u;
+        uint32_t c = meta >> 4;
+        if (adv == 0) {
             syms = escape<kGlobalEsc>(tb, syms, w, &adv);
             c = 1;
-        } else {
-            const uint32_t ends = meta & 0xFFFu;
-            const uint32_t rel = x - rd.p;  // 1..11
-            const uint32_t upto = total < rel ? total : rel;
-            c = 1 + __popc(ends & ((1u << (upto - 1)) - 1u));
-            adv = total < rel ? total : rel - 1 + __ffs(ends >> (rel - 1));
+        }
+        if (rd.p + adv >= x) {
+            uint32_t kept;  // 1..4
+            const uint32_t e = cut_window(tb, rd.p, rd.p + adv, syms, c, x, &kept);
+            slot_or(slot, n, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
+            return {e, n + kept};
         }
         slot_or(slot, n, syms);
         n += c;
@@ -406,19 +447,27 @@ __device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, ui
     const uint32_t n_groups = kThreads >> J.lg;
     J.c = (item - T.item_begin) * n_groups + (tid >> J.lg);
     // Segment length: at most kSlotCap codewords of the shortest length.
-    const uint32_t min_len = header_of(T.table)->min_len;
+    const uint32_t min_len = header_of(uniform(T.table))->min_len;
     const uint32_t S = kSlotCap * (min_len >= 1 ? min_len : 1u);
     J.S = (S < kMaxSegBits ? S : kMaxSegBits) & ~7u;
-    if (J.c < T.n_jobs) {
-        int64_t off, nb;
-        if (n_groups == 1) {
-            const int64_t cu = item - T.item_begin;  // the same for every thread
-            off = load_uniform(T.offsets + cu);
-            nb = load_uniform(T.nbytes + cu);
-        } else {
-            off = T.offsets[J.c];
-            nb = T.nbytes[J.c];
+    // A wave holds 64 >> lg sub-groups (one when lg >= 6), on consecutive
+    // chunks. Their offsets and lengths come through scalar loads, so no wait
+    // for them waits for the vector stores in flight; each lane keeps its own.
+    const int64_t c_wave = (item - T.item_begin) * n_groups + (uniform(tid & ~63u) >> J.lg);
+    const uint32_t per_wave = J.lg >= 6 ? 1u : 64u >> J.lg;
+    int64_t off = 0, nb = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < 64 / kMinTpc; ++k) {
+        if (k < per_wave && c_wave + k < T.n_jobs) {
+            const int64_t o = load_uniform(T.offsets + c_wave + k);
+            const int64_t n = load_uniform(T.nbytes + c_wave + k);
+            if (J.c == c_wave + k) {
+                off = o;
+                nb = n;
+            }
         }
+    }
+    if (J.c < T.n_jobs) {
         off = off < 0 ? 0 : (off > T.packed_nbytes ? T.packed_nbytes : off);
         nb = nb < 0 ? 0 : (nb > T.packed_nbytes - off ? T.packed_nbytes - off : nb);
         int64_t lim = T.n_symbols - J.c * T.chunk_size;
@@ -577,7 +626,7 @@ __device__ __forceinline__ void store_one(const DevTensor& T, const GemvArgs& G,
 // (groups k * tpc + i of the round), requested ahead of use.
 template <int kMode>
 struct SmBatch {
-    uint2 v[kMode != kModeU8 ? kStoreBatch : 1];
+    uint2 v[kMode != kModeU8 ? kSmAhead : 1];
 };
 
 // Buffer loads (zero past the tensor's last byte), so the batch needs no
@@ -589,7 +638,7 @@ __device__ __forceinline__ void sm_issue(SmBatch<kMode>& B, const DevTensor& T, 
     const __amdgpu_buffer_rsrc_t rs = buffer_of(T.sm, static_cast<uint32_t>(T.n_symbols));
     const uint32_t v0 = static_cast<uint32_t>(a0) + i * kGroup;
 #pragma unroll
-    for (uint32_t k = 0; k < kStoreBatch; ++k) {
+    for (uint32_t k = 0; k < kSmAhead; ++k) {
         const auto d = __builtin_amdgcn_raw_buffer_load_b64(rs, v0, k * tpc * kGroup, 0);
         B.v[k] = make_uint2(d[0], d[1]);
     }
@@ -633,9 +682,32 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
         return;
     }
 #pragma unroll
-    for (uint32_t k = 0; k < kStoreBatch; ++k) {
+    for (uint32_t k = 0; k < kSmAhead; ++k) {
         consume(B.v[k].x);
         consume(B.v[k].y);
+    }
+    // Sign/mantissa of groups past the requested ones, for waves that have any.
+    uint2 sm[kStoreBatch];
+#pragma unroll
+    for (uint32_t k = 0; k < kSmAhead; ++k) sm[k] = B.v[k];
+    if (__builtin_amdgcn_ballot_w64(kSmAhead * tpc + i < nfull) != 0) {
+        const __amdgpu_buffer_rsrc_t rs = buffer_of(T.sm, static_cast<uint32_t>(T.n_symbols));
+        const uint32_t v0 = static_cast<uint32_t>(a0) + i * kGroup;
+#pragma unroll
+        for (uint32_t k = kSmAhead; k < kStoreBatch; ++k) {
+            const auto d = __builtin_amdgcn_raw_buffer_load_b64(rs, v0, k * tpc * kGroup, 0);
+            sm[k] = make_uint2(d[0], d[1]);
+        }
+        // Waited for here, before any store is issued: a wait after the
+        // stores would wait for them too.
+#pragma unroll
+        for (uint32_t k = kSmAhead; k < kStoreBatch; ++k) {
+            consume(sm[k].x);
+            consume(sm[k].y);
+        }
+    } else {
+#pragma unroll
+        for (uint32_t k = kSmAhead; k < kStoreBatch; ++k) sm[k] = make_uint2(0u, 0u);
     }
     // All staged exponents are read (from clamped, always valid offsets)
     // before any is combined, so the LDS reads overlap.
@@ -652,10 +724,10 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
             const uint32_t v = k * tpc + i;
             if (v >= nfull) continue;
             uint4 o4;
-            o4.x = bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].x, ev[k].x);
-            o4.y = bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].x, ev[k].x);
-            o4.z = bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].y, ev[k].y);
-            o4.w = bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].y, ev[k].y);
+            o4.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, ev[k].x);
+            o4.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, ev[k].x);
+            o4.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, ev[k].y);
+            o4.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, ev[k].y);
             dst[v] = o4;
         }
         return;
@@ -685,10 +757,10 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
         const bool live = v < nfull;
         float p[kGemvMaxBatch] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (live) {
-            const uint32_t o[4] = {bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].x, ev[k].x),
-                                   bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].x, ev[k].x),
-                                   bf16_pair<0x01010000u, 0x010C000Cu>(B.v[k].y, ev[k].y),
-                                   bf16_pair<0x03030202u, 0x030C020Cu>(B.v[k].y, ev[k].y)};
+            const uint32_t o[4] = {bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, ev[k].x),
+                                   bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, ev[k].x),
+                                   bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, ev[k].y),
+                                   bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, ev[k].y)};
 #pragma unroll
             for (int b = 0; b < kGemvMaxBatch; ++b) {
                 if (b >= G.batch) break;
@@ -724,36 +796,59 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
 
 // Window table and the first kLdsEscBlocks escape blocks of a table blob to LDS.
 __device__ __forceinline__ void load_table(const uint8_t* table, uint32_t tid, uint32_t* s_wsyms,
-                                           uint16_t* s_wmeta, uint16_t* s_esc) {
+                                           uint8_t* s_wmeta, uint8_t* s_len, uint16_t* s_esc) {
     const uint4* src = reinterpret_cast<const uint4*>(table + kSymsOffset);
     uint4* dst = reinterpret_cast<uint4*>(s_wsyms);
     for (uint32_t j = tid; j < kWinEntries / 4; j += kThreads) dst[j] = src[j];
     const uint4* msrc = reinterpret_cast<const uint4*>(table + kMetaOffset);
     uint4* mdst = reinterpret_cast<uint4*>(s_wmeta);
-    for (uint32_t j = tid; j < kWinEntries / 8; j += kThreads) mdst[j] = msrc[j];
+    for (uint32_t j = tid; j < kWinEntries / 16; j += kThreads) mdst[j] = msrc[j];
+    const uint4* lsrc = reinterpret_cast<const uint4*>(table + kLenOffset);
+    for (uint32_t j = tid; j < 256 / 16; j += kThreads) reinterpret_cast<uint4*>(s_len)[j] = lsrc[j];
     const uint32_t n_blocks = header_of(table)->n_esc_blocks;
     const uint32_t n_esc = n_blocks < static_cast<uint32_t>(kLdsEscBlocks) ? n_blocks : kLdsEscBlocks;
     const uint16_t* gesc = reinterpret_cast<const uint16_t*>(table + kEscOffset);
     for (uint32_t j = tid; j < n_esc * kEscBlockEntries; j += kThreads) s_esc[j] = gesc[j];
 }
 
+// A workgroup's LDS, in one block so that the small tables sit at the lowest
+// addresses, where their bases fit the LDS instructions' 16-bit offsets.
+struct __attribute__((aligned(16))) Lds {
+    uint8_t wmeta[kWinEntries];
+    uint8_t len[256];
+    uint16_t esc[kLdsEscBlocks * kEscBlockEntries];
+    uint32_t wsyms[kWinEntries];
+    uint32_t wsum[kWaves];
+    uint32_t gpre[kMaxGroups + 1];
+    uint32_t gval[kMaxGroups];
+    uint32_t ewave[kWaves];      // segment end of each wave's last lane
+    uint32_t glast[kMaxGroups];  // segment end of each sub-group's last active thread
+    uint32_t tile[kTileWords];
+    // 16 bytes past the last slot: the word read or zero-ORed past it.
+    __attribute__((aligned(16))) uint8_t stage[kStageBytes + 16];
+};
+
 template <int kMode, int kGroup, bool kTiny>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const LaunchArgs args) {
-    __shared__ uint32_t s_wsyms[kWinEntries];
-    __shared__ uint16_t s_wmeta[kWinEntries];
-    __shared__ uint16_t s_esc[kLdsEscBlocks * kEscBlockEntries];
-    __shared__ uint32_t s_tile[kTileWords];
-    __shared__ __attribute__((aligned(16))) uint8_t s_stage[kStageBytes];
-    __shared__ uint32_t s_e[kThreads];
-    __shared__ uint32_t s_wsum[kWaves];
-    __shared__ uint32_t s_gpre[kMaxGroups + 1];
-    __shared__ uint32_t s_gval[kMaxGroups];
+    __shared__ Lds lds;
+    uint32_t* const s_wsyms = lds.wsyms;
+    uint8_t* const s_wmeta = lds.wmeta;
+    uint8_t* const s_len = lds.len;
+    uint16_t* const s_esc = lds.esc;
+    uint32_t* const s_tile = lds.tile;
+    uint8_t* const s_stage = lds.stage;
+    uint32_t* const s_ewave = lds.ewave;
+    uint32_t* const s_glast = lds.glast;
+    uint32_t* const s_wsum = lds.wsum;
+    uint32_t* const s_gpre = lds.gpre;
+    uint32_t* const s_gval = lds.gval;
 
     const uint32_t tid = threadIdx.x;
     const uint8_t* loaded = nullptr;
     Tables tb;
     tb.syms = s_wsyms;
     tb.meta = s_wmeta;
+    tb.len = s_len;
     tb.esc = s_esc;
 
     // Software pipeline: the stream words of the next round (or of the next
@@ -762,34 +857,35 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     Job cur = make_job(args, blockIdx.x, tid);
     Fetch F;
     fetch_issue<kTiny>(F, args, cur, 0, tid);
-    loaded = args.t[cur.d].table;
-    load_table(loaded, tid, s_wsyms, s_wmeta, s_esc);
+    loaded = uniform(args.t[uniform(static_cast<uint32_t>(cur.d))].table);
+    load_table(loaded, tid, s_wsyms, s_wmeta, s_len, s_esc);
     fetch_commit<kTiny>(F, args, cur, 0, tid, s_tile);
 
     for (int64_t item = blockIdx.x; item < args.total_items; item += gridDim.x) {
-        const DevTensor& T = args.t[cur.d];
-        const uint32_t lg = cur.lg;
+        const DevTensor& T = args.t[uniform(static_cast<uint32_t>(cur.d))];
+        const uint8_t* const table = uniform(T.table);
+        const uint32_t lg = uniform(cur.lg);
         const uint32_t tpc = 1u << lg;
         const uint32_t g = tid >> lg;
         const uint32_t i_item = tid & (tpc - 1);
         const uint32_t n_groups = kThreads >> lg;
-        const uint32_t S = cur.S;
+        const uint32_t S = uniform(cur.S);
         const Job nxt = make_job(args, item + gridDim.x, tid);
 
-        __syncthreads();  // the previous item is done with LDS; its tile writes are visible
-        if (T.table != loaded) {
-            loaded = T.table;
-            load_table(T.table, tid, s_wsyms, s_wmeta, s_esc);
-        }
-        const auto* hdr = header_of(T.table);
+        const auto* hdr = header_of(table);
         tb.sym0 = hdr->sym0;
         tb.min_len = hdr->min_len >= 1 ? hdr->min_len : 1u;
-        tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(T.table + kEscOffset);
+        tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(table + kEscOffset);
         const bool global_esc = hdr->n_esc_blocks > static_cast<uint32_t>(kLdsEscBlocks);
+        __syncthreads();  // the previous item is done with LDS; its tile writes are visible
+        if (table != loaded) {
+            loaded = table;
+            load_table(table, tid, s_wsyms, s_wmeta, s_len, s_esc);
+        }
 
         const int64_t chunk_base = cur.c * T.chunk_size;
         const int64_t lim = cur.lim;
-        const uint32_t* top = tile_top(s_tile, g, lg);
+        const uint32_t* below = tile_top(s_tile, g, lg) - 1;
         const uint32_t region = kStageBytes >> (kLgThreads - lg);
         uint8_t* stage = s_stage + g * region;
         uint8_t* slot = stage + kLeadBytes + i_item * kSlotBytes;
@@ -798,6 +894,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         __syncthreads();
         uint32_t NR = 0;
         for (uint32_t k = 0; k < n_groups; ++k) NR = NR > s_gval[k] ? NR : s_gval[k];
+        NR = uniform(NR);
 
         uint32_t p0 = 0;    // true start of the next round, relative to its first bit
         int64_t ob = 0;     // chunk-local symbols placed so far
@@ -828,39 +925,44 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 clear_slot(slot);
                 Adv a;
                 if (global_esc) {
-                    f = i == 0 ? p0 : advance<true>(top, tb, seg_lo - kOverlapBits, seg_lo).p;
-                    a = decode_run<true>(top, tb, f, seg_hi, slot);
+                    f = i == 0 ? p0 : advance<true>(below, tb, seg_lo - kOverlapBits, seg_lo);
+                    a = decode_run<true>(below, tb, f, seg_hi, slot);
                 } else {
-                    f = i == 0 ? p0 : advance<false>(top, tb, seg_lo - kOverlapBits, seg_lo).p;
-                    a = decode_run<false>(top, tb, f, seg_hi, slot);
+                    f = i == 0 ? p0 : advance<false>(below, tb, seg_lo - kOverlapBits, seg_lo);
+                    a = decode_run<false>(below, tb, f, seg_hi, slot);
                 }
                 e = a.p;
                 cnt = a.n;
             }
-            s_e[tid] = e;
-            __syncthreads();
+            // A segment is right when it starts where its predecessor's last
+            // codeword ends. The predecessor's end comes from the lane below;
+            // a wave's lane 0 reads the previous wave's lane 63 through LDS.
+            const uint32_t lane = tid & 63u;
+            const uint32_t wprev = ((tid >> 6) - 1u) & (kWaves - 1u);
             for (;;) {
-                const bool bad = active && i > 0 && f != s_e[tid - 1];
-                const uint32_t nf = bad ? s_e[tid - 1] : 0u;
+                uint32_t ep = __shfl_up(e, 1, 64);
+                if (lane == 63) s_ewave[tid >> 6] = e;
+                __syncthreads();
+                if (lane == 0) ep = s_ewave[wprev];
+                const bool bad = active && i > 0 && f != ep;
                 if (!__syncthreads_or(bad)) break;
                 if (bad) {
-                    f = nf;
+                    f = ep;
                     clear_slot(slot);
-                    const Adv a = global_esc ? decode_run<true>(top, tb, f, seg_hi, slot)
-                                             : decode_run<false>(top, tb, f, seg_hi, slot);
+                    const Adv a = global_esc ? decode_run<true>(below, tb, f, seg_hi, slot)
+                                             : decode_run<false>(below, tb, f, seg_hi, slot);
                     e = a.p;
                     cnt = a.n;
-                    s_e[tid] = e;
                 }
-                __syncthreads();
             }
+            const uint32_t n_active = g_active ? (RB + S - 1) / S : 1u;
+            if (i == n_active - 1) s_glast[g] = e;
 
             const uint32_t excl = block_scan_excl(cnt, s_wsum);
             if (i == 0) s_gpre[g] = excl;
             if (tid == kThreads - 1) s_gpre[n_groups] = excl + cnt;
-            const uint32_t n_active = g_active ? (RB + S - 1) / S : 1u;
             __syncthreads();
-            const uint32_t e_last = s_e[g * tpc + n_active - 1];
+            const uint32_t e_last = s_glast[g];
             const uint32_t o = excl - s_gpre[g];
             const uint32_t gtot = s_gpre[g + 1] - s_gpre[g];
             const int64_t still = lim - ob;
@@ -877,10 +979,12 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const uint32_t head = head0 < m ? head0 : m;  // bytes before the first aligned word
             const uint32_t nbody = (m - head) >> 2;       // whole words
             const uint32_t ntail = m - head - 4 * nbody;  // bytes after them
-            uint32_t rw[kSlotWords];
+            // One word past the slot (the next slot's first, or padding), for
+            // the byte shift of the last whole word.
+            uint32_t rw[kSlotWords + 1];
             const uint32_t* slot_w = reinterpret_cast<const uint32_t*>(slot);
 #pragma unroll
-            for (uint32_t j = 0; j < kSlotWords; ++j) rw[j] = slot_w[j];
+            for (uint32_t j = 0; j < kSlotWords + 1; ++j) rw[j] = slot_w[j];
             const uint32_t tv = get_u32(slot + head + 4 * nbody);
             __syncthreads();
             uint8_t* dst = stage + dpos;
@@ -889,7 +993,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 if (k < head) dst[k] = static_cast<uint8_t>(rw[0] >> (8 * k));
             uint32_t* body = reinterpret_cast<uint32_t*>(dst + head);
 #pragma unroll
-            for (uint32_t j = 0; j + 1 < kSlotWords; ++j)
+            for (uint32_t j = 0; j < kSlotWords; ++j)
                 if (j < nbody) body[j] = __builtin_amdgcn_alignbyte(rw[j + 1], rw[j], head);
             uint8_t* tl = dst + head + 4 * nbody;
 #pragma unroll

@@ -73,6 +73,7 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
     // Walk the spans: an entry of length l starts an aligned run of
     // 2^(max_bits - l) identical entries (the windows sharing its prefix).
     uint32_t min_len = 0;
+    uint8_t len_of[256] = {0};
     for (uint32_t i = 0; i < size;) {
         const uint32_t l = static_cast<uint32_t>(len_lut[i]);
         if (l == 0) {
@@ -91,13 +92,20 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
                                 " breaks the prefix span of entry " + std::to_string(i) +
                                 " (not a prefix-code LUT)");
         if (min_len == 0 || l < min_len) min_len = l;
+        const uint32_t sym = static_cast<uint32_t>(sym_lut[i]);
+        if (len_of[sym] != 0 && len_of[sym] != l)
+            return fail(AIMG_ERR_BAD_TABLE, "symbol " + std::to_string(sym) +
+                                                " has codes of two lengths (a Huffman LUT "
+                                                "gives each symbol one codeword)");
+        len_of[sym] = static_cast<uint8_t>(l);
         i += span;
     }
 
     auto* blob = static_cast<uint8_t*>(out);
     std::memset(blob, 0, need);
     auto* wsyms = reinterpret_cast<uint32_t*>(blob + aimg::kSymsOffset);
-    auto* wmeta = reinterpret_cast<uint16_t*>(blob + aimg::kMetaOffset);
+    auto* wmeta = blob + aimg::kMetaOffset;
+    std::memcpy(blob + aimg::kLenOffset, len_of, sizeof(len_of));
     auto* esc = reinterpret_cast<uint16_t*>(blob + aimg::kEscOffset);
     // (symbol, length) of the codeword starting at the first bit of `bits`
     // (MSB-first, zeros past the window).
@@ -109,7 +117,7 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
     uint32_t n_blocks = 0;
     for (uint32_t w = 0; w < static_cast<uint32_t>(aimg::kWinEntries); ++w) {
         const uint32_t bits = w << (32 - aimg::kWinBits);
-        uint32_t pos = 0, mask = 0, k = 0;
+        uint32_t pos = 0, k = 0;
         uint32_t syms = 0;
         while (k < static_cast<uint32_t>(aimg::kMaxSymsPerWindow)) {
             uint32_t s, l;
@@ -118,11 +126,10 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
             syms |= s << (8 * k);
             ++k;
             pos += l;
-            mask |= 1u << (pos - 1);
         }
         if (k > 0) {
             wsyms[w] = syms;
-            wmeta[w] = static_cast<uint16_t>(mask | (pos << 12));
+            wmeta[w] = static_cast<uint8_t>(pos | (k << 4));
             continue;
         }
         // Escape window: one entry per value of the next four bits.

@@ -8,18 +8,21 @@
 
 namespace aimg {
 
-constexpr int kAbiVersion = 4;
+constexpr int kAbiVersion = 5;
 constexpr uint32_t kTableMagic = 0x474D4941u;  // "AIMG"
 
 // Window table: for each 12-bit window, the codewords that lie wholly inside
 // it when read one after another from its first bit (at most
 // kMaxSymsPerWindow), in two arrays:
 //   syms (uint32): the symbols, symbol j in bits 8j..8j+7 (unused bytes zero)
-//   meta (uint16): bits 0..11 end mask (bit k-1 set when a codeword ends at
-//                  offset k), bits 12..15 total bits those codewords take
+//   meta (uint8):  bits 0..3 total bits those codewords take, bits 4..6 their
+//                  number
 // Total 0 marks an escape window, whose first codeword is longer than 12
 // bits or unused; its syms entry then holds the index of its escape block,
 // or kUnusedBlock when the stored LUT has no codeword there.
+// A 256-entry table gives each symbol's code length (every symbol of the
+// stored LUT has one length), from which the codeword boundaries inside a
+// window are rebuilt where a segment ends.
 constexpr int kWinBits = 12;
 constexpr int kWinEntries = 1 << kWinBits;
 constexpr int kMaxSymsPerWindow = 4;
@@ -46,7 +49,8 @@ static_assert(sizeof(TableHeader) == 64, "header is 64 bytes");
 
 constexpr size_t kSymsOffset = 64;
 constexpr size_t kMetaOffset = kSymsOffset + sizeof(uint32_t) * kWinEntries;
-constexpr size_t kEscOffset = kMetaOffset + sizeof(uint16_t) * kWinEntries;
+constexpr size_t kLenOffset = kMetaOffset + sizeof(uint8_t) * kWinEntries;
+constexpr size_t kEscOffset = kLenOffset + 256;
 
 // Fixed blob size: room for the largest possible escape-block count.
 inline size_t table_nbytes() {

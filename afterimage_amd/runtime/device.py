@@ -130,7 +130,7 @@ class DeviceTensor:
         """Bytes one bf16 decode must move: chunk bitstreams, offsets and
         lengths, sign/mantissa read, window table, and the bf16 write."""
         return (int(self.chunk_nbytes.sum().item()) + 8 * self.n_chunks
-                + self.n_symbols + 6 * 4096 + 2 * self.n_symbols)
+                + self.n_symbols + (5 * 4096 + 256) + 2 * self.n_symbols)
 
     @classmethod
     def from_encoded(cls, enc, sign_mantissa, device, tables: DecodeTables | None = None):

@@ -235,7 +235,7 @@ def _bench_gemv(args) -> int:
     n = enc.n_symbols
     chunk_bytes = int(enc.chunk_nbytes.astype(np.int64).sum())
     # bitstreams + offsets/lengths + sign/mantissa + table + x read + y read/write
-    algo_bytes = chunk_bytes + 8 * enc.n_chunks + n + 6 * 4096 + 2 * b * cols + 8 * b * rows
+    algo_bytes = chunk_bytes + 8 * enc.n_chunks + n + (5 * 4096 + 256) + 2 * b * cols + 8 * b * rows
     rec = {
         "metric": "fused decode->GEMV weight GB/s (bf16 bytes consumed per second)",
         "value": round(2 * n * args.steps / wall / 1e9, 2),
@@ -373,7 +373,7 @@ def main() -> int:
     chunk_bytes = sum(int(l.encoded.chunk_nbytes.astype(np.int64).sum()) for l in layers)
     n_tables = len({dt.tables.key for dt in dts})
     # bitstreams + offsets and lengths + sign/mantissa + window tables + bf16 write
-    algo_bytes = chunk_bytes + 8 * n_chunks + n + 6 * 4096 * n_tables + 2 * n
+    algo_bytes = chunk_bytes + 8 * n_chunks + n + (5 * 4096 + 256) * n_tables + 2 * n
     achieved = algo_bytes / kernel_s / 1e9
     value = 2 * n * args.steps / wall / 1e9
     traffic = _traffic(config_key)

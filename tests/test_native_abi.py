@@ -43,7 +43,7 @@ def test_abi_version_and_error_channel():
     assert lib.aimg_table_nbytes(17, ctypes.byref(n)) == _native.AIMG_ERR_INVALID_ARGUMENT
     assert b"max_bits" in lib.aimg_last_error()
     assert lib.aimg_table_nbytes(16, ctypes.byref(n)) == _native.AIMG_OK
-    assert n.value == 64 + 4 * 4096 + 2 * 4096 + 2 * 16 * 256
+    assert n.value == 64 + 4 * 4096 + 4096 + 256 + 2 * 16 * 256
 
 
 def test_decode_entry_points_validate_before_launching():
@@ -86,6 +86,14 @@ def test_gemv_entry_point_validates_before_launching():
     arr[0].n_symbols = 1 << 31
     arr[0].n_chunks = 1 << 27
     assert lib.aimg_decode_bf16(arr, 1, None) == _native.AIMG_ERR_UNSUPPORTED
+
+
+def test_table_builder_rejects_a_symbol_with_two_code_lengths():
+    # A valid prefix code, but symbol 5 has codes "0" and "10".
+    sym = np.array([5, 5, 5, 6], np.int32)
+    ln = np.array([1, 1, 2, 2], np.int8)
+    with pytest.raises(_native.NativeError, match="two lengths"):
+        build_table_blob(sym, ln, 2)
 
 
 def test_table_builder_rejects_wide_symbols():
@@ -162,8 +170,11 @@ def test_window_table_matches_canonical_code(name):
     assert hdr[4] == enc.sym_lut[0]
     n_blocks = int(hdr[6])
     wsyms = blob[64: 64 + 4 * 4096].view(np.uint32)
-    wmeta = blob[64 + 4 * 4096: 64 + 6 * 4096].view(np.uint16)
-    esc = blob[64 + 6 * 4096:].view(np.uint16)
+    wmeta = blob[64 + 4 * 4096: 64 + 5 * 4096]
+    len_of = blob[64 + 5 * 4096: 64 + 5 * 4096 + 256]
+    esc = blob[64 + 5 * 4096 + 256:].view(np.uint16)
+    for sym in range(256):
+        assert int(len_of[sym]) == lengths.get(sym, 0)
     long_prefixes = {codes_prefix for codes_prefix in range(4096)
                      if (fc := _first_codeword(lengths, codes_prefix << 4)) is not None
                      and fc[1] > WIN_BITS}
@@ -173,12 +184,12 @@ def test_window_table_matches_canonical_code(name):
     for w in sorted(windows):
         want = _window_expectation(lengths, w)
         ent = int(wsyms[w])
-        total = int(wmeta[w]) >> 12
-        ends = int(wmeta[w]) & 0xFFF
+        total = int(wmeta[w]) & 15
+        count = int(wmeta[w]) >> 4
         if not want:
             # Escape window: its block gives the first codeword for every
             # value of the next four bits.
-            assert total == 0 and ends == 0
+            assert total == 0 and count == 0
             blk = ent & 0xFFFF
             if w not in long_prefixes:
                 assert blk == 0xFFFF
@@ -195,11 +206,7 @@ def test_window_table_matches_canonical_code(name):
         got = [(ent >> (8 * j)) & 0xFF for j in range(len(want))]
         assert got == want
         assert ent >> (8 * len(want)) == 0
-        pos, mask = 0, 0
-        for s in want:
-            pos += lengths[s]
-            mask |= 1 << (pos - 1)
-        assert ends == mask and total == pos
+        assert count == len(want) and total == sum(lengths[s] for s in want)
 
 
 @pytest.mark.parametrize("name", case_names())
