@@ -1,0 +1,74 @@
+// Runs the CPU build of the decode kernel on one case directory written by
+// tests/test_kernel_emulation.py: decode <dir> <u8|bf16>. Every device buffer
+// is a heap block of exactly its size, so AddressSanitizer reports any access
+// past it.
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+#include "afterimage_decode.h"
+
+static std::vector<uint8_t> readf(const std::string& p) {
+    FILE* f = fopen(p.c_str(), "rb");
+    if (!f) { fprintf(stderr, "missing %s\n", p.c_str()); exit(2); }
+    std::vector<uint8_t> v;
+    uint8_t buf[65536];
+    size_t n;
+    while ((n = fread(buf, 1, sizeof buf, f)) > 0) v.insert(v.end(), buf, buf + n);
+    fclose(f);
+    return v;
+}
+template <typename T> static T* exact(const std::vector<uint8_t>& v, size_t align = 16) {
+    void* p = nullptr;
+    if (posix_memalign(&p, align, v.size() ? v.size() : 1)) exit(3);
+    if (!v.empty()) memcpy(p, v.data(), v.size());
+    return static_cast<T*>(p);
+}
+int main(int argc, char** argv) {
+    const std::string d = argv[1];
+    const bool bf16 = std::string(argv[2]) == "bf16";
+    long long meta[4];
+    FILE* m = fopen((d + "/meta.txt").c_str(), "r");
+    if (fscanf(m, "%lld %lld %lld %lld", &meta[0], &meta[1], &meta[2], &meta[3]) != 4) return 2;
+    fclose(m);
+    const int max_bits = (int)meta[0], chunk_size = (int)meta[1];
+    const long long n_symbols = meta[2], n_chunks = meta[3];
+    auto packed = readf(d + "/packed.bin"), offs = readf(d + "/offsets.bin"), nbs = readf(d + "/nbytes.bin");
+    auto slut = readf(d + "/sym_lut.bin"), llut = readf(d + "/len_lut.bin"), expect = readf(d + "/expect.bin");
+    size_t tn = 0;
+    if (aimg_table_nbytes(max_bits, &tn)) return 4;
+    void* table = nullptr;
+    if (posix_memalign(&table, 256, tn)) return 3;
+    if (aimg_build_table((const int32_t*)slut.data(), (const int8_t*)llut.data(), max_bits, table, tn)) {
+        fprintf(stderr, "build_table: %s\n", aimg_last_error());
+        return 5;
+    }
+    aimg_tensor t{};
+    t.packed = exact<uint8_t>(packed);
+    t.chunk_offsets = exact<int32_t>(offs);
+    t.chunk_nbytes = exact<int32_t>(nbs);
+    t.table = table;
+    t.packed_nbytes = (int64_t)packed.size();
+    t.n_symbols = n_symbols;
+    t.chunk_size = chunk_size;
+    t.n_chunks = (int32_t)n_chunks;
+    std::vector<uint8_t> outv(n_symbols * (bf16 ? 2 : 1));
+    void* out = exact<uint8_t>(outv);
+    memset(out, 0xAB, outv.size());
+    t.out = out;
+    int rc;
+    if (bf16) {
+        auto sm = readf(d + "/sm.bin");
+        t.sign_mantissa = exact<uint8_t>(sm);
+        rc = aimg_decode_bf16(&t, 1, nullptr);
+    } else {
+        rc = aimg_decode_u8(&t, 1, nullptr);
+    }
+    if (rc) { fprintf(stderr, "decode rc=%d: %s\n", rc, aimg_last_error()); return 6; }
+    if (expect.size() != outv.size()) { fprintf(stderr, "size mismatch\n"); return 7; }
+    size_t bad = 0;
+    for (size_t k = 0; k < outv.size(); ++k) bad += ((const uint8_t*)out)[k] != expect[k];
+    printf("%s %s: %s (%zu bad bytes of %zu)\n", d.c_str(), argv[2], bad ? "MISMATCH" : "ok", bad, outv.size());
+    return bad ? 1 : 0;
+}

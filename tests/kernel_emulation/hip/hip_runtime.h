@@ -1,0 +1,200 @@
+// CPU stand-in for the HIP device subset used by aimg_decode.hip, so that the
+// kernel source can be compiled for the host under AddressSanitizer and run
+// on small inputs: every out-of-bounds access of a global buffer or of the
+// LDS block is then reported with its source line. Test infrastructure only.
+//
+// Model: a block runs as one std::thread per work-item; blocks run one after
+// another; __shared__ data are function statics (one block at a time).
+// __syncthreads is a block barrier. Wave shuffles exchange values through a
+// per-wave buffer between per-wave barriers, so they must be reached by all
+// 64 lanes (the kernel calls them in uniform control flow only). Ballot
+// returns the calling lane's own bit: the kernel uses it as "does any lane
+// need this?", for which the per-lane answer gives the same results
+// (the fused GEMV path relies on true wave ballots and is not modelled).
+#pragma once
+#include <barrier>
+#include <cstdint>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __launch_bounds__(...)
+#define __shared__ static
+
+struct dim3 {
+    unsigned x, y, z;
+    dim3(unsigned a = 1, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
+};
+struct EmuIdx {
+    unsigned x, y, z;
+};
+inline thread_local EmuIdx threadIdx{0, 0, 0};
+inline thread_local EmuIdx blockIdx{0, 0, 0};
+inline EmuIdx gridDim{1, 1, 1};
+inline EmuIdx blockDim{1, 1, 1};
+
+typedef int hipError_t;
+enum { hipSuccess = 0 };
+typedef void* hipStream_t;
+enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 0 };
+inline hipError_t hipGetDevice(int* d) { *d = 0; return hipSuccess; }
+inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) { *v = 256; return hipSuccess; }
+inline hipError_t hipGetLastError() { return hipSuccess; }
+inline const char* hipGetErrorString(hipError_t) { return "cpu"; }
+
+namespace emu {
+struct Block {
+    unsigned n;
+    std::barrier<> bar;
+    std::vector<std::barrier<>*> wave;
+    std::vector<uint64_t> xbuf;
+    std::vector<int> flags;
+    explicit Block(unsigned n_) : n(n_), bar(n_), xbuf(n_), flags(n_) {
+        for (unsigned w = 0; w * 64 < n; ++w)
+            wave.push_back(new std::barrier<>(n - 64 * w < 64 ? n - 64 * w : 64));
+    }
+    ~Block() {
+        for (auto* b : wave) delete b;
+    }
+};
+inline Block* g_block = nullptr;
+inline unsigned lane() { return threadIdx.x & 63u; }
+
+template <typename T>
+inline T wave_xchg(T v, unsigned src) {
+    Block& B = *g_block;
+    const unsigned w = threadIdx.x >> 6;
+    uint64_t bits = 0;
+    std::memcpy(&bits, &v, sizeof(T));
+    B.wave[w]->arrive_and_wait();
+    B.xbuf[threadIdx.x] = bits;
+    B.wave[w]->arrive_and_wait();
+    const uint64_t r = B.xbuf[w * 64 + src];
+    B.wave[w]->arrive_and_wait();
+    T out;
+    std::memcpy(&out, &r, sizeof(T));
+    return out;
+}
+}  // namespace emu
+
+inline void __syncthreads() { emu::g_block->bar.arrive_and_wait(); }
+inline int __syncthreads_or(int p) {
+    emu::Block& B = *emu::g_block;
+    B.bar.arrive_and_wait();
+    B.flags[threadIdx.x] = p != 0;
+    B.bar.arrive_and_wait();
+    int r = 0;
+    for (unsigned k = 0; k < B.n; ++k) r |= B.flags[k];
+    B.bar.arrive_and_wait();
+    return r;
+}
+template <typename T>
+inline T __shfl_up(T v, unsigned d, int = 64) {
+    const unsigned l = emu::lane();
+    const T r = emu::wave_xchg(v, l >= d ? l - d : l);
+    return l >= d ? r : v;
+}
+template <typename T>
+inline T __shfl_xor(T v, int m, int = 64) { return emu::wave_xchg(v, emu::lane() ^ (unsigned)m); }
+
+inline uint64_t __builtin_amdgcn_ballot_w64(bool p) { return p ? (1ull << emu::lane()) : 0ull; }
+// Same signatures as the compiler builtins (int in, int out).
+inline int __builtin_amdgcn_readfirstlane(int v) { return v; }
+inline int __builtin_amdgcn_readlane(int v, int) { return v; }
+inline uint32_t __builtin_amdgcn_alignbyte(uint32_t a, uint32_t b, uint32_t s) {
+    return (uint32_t)((((uint64_t)a << 32) | b) >> (8 * (s & 3)));
+}
+// v_perm_b32: selector bytes 0..7 pick a byte of {a, b} (b is bytes 0..3),
+// 8..11 replicate the top bit of byte 1, 3, 5 or 7, 12 gives 0x00, 13.. 0xFF.
+inline uint32_t __builtin_amdgcn_perm(uint32_t a, uint32_t b, uint32_t sel) {
+    const uint64_t x = ((uint64_t)a << 32) | b;
+    uint32_t r = 0;
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t s = (sel >> (8 * k)) & 0xFF;
+        uint32_t byte;
+        if (s < 8) byte = (x >> (8 * s)) & 0xFF;
+        else if (s < 12) byte = ((x >> (16 * (s - 8) + 15)) & 1) ? 0xFF : 0x00;
+        else if (s == 12) byte = 0;
+        else byte = 0xFF;
+        r |= byte << (8 * k);
+    }
+    return r;
+}
+// Raw buffer resource: loads at or past num_records bytes read as zero.
+struct __amdgpu_buffer_rsrc_t {
+    const uint8_t* base;
+    uint32_t n;
+};
+inline __amdgpu_buffer_rsrc_t __builtin_amdgcn_make_buffer_rsrc(void* p, short, int n, int) {
+    return {static_cast<const uint8_t*>(p), (uint32_t)n};
+}
+inline uint32_t emu_dword(const __amdgpu_buffer_rsrc_t& r, uint64_t off) {
+    if (off + 4 > r.n) return 0;
+    uint32_t v;
+    std::memcpy(&v, r.base + off, 4);
+    return v;
+}
+inline uint32_t __builtin_amdgcn_raw_buffer_load_b32(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, int) {
+    return emu_dword(r, (uint64_t)vo + so);
+}
+typedef uint32_t emu_u32x2 __attribute__((ext_vector_type(2)));
+inline emu_u32x2 __builtin_amdgcn_raw_buffer_load_b64(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, int) {
+    const uint64_t off = (uint64_t)vo + so;
+    emu_u32x2 v;
+    v[0] = off + 8 > r.n ? 0u : emu_dword(r, off);
+    v[1] = off + 8 > r.n ? 0u : emu_dword(r, off + 4);
+    return v;
+}
+#ifndef __HIP_MEMORY_SCOPE_WORKGROUP
+#define __HIP_MEMORY_SCOPE_WORKGROUP 3
+#endif
+struct uint2 {
+    uint32_t x, y;
+};
+struct __attribute__((aligned(16))) uint4 {
+    uint32_t x, y, z, w;
+};
+inline uint2 make_uint2(uint32_t a, uint32_t b) { return {a, b}; }
+inline float __uint_as_float(uint32_t v) {
+    float f;
+    std::memcpy(&f, &v, 4);
+    return f;
+}
+inline float atomicAdd(float* p, float v) {
+    uint32_t* q = reinterpret_cast<uint32_t*>(p);
+    uint32_t o = __atomic_load_n(q, __ATOMIC_RELAXED);
+    for (;;) {
+        float f;
+        std::memcpy(&f, &o, 4);
+        const float g = f + v;
+        uint32_t n;
+        std::memcpy(&n, &g, 4);
+        if (__atomic_compare_exchange_n(q, &o, n, false, __ATOMIC_RELAXED, __ATOMIC_RELAXED)) return f;
+    }
+}
+inline int __ffs(int x) { return __builtin_ffs(x); }
+
+template <typename K, typename... A>
+inline void emu_launch(K kernel, dim3 g, dim3 b, A... args) {
+    gridDim = {g.x, 1, 1};
+    blockDim = {b.x, 1, 1};
+    for (unsigned blk = 0; blk < g.x; ++blk) {
+        emu::Block B(b.x);
+        emu::g_block = &B;
+        std::vector<std::thread> th;
+        th.reserve(b.x);
+        for (unsigned t = 0; t < b.x; ++t)
+            th.emplace_back([=] {
+                threadIdx = {t, 0, 0};
+                blockIdx = {blk, 0, 0};
+                kernel(args...);
+            });
+        for (auto& x : th) x.join();
+        emu::g_block = nullptr;
+    }
+}
+#define hipLaunchKernelGGL(K, G, B, SH, S, ...) emu_launch(K, G, B, __VA_ARGS__)

@@ -1,0 +1,129 @@
+"""The decode kernel's own source, compiled for the host under AddressSanitizer
+(tests/kernel_emulation/hip/hip_runtime.h stands in for the HIP device
+subset it uses) and run on small cases of every kernel variant: the scalar
+and vector store paths, 16..512 threads per chunk, two-round 64Ki chunks,
+escape blocks beyond the LDS share, and the tiny-buffer kernel.
+
+This checks memory safety on the CPU before any GPU run: each device buffer
+is a heap block of exactly its size, so an access past any of them, or past
+the kernel's LDS block, fails the run with the offending source line. The
+outputs are compared with the known weights / exponents as well. The fused
+GEMV mode depends on true wave ballots and is covered by the GPU tests.
+"""
+import os
+import re
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from afterimage_amd import workloads
+from afterimage_amd.runtime.compressed_store import compress_layer
+from afterimage_amd.runtime.huffman_chunked import encode_chunked
+from tests.distributions import many_escape_windows
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CXX = "/opt/rocm/llvm/bin/clang++"
+
+pytestmark = pytest.mark.skipif(not os.path.exists(CXX), reason="needs ROCm's clang++ for the host build")
+
+
+@pytest.fixture(scope="module")
+def emu(tmp_path_factory):
+    d = tmp_path_factory.mktemp("kernel_emulation")
+    src = open(os.path.join(ROOT, "afterimage_amd", "csrc", "aimg_decode.hip")).read()
+    # Host spelling of two device-only constructs: address-space qualifiers
+    # and VGPR asm operands.
+    src = re.sub(r"__attribute__\(\(address_space\(\d+\)\)\)", "", src)
+    src = src.replace('"+v"', '"+r"').replace('::"v"', '::"r"')
+    (d / "aimg_decode_emu.cpp").write_text(src)
+    flags = ["-std=c++20", "-g", "-O1", "-fsanitize=address", "-fno-omit-frame-pointer",
+             "-I", os.path.join(HERE, "kernel_emulation"), "-I", os.path.join(ROOT, "include"),
+             "-I", os.path.join(ROOT, "afterimage_amd", "csrc"), "-w"]
+    objs = []
+    for s in (str(d / "aimg_decode_emu.cpp"), os.path.join(ROOT, "afterimage_amd", "csrc", "aimg_host.cpp"),
+              os.path.join(HERE, "kernel_emulation", "driver.cpp")):
+        o = str(d / (os.path.basename(s) + ".o"))
+        subprocess.run([CXX, *flags, "-c", s, "-o", o], check=True)
+        objs.append(o)
+    exe = str(d / "emu")
+    subprocess.run([CXX, "-fsanitize=address", "-o", exe, *objs, "-lpthread"], check=True)
+    yield exe, d
+    shutil.rmtree(d, ignore_errors=True)
+
+
+def _write(d, enc, expect, sm=None):
+    os.makedirs(d, exist_ok=True)
+    np.asarray(enc.packed, np.uint8).tofile(os.path.join(d, "packed.bin"))
+    np.asarray(enc.chunk_offsets, np.int32).tofile(os.path.join(d, "offsets.bin"))
+    np.asarray(enc.chunk_nbytes, np.int32).tofile(os.path.join(d, "nbytes.bin"))
+    np.asarray(enc.sym_lut, np.int32).tofile(os.path.join(d, "sym_lut.bin"))
+    np.asarray(enc.len_lut, np.int8).tofile(os.path.join(d, "len_lut.bin"))
+    np.ascontiguousarray(expect).view(np.uint8).tofile(os.path.join(d, "expect.bin"))
+    if sm is not None:
+        np.asarray(sm, np.uint8).tofile(os.path.join(d, "sm.bin"))
+    with open(os.path.join(d, "meta.txt"), "w") as f:
+        f.write("%d %d %d %d\n" % (enc.max_bits, enc.chunk_size, enc.n_symbols, len(enc.chunk_offsets)))
+
+
+def _run(emu, name, mode):
+    exe, d = emu
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0")
+    r = subprocess.run([exe, str(d / name), mode], capture_output=True, text=True, env=env, timeout=600)
+    assert r.returncode == 0 and ": ok" in r.stdout, (r.stdout + r.stderr)[-4000:]
+
+
+def _u8(emu, name, exps, chunk_size):
+    exps = np.asarray(exps)
+    enc = encode_chunked(torch.as_tensor(exps), chunk_size=chunk_size)
+    _write(emu[1] / name, enc, exps.astype(np.uint8))
+    _run(emu, name, "u8")
+
+
+def _bf16(emu, name, W, chunk_size):
+    layer = compress_layer(W, chunk_size=chunk_size)
+    _write(emu[1] / name, layer.encoded, W.reshape(-1).view(torch.int16).numpy(),
+           layer.sign_mantissa.numpy())
+    _run(emu, name, "bf16")
+
+
+def test_u8_small_chunks_16_threads_per_chunk(emu):
+    torch.manual_seed(0)
+    _u8(emu, "skewed64", torch.randint(100, 140, (2000,)).numpy(), 64)
+
+
+@pytest.mark.parametrize("chunk_size", [32, 256, 1024])
+def test_u8_chunk_sizes(emu, chunk_size):
+    torch.manual_seed(3)
+    _u8(emu, "sizes%d" % chunk_size, torch.randint(50, 90, (10000,)).numpy(), chunk_size)
+
+
+def test_u8_full_alphabet(emu):
+    torch.manual_seed(1)
+    _u8(emu, "uniform256", torch.randint(0, 256, (8000,)).numpy(), 256)
+
+
+def test_u8_escape_blocks_beyond_the_lds_share(emu):
+    _u8(emu, "escapes", many_escape_windows(seed=5, n=30000), 4096)
+
+
+def test_u8_tiny_packed_buffer(emu):
+    _u8(emu, "tiny", np.array([7, 7, 7], np.uint8), 64)
+
+
+def test_bf16_vector_path(emu):
+    torch.manual_seed(2)
+    _bf16(emu, "bf16_vec", (torch.randn(256, 1024) * 0.02).to(torch.bfloat16), 4096)
+
+
+def test_bf16_scalar_path_ragged(emu):
+    torch.manual_seed(4)
+    _bf16(emu, "bf16_ragged", (torch.randn(300, 333) * 0.02).to(torch.bfloat16), 1000)
+
+
+def test_bf16_two_round_64k_chunks_with_outliers(emu):
+    W = workloads.bf16_normal((64, 17408), 2, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "bf16_64k", W, 65536)
