@@ -568,15 +568,37 @@ __device__ __forceinline__ void fetch_commit(const Fetch& F, const LaunchArgs& a
     }
 }
 
+// Cross-lane moves through DPP (data-parallel primitives: the VALU reads a
+// neighbour lane's operand), with no LDS round trip. Lanes whose source lies
+// outside the pattern, or whose row is masked off, read 0. Controls:
+// row_shr:n = 0x110 + n (within rows of 16 lanes), wave_shr:1 = 0x138,
+// row_bcast:15 = 0x142 (lane 15 of each row to the next row), row_bcast:31 =
+// 0x143 (lane 31 to rows 2 and 3).
+template <int kCtrl, int kRowMask = 0xF>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, kRowMask, 0xF, true));
+}
+
+// Inclusive prefix sum of v over the wave (every lane active).
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
+    uint32_t x = v;
+    x += dpp<0x111>(x);
+    x += dpp<0x112>(x);
+    x += dpp<0x114>(x);
+    x += dpp<0x118>(x);
+    x += dpp<0x142, 0xA>(x);
+    x += dpp<0x143, 0xC>(x);
+    return x;
+}
+
+// v of the lane below (0 in lane 0; every lane active).
+__device__ __forceinline__ uint32_t lane_below(uint32_t v) { return dpp<0x138>(v); }
+
 __device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* s_wsum) {
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
-    uint32_t x = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t y = __shfl_up(x, d, 64);
-        if (lane >= d) x += y;
-    }
+    const uint32_t x = wave_scan_incl(v);
     if (lane == 63) s_wsum[w] = x;
     __syncthreads();
     uint32_t pre = 0;
@@ -940,7 +962,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const uint32_t lane = tid & 63u;
             const uint32_t wprev = ((tid >> 6) - 1u) & (kWaves - 1u);
             for (;;) {
-                uint32_t ep = __shfl_up(e, 1, 64);
+                uint32_t ep = lane_below(e);
                 if (lane == 63) s_ewave[tid >> 6] = e;
                 __syncthreads();
                 if (lane == 0) ep = s_ewave[wprev];

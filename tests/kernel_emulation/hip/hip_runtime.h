@@ -100,6 +100,24 @@ inline T __shfl_up(T v, unsigned d, int = 64) {
 }
 template <typename T>
 inline T __shfl_xor(T v, int m, int = 64) { return emu::wave_xchg(v, emu::lane() ^ (unsigned)m); }
+template <typename T>
+inline T __shfl(T v, int src, int = 64) { return emu::wave_xchg(v, (unsigned)src & 63u); }
+
+// DPP move, for the controls the kernel uses: row_shr:1..15 (0x111..0x11F),
+// wave_shr:1 (0x138), row_bcast:15 (0x142), row_bcast:31 (0x143).
+inline int __builtin_amdgcn_update_dpp(int old, int src, int ctrl, int row_mask, int, bool bound_ctrl) {
+    const int l = (int)emu::lane(), row = l >> 4;
+    int from = -1;
+    if (ctrl >= 0x111 && ctrl <= 0x11F) from = (l & 15) >= ctrl - 0x110 ? l - (ctrl - 0x110) : -1;
+    else if (ctrl == 0x138) from = l - 1;
+    else if (ctrl == 0x142) from = row >= 1 ? 16 * row - 1 : -1;
+    else if (ctrl == 0x143) from = row >= 2 ? 31 : -1;
+    else __builtin_trap();
+    const int v = emu::wave_xchg(src, from >= 0 ? (unsigned)from : (unsigned)l);
+    if (!((row_mask >> row) & 1)) return old;
+    if (from < 0) return bound_ctrl ? 0 : old;
+    return v;
+}
 
 inline uint64_t __builtin_amdgcn_ballot_w64(bool p) { return p ? (1ull << emu::lane()) : 0ull; }
 // Same signatures as the compiler builtins (int in, int out).
