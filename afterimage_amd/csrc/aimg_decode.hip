@@ -842,6 +842,7 @@ struct __attribute__((aligned(16))) Lds {
     uint32_t wsyms[kWinEntries];
     uint32_t wsum[kWaves];
     uint32_t gpre[kMaxGroups + 1];
+    uint32_t wbad[kWaves];  // some thread of the wave disagrees with its predecessor
     uint32_t gval[kMaxGroups];
     uint32_t ewave[kWaves];      // segment end of each wave's last lane
     uint32_t glast[kMaxGroups];  // segment end of each sub-group's last active thread
@@ -863,6 +864,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     uint32_t* const s_glast = lds.glast;
     uint32_t* const s_wsum = lds.wsum;
     uint32_t* const s_gpre = lds.gpre;
+    uint32_t* const s_wbad = lds.wbad;
     uint32_t* const s_gval = lds.gval;
 
     const uint32_t tid = threadIdx.x;
@@ -959,15 +961,23 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             // A segment is right when it starts where its predecessor's last
             // codeword ends. The predecessor's end comes from the lane below;
             // a wave's lane 0 reads the previous wave's lane 63 through LDS.
+            // Whether any thread disagrees goes through one flag per wave.
             const uint32_t lane = tid & 63u;
-            const uint32_t wprev = ((tid >> 6) - 1u) & (kWaves - 1u);
+            const uint32_t w = tid >> 6;
+            const uint32_t wprev = (w - 1u) & (kWaves - 1u);
             for (;;) {
                 uint32_t ep = lane_below(e);
-                if (lane == 63) s_ewave[tid >> 6] = e;
+                if (lane == 63) s_ewave[w] = e;
                 __syncthreads();
                 if (lane == 0) ep = s_ewave[wprev];
                 const bool bad = active && i > 0 && f != ep;
-                if (!__syncthreads_or(bad)) break;
+                const bool wave_bad = __ballot(bad) != 0;
+                if (lane == 0) s_wbad[w] = wave_bad;
+                __syncthreads();
+                bool any_bad = false;
+#pragma unroll
+                for (uint32_t k = 0; k < kWaves; ++k) any_bad |= s_wbad[k] != 0;
+                if (!any_bad) break;
                 if (bad) {
                     f = ep;
                     clear_slot(slot);

@@ -119,6 +119,14 @@ inline int __builtin_amdgcn_update_dpp(int old, int src, int ctrl, int row_mask,
     return v;
 }
 
+// HIP's wave ballot, used by the kernel where every lane of the wave takes
+// part: the real OR over the wave's lanes.
+inline unsigned long long __ballot(int p) {
+    uint64_t m = 0;
+    for (unsigned k = 0; k < 64; ++k) m |= (uint64_t)(emu::wave_xchg(p != 0 ? 1 : 0, k) != 0) << k;
+    return m;
+}
+
 inline uint64_t __builtin_amdgcn_ballot_w64(bool p) { return p ? (1ull << emu::lane()) : 0ull; }
 // Same signatures as the compiler builtins (int in, int out).
 inline int __builtin_amdgcn_readfirstlane(int v) { return v; }

@@ -177,3 +177,14 @@ def test_whole_chunk_decode_with_padding_across_rounds():
     sub = _slice_encoded(enc, 0, enc.n_chunks)
     gpu = decode_gpu_v2(sub).cpu().numpy()
     assert np.array_equal(gpu, oracle.decode_chunks(sub))
+
+
+def test_segment_guesses_all_wrong():
+    # Eight equiprobable symbols get 3-bit codes. Segment starts are multiples
+    # of 168 bits and the 32-bit lead-in before each lands one bit past a
+    # codeword boundary, which fixed-length codes never leave: every thread but
+    # the first of each round is wrong on its first pass, and the output rests
+    # on the re-decode from the predecessor's end (up to one pass per thread).
+    rng = np.random.default_rng(8)
+    _check(rng.integers(0, 8, 20000), chunk_size=4096)
+    _check(rng.integers(0, 8, 70000), chunk_size=65536)

@@ -127,3 +127,14 @@ def test_bf16_scalar_path_ragged(emu):
 def test_bf16_two_round_64k_chunks_with_outliers(emu):
     W = workloads.bf16_normal((64, 17408), 2, 0.02, outlier_frac=1e-3)
     _bf16(emu, "bf16_64k", W, 65536)
+
+
+def test_u8_segment_guesses_all_wrong(emu):
+    # Eight equiprobable symbols get 3-bit codes; segment starts are multiples
+    # of 168 bits, and the 32-bit lead-in before each lands one bit past a
+    # codeword boundary, which fixed-length codes never leave. Every thread
+    # but the first is wrong on its first pass, so the result rests entirely
+    # on the re-decode from the predecessor's end.
+    rng = np.random.default_rng(8)
+    _u8(emu, "guess4096", rng.integers(0, 8, 20000), 4096)
+    _u8(emu, "guess65536", rng.integers(0, 8, 70000), 65536)
