@@ -416,9 +416,10 @@ __device__ __forceinline__ uint32_t load_bytes(const uint8_t* cbytes, int64_t nb
 }
 
 // Big-endian stream word with the bytes at or past the chunk end zeroed.
-__device__ __forceinline__ uint32_t be_word(uint32_t v, int64_t nb, int64_t b) {
-    const int64_t left = nb - b;
-    if (left <= 0) return 0u;
+// (Chunk byte offsets and lengths are below 2^31.)
+__device__ __forceinline__ uint32_t be_word(uint32_t v, uint32_t nb, uint32_t b) {
+    if (b >= nb) return 0u;
+    const uint32_t left = nb - b;
     if (left < 4) v &= (1u << (8 * left)) - 1u;
     return __builtin_bswap32(v);
 }
@@ -558,6 +559,12 @@ __device__ __forceinline__ void fetch_commit(const Fetch& F, const LaunchArgs& a
         if (j >= nw) continue;
         const uint32_t b = b0 + 4 * j;
         uint32_t v = F.raw[k];
+        // A word wholly inside the chunk was loaded from its own address
+        // (A + 4 <= off + nb <= buffer size): only its byte order changes.
+        if (b + 4 <= J.nb) {
+            *(top - j) = __builtin_bswap32(v);
+            continue;
+        }
         if (!kTiny) {
             // Within the chunk A - word_at(A, last) is 0..3; words at or past
             // its end are zeroed below, whatever the shift.
