@@ -437,6 +437,8 @@ struct Job {
     uint32_t nr;   // rounds
 };
 
+// kLg > 0: every tensor of the launch has 1 << kLg threads per chunk.
+template <uint32_t kLg>
 __device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, uint32_t tid) {
     Job J{-1, 0u, kMaxSegBits, 0, 0u, 0u, 0u, 0u};
     if (item >= args.total_items) return J;
@@ -444,7 +446,7 @@ __device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, ui
     while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
     const DevTensor& T = args.t[d];
     J.d = d;
-    J.lg = static_cast<uint32_t>(__ffs(T.tpc) - 1);
+    J.lg = kLg > 0 ? kLg : static_cast<uint32_t>(__ffs(T.tpc) - 1);
     const uint32_t n_groups = kThreads >> J.lg;
     J.c = (item - T.item_begin) * n_groups + (tid >> J.lg);
     // Segment length: at most kSlotCap codewords of the shortest length.
@@ -858,7 +860,10 @@ struct __attribute__((aligned(16))) Lds {
     __attribute__((aligned(16))) uint8_t stage[kStageBytes + 16];
 };
 
-template <int kMode, int kGroup, bool kTiny>
+// kLg > 0 fixes the threads per chunk at 1 << kLg for the whole launch, so
+// that sub-group geometry and the per-thread offsets derived from it are
+// compile-time constants.
+template <int kMode, int kGroup, bool kTiny, uint32_t kLg>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const LaunchArgs args) {
     __shared__ Lds lds;
     uint32_t* const s_wsyms = lds.wsyms;
@@ -885,7 +890,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     // Software pipeline: the stream words of the next round (or of the next
     // item's first round) are in flight while the current round decodes.
     // The first item's words and table load together.
-    Job cur = make_job(args, blockIdx.x, tid);
+    Job cur = make_job<kLg>(args, blockIdx.x, tid);
     Fetch F;
     fetch_issue<kTiny>(F, args, cur, 0, tid);
     loaded = uniform(args.t[uniform(static_cast<uint32_t>(cur.d))].table);
@@ -895,13 +900,13 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     for (int64_t item = blockIdx.x; item < args.total_items; item += gridDim.x) {
         const DevTensor& T = args.t[uniform(static_cast<uint32_t>(cur.d))];
         const uint8_t* const table = uniform(T.table);
-        const uint32_t lg = uniform(cur.lg);
+        const uint32_t lg = kLg > 0 ? kLg : uniform(cur.lg);
         const uint32_t tpc = 1u << lg;
         const uint32_t g = tid >> lg;
         const uint32_t i_item = tid & (tpc - 1);
         const uint32_t n_groups = kThreads >> lg;
         const uint32_t S = uniform(cur.S);
-        const Job nxt = make_job(args, item + gridDim.x, tid);
+        const Job nxt = make_job<kLg>(args, item + gridDim.x, tid);
 
         const auto* hdr = header_of(table);
         tb.sym0 = hdr->sym0;
@@ -1097,6 +1102,7 @@ struct Batch {
     int64_t items = 0;
     int m = 0;
     bool vec = true;
+    bool full = true;  // every tensor has kThreads threads per chunk
 };
 
 template <int kMode>
@@ -1109,11 +1115,13 @@ int launch_batch(Batch& B, hipStream_t s, bool tiny) {
     const dim3 gdim(static_cast<uint32_t>(grid)), bdim(kThreads);
     constexpr int kVecGroup = kMode == kModeU8 ? 16 : 8;
     if (tiny) {
-        hipLaunchKernelGGL((decode_kernel<kMode, 1, true>), gdim, bdim, 0, s, B.args);
+        hipLaunchKernelGGL((decode_kernel<kMode, 1, true, 0>), gdim, bdim, 0, s, B.args);
+    } else if (B.vec && B.full) {
+        hipLaunchKernelGGL((decode_kernel<kMode, kVecGroup, false, kLgThreads>), gdim, bdim, 0, s, B.args);
     } else if (B.vec) {
-        hipLaunchKernelGGL((decode_kernel<kMode, kVecGroup, false>), gdim, bdim, 0, s, B.args);
+        hipLaunchKernelGGL((decode_kernel<kMode, kVecGroup, false, 0>), gdim, bdim, 0, s, B.args);
     } else {
-        hipLaunchKernelGGL((decode_kernel<kMode, 1, false>), gdim, bdim, 0, s, B.args);
+        hipLaunchKernelGGL((decode_kernel<kMode, 1, false, 0>), gdim, bdim, 0, s, B.args);
     }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess)
@@ -1159,6 +1167,7 @@ int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny) {
     dt.n_symbols = t.n_symbols;
     dt.chunk_size = t.chunk_size;
     dt.tpc = static_cast<int32_t>(threads_per_chunk(t.chunk_size));
+    if (dt.tpc != kThreads) B.full = false;
     // Chunks past the last output element hold nothing to write.
     dt.n_jobs = (t.n_symbols + t.chunk_size - 1) / t.chunk_size;
     dt.item_begin = B.items;
