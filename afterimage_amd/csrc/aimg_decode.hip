@@ -175,29 +175,33 @@ struct Tables {
 };
 
 // Bit reader over the staged stream. A sub-group's tile holds its round's
-// stream words in reverse order (word j at below[-j]), so one 8-byte LDS read
-// at below - k - 1 returns words k+1 and k as the low and high halves of the
+// stream words in reverse order (word j at top[-j]), so one 8-byte LDS read
+// at top - k - 1 returns words k+1 and k as the low and high halves of the
 // 64-bit pair that starts at word k. `pair` holds the words from bit
 // p - sh (a multiple of 32, sh <= 47); a step reads at most 16 bits, all
 // inside the pair. While a step's table lookup is in flight, the reader
 // already fetches the pair starting at the word that contains p, which
 // holds the next step's bits, so each step waits for one LDS round trip.
+//
+// `below` is the LDS byte address of top - 1: the pair whose first word
+// starts at bit m (a multiple of 32) is at below - m / 8.
+typedef const __attribute__((address_space(3))) uint8_t* TileRef;
+typedef const __attribute__((address_space(3))) uint32_t* TileWords;
+
 struct Reader {
-    const uint32_t* below;
+    TileRef below;
     uint32_t p;
     uint32_t sh;
     uint64_t pair;
 };
 
-// `below` is below - 1: the pair starting at word k is read at below - k.
-__device__ __forceinline__ uint64_t load_pair(const uint32_t* below, uint32_t k) {
-    uint64_t v;
-    __builtin_memcpy(&v, below - k, 8);  // 4-byte aligned: two word reads
-    return v;
+__device__ __forceinline__ uint64_t load_pair(TileRef below, uint32_t m) {
+    const TileWords w = reinterpret_cast<TileWords>(below - (m >> 3));
+    return static_cast<uint64_t>(w[0]) | (static_cast<uint64_t>(w[1]) << 32);
 }
 
-__device__ __forceinline__ Reader reader_at(const uint32_t* below, uint32_t p) {
-    return {below, p, p & 31u, load_pair(below, p >> 5)};
+__device__ __forceinline__ Reader reader_at(TileRef below, uint32_t p) {
+    return {below, p, p & 31u, load_pair(below, p & ~31u)};
 }
 
 // The 32 bits at the reader's position (bits past the pair read as zero;
@@ -207,11 +211,11 @@ __device__ __forceinline__ uint32_t reader_bits(const Reader& rd) {
 }
 
 // Move the reader forward by n bits (n <= 16), using the pair prefetched at
-// the old position.
-__device__ __forceinline__ void reader_skip(Reader& rd, uint64_t next_pair, uint32_t n) {
-    rd.sh = (rd.p & 31u) + n;
-    rd.pair = next_pair;
+// the old position (first word at bit m = old p & ~31).
+__device__ __forceinline__ void reader_skip(Reader& rd, uint64_t next_pair, uint32_t m, uint32_t n) {
     rd.p += n;
+    rd.sh = rd.p - m;
+    rd.pair = next_pair;
 }
 
 // (symbol, length) of an escape window's first codeword; w holds the window
@@ -277,7 +281,7 @@ __device__ __forceinline__ uint32_t cut_window(const Tables& tb, uint32_t P, uin
 
 // The first codeword boundary at or after x, parsing from boundary p.
 template <bool kGlobalEsc>
-__device__ __forceinline__ uint32_t advance(const uint32_t* below, const Tables& tb, uint32_t p,
+__device__ __forceinline__ uint32_t advance(TileRef below, const Tables& tb, uint32_t p,
                                             uint32_t x) {
     Reader rd = reader_at(below, p);
     // Whole windows while no codeword of the window can reach x.
@@ -286,19 +290,21 @@ __device__ __forceinline__ uint32_t advance(const uint32_t* below, const Tables&
         const uint32_t w = reader_bits(rd);
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
-        const uint64_t next = load_pair(below, rd.p >> 5);
+        const uint32_t m = rd.p & ~31u;
+        const uint64_t next = load_pair(below, m);
         uint32_t adv = meta & 15u;
         if (__builtin_expect(any_lane(adv == 0), 0)) {
             if (adv == 0) escape<kGlobalEsc>(tb, tb.syms[idx], w, &adv);
         }
-        reader_skip(rd, next, adv);
+        reader_skip(rd, next, m, adv);
     }
     while (rd.p < x) {
         const uint32_t w = reader_bits(rd);
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
         uint32_t syms = tb.syms[idx];
-        const uint64_t next = load_pair(below, rd.p >> 5);
+        const uint32_t m = rd.p & ~31u;
+        const uint64_t next = load_pair(below, m);
         uint32_t adv = meta & 15u;
         uint32_t c = meta >> 4;
         if (adv == 0) {
@@ -309,7 +315,7 @@ __device__ __forceinline__ uint32_t advance(const uint32_t* below, const Tables&
             uint32_t kept;
             return cut_window(tb, rd.p, rd.p + adv, syms, c, x, &kept);
         }
-        reader_skip(rd, next, adv);
+        reader_skip(rd, next, m, adv);
     }
     return rd.p;
 }
@@ -345,7 +351,7 @@ __device__ __forceinline__ void slot_or(uint8_t* slot, uint32_t n, uint32_t syms
 // lies inside the slot. The last lookup's symbols that start at or after x
 // are masked off before it is placed.
 template <bool kGlobalEsc>
-__device__ __forceinline__ Adv decode_run(const uint32_t* below, const Tables& tb, uint32_t p,
+__device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint32_t p,
                                           uint32_t x, uint8_t* slot) {
     uint32_t n = 0;
     Reader rd = reader_at(below, p);
@@ -355,7 +361,8 @@ __device__ __forceinline__ Adv decode_run(const uint32_t* below, const Tables& t
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
         uint32_t syms = tb.syms[idx];
-        const uint64_t next = load_pair(below, rd.p >> 5);
+        const uint32_t m = rd.p & ~31u;
+        const uint64_t next = load_pair(below, m);
         uint32_t adv = meta & 15u;
         uint32_t c = meta >> 4;
         if (__builtin_expect(any_lane(adv == 0), 0)) {
@@ -366,14 +373,15 @@ __device__ __forceinline__ Adv decode_run(const uint32_t* below, const Tables& t
         }
         slot_or(slot, n, syms);
         n += c;
-        reader_skip(rd, next, adv);
+        reader_skip(rd, next, m, adv);
     }
     while (rd.p < x) {
         const uint32_t w = reader_bits(rd);
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
         uint32_t syms = tb.syms[idx];
-        const uint64_t next = load_pair(below, rd.p >> 5);
+        const uint32_t m = rd.p & ~31u;
+        const uint64_t next = load_pair(below, m);
         uint32_t adv = meta & 15u;
         uint32_t c = meta >> 4;
         if (adv == 0) {
@@ -388,7 +396,7 @@ __device__ __forceinline__ Adv decode_run(const uint32_t* below, const Tables& t
         }
         slot_or(slot, n, syms);
         n += c;
-        reader_skip(rd, next, adv);
+        reader_skip(rd, next, m, adv);
     }
     return {rd.p, n};
 }
@@ -921,7 +929,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
 
         const int64_t chunk_base = cur.c * T.chunk_size;
         const int64_t lim = cur.lim;
-        const uint32_t* below = tile_top(s_tile, g, lg) - 1;
+        // Laundered: the tile base then stays one register, not a base plus
+        // a constant added in every step of the decode loops.
+        TileRef below = (TileRef)(tile_top(s_tile, g, lg) - 1);
+        asm volatile("" : "+v"(below));
         const uint32_t region = kStageBytes >> (kLgThreads - lg);
         uint8_t* stage = s_stage + g * region;
         uint8_t* slot = stage + kLeadBytes + i_item * kSlotBytes;
