@@ -279,45 +279,33 @@ __device__ __forceinline__ uint32_t cut_window(const Tables& tb, uint32_t P, uin
     return e;
 }
 
-// The first codeword boundary at or after x, parsing from boundary p.
+// The first codeword boundary at or after x, parsing from boundary p < x.
+// Each step takes a whole window; the step whose window reaches x is cut
+// there, once, after the loop.
 template <bool kGlobalEsc>
 __device__ __forceinline__ uint32_t advance(TileRef below, const Tables& tb, uint32_t p,
                                             uint32_t x) {
     Reader rd = reader_at(below, p);
-    // Whole windows while no codeword of the window can reach x.
-    const int32_t x12 = static_cast<int32_t>(x) - kWinBits;
-    while (static_cast<int32_t>(rd.p) <= x12) {
-        const uint32_t w = reader_bits(rd);
-        const uint32_t idx = w >> (32 - kWinBits);
+    uint32_t w, idx, adv, c;
+    for (;;) {
+        w = reader_bits(rd);
+        idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
         const uint32_t m = rd.p & ~31u;
         const uint64_t next = load_pair(below, m);
-        uint32_t adv = meta & 15u;
+        adv = meta & 15u;
+        c = meta >> 4;
         if (__builtin_expect(any_lane(adv == 0), 0)) {
-            if (adv == 0) escape<kGlobalEsc>(tb, tb.syms[idx], w, &adv);
+            if (adv == 0) {
+                escape<kGlobalEsc>(tb, tb.syms[idx], w, &adv);
+                c = 1;
+            }
         }
+        if (rd.p + adv >= x) break;
         reader_skip(rd, next, m, adv);
     }
-    while (rd.p < x) {
-        const uint32_t w = reader_bits(rd);
-        const uint32_t idx = w >> (32 - kWinBits);
-        const uint32_t meta = tb.meta[idx];
-        uint32_t syms = tb.syms[idx];
-        const uint32_t m = rd.p & ~31u;
-        const uint64_t next = load_pair(below, m);
-        uint32_t adv = meta & 15u;
-        uint32_t c = meta >> 4;
-        if (adv == 0) {
-            escape<kGlobalEsc>(tb, syms, w, &adv);
-            c = 1;
-        }
-        if (rd.p + adv >= x) {
-            uint32_t kept;
-            return cut_window(tb, rd.p, rd.p + adv, syms, c, x, &kept);
-        }
-        reader_skip(rd, next, m, adv);
-    }
-    return rd.p;
+    uint32_t kept;
+    return cut_window(tb, rd.p, rd.p + adv, c > 1 ? tb.syms[idx] : 0u, c, x, &kept);
 }
 
 __device__ __forceinline__ uint32_t get_u32(const uint8_t* p) {
@@ -353,52 +341,34 @@ __device__ __forceinline__ void slot_or(uint8_t* slot, uint32_t n, uint32_t syms
 template <bool kGlobalEsc>
 __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint32_t p,
                                           uint32_t x, uint8_t* slot) {
+    if (p >= x) return {p, 0u};
     uint32_t n = 0;
     Reader rd = reader_at(below, p);
-    const int32_t x12 = static_cast<int32_t>(x) - kWinBits;
-    while (static_cast<int32_t>(rd.p) <= x12) {
+    uint32_t syms, adv, c;
+    for (;;) {
         const uint32_t w = reader_bits(rd);
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
-        uint32_t syms = tb.syms[idx];
+        syms = tb.syms[idx];
         const uint32_t m = rd.p & ~31u;
         const uint64_t next = load_pair(below, m);
-        uint32_t adv = meta & 15u;
-        uint32_t c = meta >> 4;
+        adv = meta & 15u;
+        c = meta >> 4;
         if (__builtin_expect(any_lane(adv == 0), 0)) {
             if (adv == 0) {
                 syms = escape<kGlobalEsc>(tb, syms, w, &adv);
                 c = 1;
             }
         }
+        if (rd.p + adv >= x) break;
         slot_or(slot, n, syms);
         n += c;
         reader_skip(rd, next, m, adv);
     }
-    while (rd.p < x) {
-        const uint32_t w = reader_bits(rd);
-        const uint32_t idx = w >> (32 - kWinBits);
-        const uint32_t meta = tb.meta[idx];
-        uint32_t syms = tb.syms[idx];
-        const uint32_t m = rd.p & ~31u;
-        const uint64_t next = load_pair(below, m);
-        uint32_t adv = meta & 15u;
-        uint32_t c = meta >> 4;
-        if (adv == 0) {
-            syms = escape<kGlobalEsc>(tb, syms, w, &adv);
-            c = 1;
-        }
-        if (rd.p + adv >= x) {
-            uint32_t kept;  // 1..4
-            const uint32_t e = cut_window(tb, rd.p, rd.p + adv, syms, c, x, &kept);
-            slot_or(slot, n, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
-            return {e, n + kept};
-        }
-        slot_or(slot, n, syms);
-        n += c;
-        reader_skip(rd, next, m, adv);
-    }
-    return {rd.p, n};
+    uint32_t kept;  // 1..4
+    const uint32_t e = cut_window(tb, rd.p, rd.p + adv, syms, c, x, &kept);
+    slot_or(slot, n, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
+    return {e, n + kept};
 }
 
 // Where to load the 4 bytes from packed-buffer byte A (A below the buffer
