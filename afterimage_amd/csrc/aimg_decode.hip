@@ -81,6 +81,8 @@ constexpr uint32_t kTileBatch = kMaxSegBits / 32 + 1;
 // kSlotCap symbols per thread, plus a carried partial group.
 constexpr uint32_t kStoreBatch = (kSlotCap * kMinTpc + 15 + 8 * kMinTpc - 1) / (8 * kMinTpc);
 static_assert(kStoreBatch * 8 * kMinTpc >= kSlotCap * kMinTpc + 15, "one store batch covers a round");
+constexpr uint32_t kStagePadded =
+    (kStageBytes + 16 > kStoreBatch * kThreads * 8 ? kStageBytes + 16 : kStoreBatch * kThreads * 8);
 // Of those, the groups whose sign/mantissa bytes are requested while the round
 // decodes. A round of bf16 weights fills about 8 groups per thread; the rest
 // are loaded at the store, by waves that need them.
@@ -157,8 +159,11 @@ __device__ __forceinline__ const __attribute__((address_space(4))) TableHeader* 
     return (const __attribute__((address_space(4))) TableHeader*)(table);
 }
 
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+
 // Buffer resource over `nbytes` bytes at `base` (raw, stride 0): loads past
-// the end return zero instead of touching memory outside the buffer.
+// the end return zero and stores past it are dropped, instead of touching
+// memory outside the buffer.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, uint32_t nbytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(nbytes),
                                              0x00020000);
@@ -675,8 +680,10 @@ __device__ __forceinline__ void gemv_flush(const GemvArgs& G, float (&acc)[kGemv
 }
 
 // Vector groups [0, nfull) of the staged round to output elements a0...;
-// thread i of a sub-group of tpc takes groups i, i + tpc, ...
-template <int kMode, int kGroup>
+// thread i of a sub-group of tpc takes groups i, i + tpc, ... kWhole: the
+// sub-group is the whole workgroup, whose stage area is readable for every
+// group a store batch can name, so the staged reads need no clamping.
+template <int kMode, int kGroup, bool kWhole>
 __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTensor& T,
                                             const GemvArgs& G, const uint8_t* stage, int64_t a0,
                                             uint32_t nfull, uint32_t i, uint32_t tpc) {
@@ -718,26 +725,30 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
 #pragma unroll
         for (uint32_t k = kSmAhead; k < kStoreBatch; ++k) sm[k] = make_uint2(0u, 0u);
     }
-    // All staged exponents are read (from clamped, always valid offsets)
-    // before any is combined, so the LDS reads overlap.
+    // All staged exponents are read (from always valid offsets) before any
+    // is combined, so the LDS reads overlap.
     uint2 ev[kStoreBatch];
 #pragma unroll
     for (uint32_t k = 0; k < kStoreBatch; ++k) {
         const uint32_t v = k * tpc + i;
-        ev[k] = *reinterpret_cast<const uint2*>(stage + (v < nfull ? v : 0u) * kGroup);
+        ev[k] = *reinterpret_cast<const uint2*>(stage + (kWhole || v < nfull ? v : 0u) * kGroup);
     }
     if (kMode == kModeBf16) {
-        uint4* dst = reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.out) + a0);
+        // Buffer stores: per-lane offset 2 * a0 + 16 i, the batch step as a
+        // scalar offset (outputs are below 2^31 elements).
+        const __amdgpu_buffer_rsrc_t rs =
+            buffer_of(T.out, static_cast<uint32_t>(T.n_symbols) * 2u);
+        const uint32_t vo = static_cast<uint32_t>(a0) * 2u + 16u * i;
 #pragma unroll
         for (uint32_t k = 0; k < kStoreBatch; ++k) {
             const uint32_t v = k * tpc + i;
             if (v >= nfull) continue;
-            uint4 o4;
-            o4.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, ev[k].x);
-            o4.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, ev[k].x);
-            o4.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, ev[k].y);
-            o4.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, ev[k].y);
-            dst[v] = o4;
+            v4u32 o4;
+            o4[0] = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, ev[k].x);
+            o4[1] = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, ev[k].x);
+            o4[2] = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, ev[k].y);
+            o4[3] = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, ev[k].y);
+            __builtin_amdgcn_raw_buffer_store_b128(o4, rs, vo, 16u * k * tpc, 0);
         }
         return;
     }
@@ -834,8 +845,9 @@ struct __attribute__((aligned(16))) Lds {
     uint32_t ewave[kWaves];      // segment end of each wave's last lane
     uint32_t glast[kMaxGroups];  // segment end of each sub-group's last active thread
     uint32_t tile[kTileWords];
-    // 16 bytes past the last slot: the word read or zero-ORed past it.
-    __attribute__((aligned(16))) uint8_t stage[kStageBytes + 16];
+    // Past the slots: the word read or zero-ORed past the last slot, and the
+    // groups an unclamped store batch of a whole-workgroup chunk reads.
+    __attribute__((aligned(16))) uint8_t stage[kStagePadded];
 };
 
 // kLg > 0 fixes the threads per chunk at 1 << kLg for the whole launch, so
@@ -1028,7 +1040,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
             __syncthreads();
 
-            store_round<kMode, kGroup>(smb, T, args.gemv, stage, a0, nfull, i, tpc);
+            store_round<kMode, kGroup, kLg == kLgThreads>(smb, T, args.gemv, stage, a0, nfull, i, tpc);
             ob += want;
             // The partial vector group moves to the front for the next round.
             const uint32_t rem = avail - nfull * kGroup;

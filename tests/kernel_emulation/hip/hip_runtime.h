@@ -175,6 +175,17 @@ inline emu_u32x2 __builtin_amdgcn_raw_buffer_load_b64(__amdgpu_buffer_rsrc_t r, 
     v[1] = off + 8 > r.n ? 0u : emu_dword(r, off + 4);
     return v;
 }
+typedef uint32_t emu_u32x4 __attribute__((ext_vector_type(4)));
+// Stores: each dword past num_records is dropped.
+inline void __builtin_amdgcn_raw_buffer_store_b128(emu_u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t vo,
+                                                   uint32_t so, int) {
+    const uint64_t off = (uint64_t)vo + so;
+    for (int k = 0; k < 4; ++k)
+        if (off + 4 * k + 4 <= r.n) {
+            const uint32_t d = v[k];
+            std::memcpy(const_cast<uint8_t*>(r.base) + off + 4 * k, &d, 4);
+        }
+}
 #ifndef __HIP_MEMORY_SCOPE_WORKGROUP
 #define __HIP_MEMORY_SCOPE_WORKGROUP 3
 #endif
