@@ -284,33 +284,58 @@ __device__ __forceinline__ uint32_t cut_window(const Tables& tb, uint32_t P, uin
     return e;
 }
 
+// One table lookup: the window at the reader's position, its meta and (for
+// decode) symbols, and the pair the following step reads, prefetched from the
+// word holding the position (first word at bit m).
+struct Step {
+    uint32_t p;      // window start
+    uint32_t w;      // window bits (31..20) and the next four (19..16)
+    uint32_t idx;    // window table index
+    uint32_t meta;
+    uint32_t syms;
+    uint32_t m;
+    uint64_t next;
+};
+
+template <bool kSyms>
+__device__ __forceinline__ Step lookup(TileRef below, const Tables& tb, uint32_t p, uint32_t sh,
+                                       uint64_t pair) {
+    Step s;
+    s.p = p;
+    s.w = static_cast<uint32_t>((pair << sh) >> 32);
+    s.idx = s.w >> (32 - kWinBits);
+    s.meta = tb.meta[s.idx];
+    s.syms = kSyms ? tb.syms[s.idx] : 0u;
+    s.m = p & ~31u;
+    s.next = load_pair(below, s.m);
+    return s;
+}
+
 // The first codeword boundary at or after x, parsing from boundary p < x.
 // Each step takes a whole window; the step whose window reaches x is cut
-// there, once, after the loop.
+// there, once, after the loop. Steps are software-pipelined: as soon as a
+// step's length is known, the next step's lookup is issued.
 template <bool kGlobalEsc>
 __device__ __forceinline__ uint32_t advance(TileRef below, const Tables& tb, uint32_t p,
                                             uint32_t x) {
-    Reader rd = reader_at(below, p);
-    uint32_t w, idx, adv, c;
+    const Reader rd = reader_at(below, p);
+    Step s = lookup<false>(below, tb, rd.p, rd.sh, rd.pair);
+    uint32_t adv, c;
     for (;;) {
-        w = reader_bits(rd);
-        idx = w >> (32 - kWinBits);
-        const uint32_t meta = tb.meta[idx];
-        const uint32_t m = rd.p & ~31u;
-        const uint64_t next = load_pair(below, m);
-        adv = meta & 15u;
-        c = meta >> 4;
+        adv = s.meta & 15u;
+        c = s.meta >> 4;
         if (__builtin_expect(any_lane(adv == 0), 0)) {
             if (adv == 0) {
-                escape<kGlobalEsc>(tb, tb.syms[idx], w, &adv);
+                escape<kGlobalEsc>(tb, tb.syms[s.idx], s.w, &adv);
                 c = 1;
             }
         }
-        if (rd.p + adv >= x) break;
-        reader_skip(rd, next, m, adv);
+        const uint32_t pn = s.p + adv;
+        if (pn >= x) break;
+        s = lookup<false>(below, tb, pn, pn - s.m, s.next);
     }
     uint32_t kept;
-    return cut_window(tb, rd.p, rd.p + adv, c > 1 ? tb.syms[idx] : 0u, c, x, &kept);
+    return cut_window(tb, s.p, s.p + adv, c > 1 ? tb.syms[s.idx] : 0u, c, x, &kept);
 }
 
 __device__ __forceinline__ uint32_t get_u32(const uint8_t* p) {
@@ -348,30 +373,29 @@ __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint3
                                           uint32_t x, uint8_t* slot) {
     if (p >= x) return {p, 0u};
     uint32_t n = 0;
-    Reader rd = reader_at(below, p);
+    const Reader rd = reader_at(below, p);
+    Step s = lookup<true>(below, tb, rd.p, rd.sh, rd.pair);
     uint32_t syms, adv, c;
     for (;;) {
-        const uint32_t w = reader_bits(rd);
-        const uint32_t idx = w >> (32 - kWinBits);
-        const uint32_t meta = tb.meta[idx];
-        syms = tb.syms[idx];
-        const uint32_t m = rd.p & ~31u;
-        const uint64_t next = load_pair(below, m);
-        adv = meta & 15u;
-        c = meta >> 4;
+        syms = s.syms;
+        adv = s.meta & 15u;
+        c = s.meta >> 4;
         if (__builtin_expect(any_lane(adv == 0), 0)) {
             if (adv == 0) {
-                syms = escape<kGlobalEsc>(tb, syms, w, &adv);
+                syms = escape<kGlobalEsc>(tb, syms, s.w, &adv);
                 c = 1;
             }
         }
-        if (rd.p + adv >= x) break;
+        const uint32_t pn = s.p + adv;
+        if (pn >= x) break;
+        // The next lookup goes out before this step's symbols are placed.
+        const Step t = lookup<true>(below, tb, pn, pn - s.m, s.next);
         slot_or(slot, n, syms);
         n += c;
-        reader_skip(rd, next, m, adv);
+        s = t;
     }
     uint32_t kept;  // 1..4
-    const uint32_t e = cut_window(tb, rd.p, rd.p + adv, syms, c, x, &kept);
+    const uint32_t e = cut_window(tb, s.p, s.p + adv, syms, c, x, &kept);
     slot_or(slot, n, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
     return {e, n + kept};
 }
