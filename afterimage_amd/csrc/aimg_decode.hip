@@ -171,7 +171,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, ui
 
 struct Tables {
     const uint32_t* syms;    // LDS window table: symbols / escape block
-    const uint8_t* meta;     // LDS window table: total | count << 4
+    const uint8_t* meta;     // LDS window table: total | (count - 1) << 6
     const uint8_t* len;      // LDS code length of each symbol
     const uint16_t* esc;     // LDS escape blocks (first kLdsEscBlocks)
     const __attribute__((address_space(1))) uint16_t* gesc;  // all escape blocks, global memory
@@ -322,8 +322,8 @@ __device__ __forceinline__ uint32_t advance(TileRef below, const Tables& tb, uin
     Step s = lookup<false>(below, tb, rd.p, rd.sh, rd.pair);
     uint32_t adv, c;
     for (;;) {
-        adv = s.meta & 15u;
-        c = s.meta >> 4;
+        adv = s.meta & 63u;
+        c = (s.meta >> 6) + 1;
         if (__builtin_expect(any_lane(adv == 0), 0)) {
             if (adv == 0) {
                 escape<kGlobalEsc>(tb, tb.syms[s.idx], s.w, &adv);
@@ -378,8 +378,8 @@ __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint3
     uint32_t syms, adv, c;
     for (;;) {
         syms = s.syms;
-        adv = s.meta & 15u;
-        c = s.meta >> 4;
+        adv = s.meta & 63u;
+        c = (s.meta >> 6) + 1;
         if (__builtin_expect(any_lane(adv == 0), 0)) {
             if (adv == 0) {
                 syms = escape<kGlobalEsc>(tb, syms, s.w, &adv);
