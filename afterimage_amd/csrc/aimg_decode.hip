@@ -33,7 +33,7 @@
 //
 // Codewords are read through a 12-bit window table of up to 4 codewords per
 // lookup (LDS); codewords of 13..16 bits go through 16-entry escape blocks
-// (LDS for the first 64 blocks, global memory beyond).
+// (LDS for the first 48 blocks, global memory beyond).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -57,15 +57,18 @@ static_assert(kThreads == 1 << kLgThreads, "kLgThreads");
 constexpr int kMinTpc = 16;
 constexpr int kMaxGroups = kThreads / kMinTpc;
 constexpr uint32_t kOverlapBits = 32;
-// Per-thread slot for one segment's symbols, kSlotCap bytes. Slots are an
-// odd number of words apart, so the lanes of a wave writing at similar counts
-// hit different LDS banks. 168-bit segments at the 2-bit shortest code of
-// bf16 weights make a 64Ki-symbol chunk (about 171K bits) two rounds of 512
+// Per-thread slot for one segment's symbols: at most kSlotCap of them. A
+// lookup's symbols go into the aligned word holding the first and the word
+// after it, which may lie past the cap. Slots are kSlotBytes apart, an odd
+// number of words, so the lanes of a wave writing at similar counts hit
+// different LDS banks. 168-bit segments at the 2-bit shortest code of bf16
+// weights make a 64Ki-symbol chunk (about 171K bits) two rounds of 512
 // segments.
 constexpr uint32_t kSlotCap = 84;
-constexpr uint32_t kSlotBytes = kSlotCap;
-constexpr uint32_t kSlotWords = kSlotBytes / 4;
-static_assert(kSlotBytes % 4 == 0 && kSlotWords % 2 == 1, "slot stride: an odd number of words");
+constexpr uint32_t kSlotWords = kSlotCap / 4;  // compaction reads these and one more
+constexpr uint32_t kSlotBytes = 92;
+static_assert(kSlotCap % 4 == 0 && kSlotBytes >= kSlotCap + 4, "slot room for the word after the cap");
+static_assert(kSlotBytes % 4 == 0 && (kSlotBytes / 4) % 2 == 1, "slot stride: an odd number of words");
 constexpr uint32_t kMaxSegBits = 168;
 constexpr uint32_t kLeadBytes = 16;  // room for a carried partial vector group
 constexpr uint32_t kTileSlackWords = 4;
@@ -73,7 +76,7 @@ constexpr uint32_t kTileWords = kThreads * kMaxSegBits / 32 + kTileSlackWords * 
 constexpr uint32_t kStageBytes = kThreads * kSlotBytes + kLeadBytes * kMaxGroups;
 static_assert(kStageBytes % (16 * kMaxGroups) == 0, "stage regions stay 16-byte aligned");
 static_assert(kTileWords % kMaxGroups == 0, "tile regions split evenly");
-constexpr int kLdsEscBlocks = 64;
+constexpr int kLdsEscBlocks = 48;
 // Stream words a thread fetches per round: a round has at most
 // tpc * kMaxSegBits / 32 + 3 words.
 constexpr uint32_t kTileBatch = kMaxSegBits / 32 + 1;
@@ -342,32 +345,28 @@ __device__ __forceinline__ uint32_t get_u32(const uint8_t* p) {
     return *reinterpret_cast<const uint32_t*>(p);  // LDS, any byte alignment
 }
 
-// A thread's slot is zero before its segment is decoded into it.
-__device__ __forceinline__ void clear_slot(uint8_t* slot) {
-    uint32_t* w = reinterpret_cast<uint32_t*>(slot);
-#pragma unroll
-    for (uint32_t j = 0; j < kSlotWords; ++j) w[j] = 0;
-}
+// Before a segment is decoded into a slot, its first word is zero.
+__device__ __forceinline__ void start_slot(uint8_t* slot) { *reinterpret_cast<uint32_t*>(slot) = 0u; }
 
 // Place the symbols of one lookup (bytes of syms, zero above the lookup's
-// count) at slot[n...]: OR them into the one or two words they fall in,
-// so no word needs reading or merging first. For n near kSlotCap the second
-// word is the next slot's first: only zero bits go there.
-__device__ __forceinline__ void slot_or(uint8_t* slot, uint32_t n, uint32_t syms) {
+// count) at slot[n...]: OR them into the aligned word holding byte n and
+// write the word after it whole. Invariant: the word holding byte n is zero
+// from byte n up, since it was either the slot's first word or the last
+// whole word written, whose bytes from n up are zero bytes of syms.
+__device__ __forceinline__ void slot_put(uint8_t* slot, uint32_t n, uint32_t syms) {
     const uint64_t v = static_cast<uint64_t>(syms) << (8 * (n & 3u));
     uint32_t* w = reinterpret_cast<uint32_t*>(slot + (n & ~3u));
     __hip_atomic_fetch_or(w, static_cast<uint32_t>(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    __hip_atomic_fetch_or(w + 1, static_cast<uint32_t>(v >> 32), __ATOMIC_RELAXED,
-                          __HIP_MEMORY_SCOPE_WORKGROUP);
+    w[1] = static_cast<uint32_t>(v >> 32);
 }
 
 // Parse codewords from true boundary p while they start before x, placing
-// their symbols in the (zeroed) slot. Returns the first boundary at or
-// after x and the number of codewords. Every codeword (or unused window)
+// their symbols in the slot (first word zero). Returns the first boundary at
+// or after x and the number of codewords. Every codeword (or unused window)
 // takes at least min_len bits, so a segment of at most kSlotCap * min_len
-// bits never holds more than kSlotCap codewords: every nonzero byte written
-// lies inside the slot. The last lookup's symbols that start at or after x
-// are masked off before it is placed.
+// bits never holds more than kSlotCap codewords, and every write stays
+// inside the slot. The last lookup's symbols that start at or after x are
+// masked off before it is placed.
 template <bool kGlobalEsc>
 __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint32_t p,
                                           uint32_t x, uint8_t* slot) {
@@ -390,13 +389,13 @@ __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint3
         if (pn >= x) break;
         // The next lookup goes out before this step's symbols are placed.
         const Step t = lookup<true>(below, tb, pn, pn - s.m, s.next);
-        slot_or(slot, n, syms);
+        slot_put(slot, n, syms);
         n += c;
         s = t;
     }
     uint32_t kept;  // 1..4
     const uint32_t e = cut_window(tb, s.p, s.p + adv, syms, c, x, &kept);
-    slot_or(slot, n, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
+    slot_put(slot, n, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
     return {e, n + kept};
 }
 
@@ -975,7 +974,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const uint32_t seg_hi = active ? (seg_lo + S < RB ? seg_lo + S : RB) : 0u;
             uint32_t f = 0, e = 0, cnt = 0;
             if (active) {
-                clear_slot(slot);
+                start_slot(slot);
                 Adv a;
                 if (global_esc) {
                     f = i == 0 ? p0 : advance<true>(below, tb, seg_lo - kOverlapBits, seg_lo);
@@ -1009,7 +1008,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 if (!any_bad) break;
                 if (bad) {
                     f = ep;
-                    clear_slot(slot);
+                    start_slot(slot);
                     const Adv a = global_esc ? decode_run<true>(below, tb, f, seg_hi, slot)
                                              : decode_run<false>(below, tb, f, seg_hi, slot);
                     e = a.p;
@@ -1040,8 +1039,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const uint32_t head = head0 < m ? head0 : m;  // bytes before the first aligned word
             const uint32_t nbody = (m - head) >> 2;       // whole words
             const uint32_t ntail = m - head - 4 * nbody;  // bytes after them
-            // One word past the slot (the next slot's first, or padding), for
-            // the byte shift of the last whole word.
+            // One word past the cap (still inside the slot), for the byte
+            // shift of the last whole word.
             uint32_t rw[kSlotWords + 1];
             const uint32_t* slot_w = reinterpret_cast<const uint32_t*>(slot);
 #pragma unroll
