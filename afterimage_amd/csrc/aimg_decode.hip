@@ -314,6 +314,23 @@ __device__ __forceinline__ Step lookup(TileRef below, const Tables& tb, uint32_t
     return s;
 }
 
+// A lookup's symbols, bits and codewords; an escape window (rare: the wave
+// branches only when one of its lanes has one) takes its first codeword from
+// the escape block.
+template <bool kGlobalEsc>
+__device__ __forceinline__ void take(const Tables& tb, const Step& s, uint32_t* syms, uint32_t* adv,
+                                     uint32_t* c) {
+    *syms = s.syms;
+    *adv = s.meta & 63u;
+    *c = (s.meta >> 6) + 1;
+    if (__builtin_expect(any_lane(*adv == 0), 0)) {
+        if (*adv == 0) {
+            *syms = escape<kGlobalEsc>(tb, tb.syms[s.idx], s.w, adv);
+            *c = 1;
+        }
+    }
+}
+
 // The first codeword boundary at or after x, parsing from boundary p < x.
 // Each step takes a whole window; the step whose window reaches x is cut
 // there, once, after the loop. Steps are software-pipelined: as soon as a
@@ -323,26 +340,16 @@ __device__ __forceinline__ uint32_t advance(TileRef below, const Tables& tb, uin
                                             uint32_t x) {
     const Reader rd = reader_at(below, p);
     Step s = lookup<false>(below, tb, rd.p, rd.sh, rd.pair);
-    uint32_t adv, c;
-    for (;;) {
-        adv = s.meta & 63u;
-        c = (s.meta >> 6) + 1;
-        if (__builtin_expect(any_lane(adv == 0), 0)) {
-            if (adv == 0) {
-                escape<kGlobalEsc>(tb, tb.syms[s.idx], s.w, &adv);
-                c = 1;
-            }
-        }
-        const uint32_t pn = s.p + adv;
-        if (pn >= x) break;
+    uint32_t syms, adv, c;
+    take<kGlobalEsc>(tb, s, &syms, &adv, &c);
+    uint32_t pn = s.p + adv;
+    while (pn < x) {
         s = lookup<false>(below, tb, pn, pn - s.m, s.next);
+        take<kGlobalEsc>(tb, s, &syms, &adv, &c);
+        pn = s.p + adv;
     }
     uint32_t kept;
     return cut_window(tb, s.p, s.p + adv, c > 1 ? tb.syms[s.idx] : 0u, c, x, &kept);
-}
-
-__device__ __forceinline__ uint32_t get_u32(const uint8_t* p) {
-    return *reinterpret_cast<const uint32_t*>(p);  // LDS, any byte alignment
 }
 
 // Before a segment is decoded into a slot, its first word is zero.
@@ -375,23 +382,16 @@ __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint3
     const Reader rd = reader_at(below, p);
     Step s = lookup<true>(below, tb, rd.p, rd.sh, rd.pair);
     uint32_t syms, adv, c;
-    for (;;) {
-        syms = s.syms;
-        adv = s.meta & 63u;
-        c = (s.meta >> 6) + 1;
-        if (__builtin_expect(any_lane(adv == 0), 0)) {
-            if (adv == 0) {
-                syms = escape<kGlobalEsc>(tb, syms, s.w, &adv);
-                c = 1;
-            }
-        }
-        const uint32_t pn = s.p + adv;
-        if (pn >= x) break;
+    take<kGlobalEsc>(tb, s, &syms, &adv, &c);
+    uint32_t pn = s.p + adv;
+    while (pn < x) {
         // The next lookup goes out before this step's symbols are placed.
         const Step t = lookup<true>(below, tb, pn, pn - s.m, s.next);
         slot_put(slot, n, syms);
         n += c;
         s = t;
+        take<kGlobalEsc>(tb, s, &syms, &adv, &c);
+        pn = s.p + adv;
     }
     uint32_t kept;  // 1..4
     const uint32_t e = cut_window(tb, s.p, s.p + adv, syms, c, x, &kept);
@@ -1045,7 +1045,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const uint32_t* slot_w = reinterpret_cast<const uint32_t*>(slot);
 #pragma unroll
             for (uint32_t j = 0; j < kSlotWords + 1; ++j) rw[j] = slot_w[j];
-            const uint32_t tv = get_u32(slot + head + 4 * nbody);
+            const uint32_t tv = __builtin_amdgcn_alignbyte(slot_w[nbody + 1], slot_w[nbody], head);
             __syncthreads();
             uint8_t* dst = stage + dpos;
 #pragma unroll
