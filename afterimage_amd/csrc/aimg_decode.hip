@@ -308,9 +308,9 @@ __device__ __forceinline__ Step lookup(TileRef below, const Tables& tb, uint32_t
     s.w = static_cast<uint32_t>((pair << sh) >> 32);
     s.idx = s.w >> (32 - kWinBits);
     s.meta = tb.meta[s.idx];
-    s.syms = kSyms ? tb.syms[s.idx] : 0u;
     s.m = p & ~31u;
     s.next = load_pair(below, s.m);
+    s.syms = kSyms ? tb.syms[s.idx] : 0u;
     return s;
 }
 
@@ -356,13 +356,14 @@ __device__ __forceinline__ uint32_t advance(TileRef below, const Tables& tb, uin
 __device__ __forceinline__ void start_slot(uint8_t* slot) { *reinterpret_cast<uint32_t*>(slot) = 0u; }
 
 // Place the symbols of one lookup (bytes of syms, zero above the lookup's
-// count) at slot[n...]: OR them into the aligned word holding byte n and
-// write the word after it whole. Invariant: the word holding byte n is zero
-// from byte n up, since it was either the slot's first word or the last
-// whole word written, whose bytes from n up are zero bytes of syms.
-__device__ __forceinline__ void slot_put(uint8_t* slot, uint32_t n, uint32_t syms) {
-    const uint64_t v = static_cast<uint64_t>(syms) << (8 * (n & 3u));
-    uint32_t* w = reinterpret_cast<uint32_t*>(slot + (n & ~3u));
+// count) at q (inside a slot, which is word-aligned): OR them into the word
+// holding q and write the word after it whole. Invariant: the word holding q
+// is zero from q up, since it was either the slot's first word or the last
+// whole word written, whose bytes from q up are zero bytes of syms.
+__device__ __forceinline__ void slot_put(uint8_t* q, uint32_t syms) {
+    const uint32_t b = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(q)) & 3u;
+    const uint64_t v = static_cast<uint64_t>(syms) << (8 * b);
+    uint32_t* w = reinterpret_cast<uint32_t*>(q - b);
     __hip_atomic_fetch_or(w, static_cast<uint32_t>(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     w[1] = static_cast<uint32_t>(v >> 32);
 }
@@ -378,25 +379,27 @@ template <bool kGlobalEsc>
 __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint32_t p,
                                           uint32_t x, uint8_t* slot) {
     if (p >= x) return {p, 0u};
-    uint32_t n = 0;
+    uint8_t* q = slot;
     const Reader rd = reader_at(below, p);
     Step s = lookup<true>(below, tb, rd.p, rd.sh, rd.pair);
     uint32_t syms, adv, c;
     take<kGlobalEsc>(tb, s, &syms, &adv, &c);
     uint32_t pn = s.p + adv;
     while (pn < x) {
-        // The next lookup goes out before this step's symbols are placed.
-        const Step t = lookup<true>(below, tb, pn, pn - s.m, s.next);
-        slot_put(slot, n, syms);
-        n += c;
+        // The next step's meta and pair go out before this step's symbols
+        // are placed, its symbols after.
+        Step t = lookup<false>(below, tb, pn, pn - s.m, s.next);
+        slot_put(q, syms);
+        q += c;
+        t.syms = tb.syms[t.idx];
         s = t;
         take<kGlobalEsc>(tb, s, &syms, &adv, &c);
         pn = s.p + adv;
     }
     uint32_t kept;  // 1..4
     const uint32_t e = cut_window(tb, s.p, s.p + adv, syms, c, x, &kept);
-    slot_put(slot, n, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
-    return {e, n + kept};
+    slot_put(q, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
+    return {e, static_cast<uint32_t>(q - slot) + kept};
 }
 
 // Where to load the 4 bytes from packed-buffer byte A (A below the buffer
