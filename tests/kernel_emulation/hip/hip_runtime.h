@@ -214,6 +214,7 @@ inline float atomicAdd(float* p, float v) {
     }
 }
 inline int __ffs(int x) { return __builtin_ffs(x); }
+inline void __builtin_amdgcn_s_setprio(int) {}  // wave issue priority: no effect here
 
 template <typename K, typename... A>
 inline void emu_launch(K kernel, dim3 g, dim3 b, A... args) {
