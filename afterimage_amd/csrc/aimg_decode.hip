@@ -113,8 +113,12 @@ enum Mode : int {
     kModeU8 = 0,    // the exponent bytes themselves
     kModeBf16 = 1,  // bf16 weights
     kModeGemv = 2,  // y += W x with W decoded on the fly and never written
+    kModeGemv1 = 3, // kModeGemv for one x vector (batch 1)
 };
 constexpr int kGemvMaxBatch = 4;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct GemvArgs {
     const uint16_t* x;  // bf16 [batch][cols]
@@ -122,6 +126,8 @@ struct GemvArgs {
     uint32_t rows;
     uint32_t cols;
     int32_t batch;
+    uint32_t step_rows;  // 4096 elements (8 per thread of a 512-thread chunk)
+    uint32_t step_cols;  // = step_rows rows + step_cols columns
 };
 
 struct LaunchArgs {
@@ -610,6 +616,19 @@ __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
     return x;
 }
 
+// Inclusive prefix sum over the wave of the fp32 value with bits v (every
+// lane active); lane 63 ends with the total.
+__device__ __forceinline__ uint32_t wave_scan_incl_f32(uint32_t v) {
+    float x = __uint_as_float(v);
+    x += __uint_as_float(dpp<0x111>(__float_as_uint(x)));
+    x += __uint_as_float(dpp<0x112>(__float_as_uint(x)));
+    x += __uint_as_float(dpp<0x114>(__float_as_uint(x)));
+    x += __uint_as_float(dpp<0x118>(__float_as_uint(x)));
+    x += __uint_as_float(dpp<0x142, 0xA>(__float_as_uint(x)));
+    x += __uint_as_float(dpp<0x143, 0xC>(__float_as_uint(x)));
+    return __float_as_uint(x);
+}
+
 // v of the lane below (0 in lane 0; every lane active).
 __device__ __forceinline__ uint32_t lane_below(uint32_t v) { return dpp<0x138>(v); }
 
@@ -684,25 +703,194 @@ __device__ __forceinline__ void sm_issue(SmBatch<kMode>& B, const DevTensor& T, 
     }
 }
 
-// Sum of v over the wave (every lane active).
-__device__ __forceinline__ float wave_sum(float v) {
+// The diagonal of a 16x16 MFMA result summed over the wave, in lane 63.
+// Lane l holds result rows 4 (l / 16) + r, r < 4, of column l % 16, so its
+// diagonal element (if any) is r = l % 16 - 4 (l / 16).
+__device__ __forceinline__ float mfma_diag_sum(const f32x4& d) {
+    const int lane = threadIdx.x & 63;
+    const int r = (lane & 15) - 4 * (lane >> 4);
+    uint32_t v = 0;
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-    return v;
+    for (int j = 0; j < 4; ++j) v |= __float_as_uint(d[j]) & (r == j ? 0xFFFFFFFFu : 0u);
+    return __uint_as_float(wave_scan_incl_f32(v));
 }
 
-// Add the wave's per-row sums in acc to y[b][row] (one atomic per batch row,
-// from lane 0) and clear them.
-__device__ __forceinline__ void gemv_flush(const GemvArgs& G, float (&acc)[kGemvMaxBatch],
+// Add the wave's accumulated products for y[b][row], b < nb, to y (one
+// atomic per batch row, from lane 63) and clear the accumulators.
+template <int kB>
+__device__ __forceinline__ void gemv_flush(const GemvArgs& G, int nb, f32x4 (&acc)[kB],
                                            uint32_t row) {
 #pragma unroll
-    for (int b = 0; b < kGemvMaxBatch; ++b) {
-        if (b >= G.batch) break;
-        const float s = wave_sum(acc[b]);
-        if ((threadIdx.x & 63) == 0 && s != 0.0f)
+    for (int b = 0; b < kB; ++b) {
+        if (b >= nb) break;
+        const float s = mfma_diag_sum(acc[b]);
+        if ((threadIdx.x & 63) == 63 && s != 0.0f)
             atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + row, s);
-        acc[b] = 0.0f;
+        acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
+}
+
+// Sum of the products of 8 bf16 weights and 8 bf16 x values, in fp32.
+__device__ __forceinline__ float dot8_bf16(const uint4& w, const uint4& x) {
+    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t xv[4] = {x.x, x.y, x.z, x.w};
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        s += __uint_as_float(wv[q] << 16) * __uint_as_float(xv[q] << 16);
+        s += __uint_as_float(wv[q] & 0xFFFF0000u) * __uint_as_float(xv[q] & 0xFFFF0000u);
+    }
+    return s;
+}
+
+// Column col moved on by step elements of a row of cols.
+__device__ __forceinline__ void advance_col(uint32_t& col, uint32_t step, uint32_t cols) {
+    col += step;
+    while (col >= cols) col -= cols;
+}
+
+// The 8 x values at column col of each batch row b < nb (col < cols, and
+// col % 8 == 0 with a 16-byte-aligned x, so the reads are in bounds and
+// aligned). Rows b >= nb are left zero.
+template <int kB>
+__device__ __forceinline__ void gemv_load_x(uint4 (&dst)[kB], const GemvArgs& G, int nb,
+                                            uint32_t col) {
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+        dst[b] = make_uint4(0u, 0u, 0u, 0u);
+        if (b < nb)
+            dst[b] = *reinterpret_cast<const uint4*>(G.x + static_cast<int64_t>(b) * G.cols + col);
+    }
+}
+
+// (row, col) of an element moved on by 4096 elements (step_rows rows and
+// step_cols columns, step_cols < cols): one add and at most one wrap.
+__device__ __forceinline__ void step_rc(uint32_t& row, uint32_t& col, const GemvArgs& G) {
+    row += G.step_rows;
+    col += G.step_cols;
+    const bool wrap = col >= G.cols;
+    col = wrap ? col - G.cols : col;
+    row += wrap ? 1u : 0u;
+}
+
+// Fused GEMV over one staged round when the workgroup is one chunk. Thread i
+// holds group i + 512 k, so at each step k wave w's 64 groups are the 512
+// consecutive elements from a0 + 8 (64 w + 512 k). Their first row and
+// column are tracked for the whole wave as scalars, each lane's own as
+// registers, both by step_rc (no division past the first step). When the
+// 512 lie in one row (all but about 512 / cols of the steps for
+// cols >= 512), one MFMA per x vector takes the wave's products: lane l
+// supplies its 8 weights as A row l % 16 and its 8 x values as B column
+// l % 16 over the same k, so the diagonal of the 16x16 result holds the sums
+// of each lane's own products (dead lanes supply zeros). The accumulator is
+// reduced over the wave and added to y when the row changes. A step that
+// crosses a row boundary (about 512 / cols of them) takes two masked MFMAs,
+// the lanes of the first row and then those of the second, with the first
+// row's sum added in between: two atomics per x vector instead of one per
+// lane (per-lane atomics at one step in 34 on 17408-column rows made up
+// most of the fused GEMV's time). Only rows shorter than 512 elements take
+// per-lane atomics. Liveness is applied as masks, so the step is straight
+// code. With one x vector its words are requested kXAhead steps ahead of
+// use; every x read is in bounds, since a column is always below cols.
+template <int kMode, int kGroup>
+__device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch], const GemvArgs& G,
+                                                 const uint8_t* stage, uint32_t a0, uint32_t nfull,
+                                                 uint32_t i) {
+    static_assert(kThreads * kGroup == 4096, "step_rows / step_cols are for 4096 elements");
+    constexpr int kB = kMode == kModeGemv1 ? 1 : kGemvMaxBatch;
+    constexpr uint32_t kXAhead = kMode == kModeGemv1 ? 3 : 0;
+    constexpr uint32_t kSpan = 64 * kGroup;  // elements a wave holds at one step
+    const int nb = kMode == kModeGemv1 ? 1 : G.batch;
+    const uint32_t cols = G.cols;
+    const uint32_t lane = i & 63;
+    const uint32_t wave_first = uniform(i - lane);  // first thread of this wave
+    const uint32_t wave_el = uniform(a0 + wave_first * kGroup);
+    uint32_t er = wave_el / cols;  // row and column of the wave's first element
+    uint32_t ec = wave_el - er * cols;
+    const uint32_t lane_el = wave_el + lane * kGroup;
+    uint32_t lr = lane_el / cols;  // row and column of this lane's group
+    uint32_t lc = lane_el - lr * cols;
+    uint32_t lr_ld = lr, lc_ld = lc;  // the same for the next step whose x is requested
+    uint4 xq[kXAhead + 1][kB];
+#pragma unroll
+    for (uint32_t k = 0; k < kXAhead && k < kStoreBatch; ++k) {
+        if (k > 0) step_rc(lr_ld, lc_ld, G);
+        gemv_load_x<kB>(xq[k], G, nb, lc_ld);
+    }
+    f32x4 acc[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t acc_row = 0xFFFFFFFFu;
+#pragma unroll
+    for (uint32_t k = 0; k < kStoreBatch; ++k) {
+        if (k + kXAhead < kStoreBatch) {
+            if (k + kXAhead > 0) step_rc(lr_ld, lc_ld, G);
+            gemv_load_x<kB>(xq[(k + kXAhead) % (kXAhead + 1)], G, nb, lc_ld);
+        }
+        if (k > 0) {
+            step_rc(er, ec, G);
+            step_rc(lr, lc, G);
+        }
+        if (k * kThreads + wave_first >= nfull) break;  // this wave's groups are done
+        const uint4(&xc)[kB] = xq[k % (kXAhead + 1)];
+        const uint32_t v = k * kThreads + i;
+        const uint32_t m = v < nfull ? 0xFFFFFFFFu : 0u;  // live group
+        const uint2 e = *reinterpret_cast<const uint2*>(stage + v * kGroup);
+        uint4 w;
+        w.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, e.x) & m;
+        w.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, e.x) & m;
+        w.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, e.y) & m;
+        w.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, e.y) & m;
+        if (ec + kSpan <= cols) {
+            if (er != acc_row) {
+                if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);
+                acc_row = er;
+            }
+#pragma unroll
+            for (int b = 0; b < kB; ++b) {
+                if (b >= nb) break;
+                const uint4 xz = make_uint4(xc[b].x & m, xc[b].y & m, xc[b].z & m, xc[b].w & m);
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, xz), acc[b], 0, 0, 0);
+            }
+        } else if (cols >= kSpan) {
+            // Two rows: lanes below the boundary finish row er, the rest
+            // start row er + 1.
+            if (er != acc_row) {
+                if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);
+                acc_row = er;
+            }
+            const uint32_t lo = lr == er ? 0xFFFFFFFFu : 0u;
+            const uint4 w_lo = make_uint4(w.x & lo, w.y & lo, w.z & lo, w.w & lo);
+            const uint4 w_hi = make_uint4(w.x & ~lo, w.y & ~lo, w.z & ~lo, w.w & ~lo);
+#pragma unroll
+            for (int b = 0; b < kB; ++b) {
+                if (b >= nb) break;
+                const uint32_t ml = m & lo;
+                const uint4 xz = make_uint4(xc[b].x & ml, xc[b].y & ml, xc[b].z & ml, xc[b].w & ml);
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8, w_lo), __builtin_bit_cast(bf16x8, xz), acc[b], 0, 0, 0);
+            }
+            gemv_flush<kB>(G, nb, acc, er);
+            acc_row = er + 1;
+#pragma unroll
+            for (int b = 0; b < kB; ++b) {
+                if (b >= nb) break;
+                const uint32_t mh = m & ~lo;
+                const uint4 xz = make_uint4(xc[b].x & mh, xc[b].y & mh, xc[b].z & mh, xc[b].w & mh);
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8, w_hi), __builtin_bit_cast(bf16x8, xz), acc[b], 0, 0, 0);
+            }
+        } else if (m != 0u) {
+            // Rows shorter than a wave's 512 elements: per-lane atomics.
+#pragma unroll
+            for (int b = 0; b < kB; ++b) {
+                if (b >= nb) break;
+                atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + lr, dot8_bf16(w, xc[b]));
+            }
+        }
+    }
+    if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);
 }
 
 // Vector groups [0, nfull) of the staged round to output elements a0...;
@@ -778,20 +966,47 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
         }
         return;
     }
+    if constexpr (kWhole && (kMode == kModeGemv || kMode == kModeGemv1)) {
+        gemv_round_whole<kMode, kGroup>(sm, G, stage, static_cast<uint32_t>(a0), nfull, i);
+        return;
+    }
     // Fused GEMV: each group's 8 weights (one matrix row, as cols % 8 == 0)
-    // are multiplied by x in registers. A wave's groups at one k usually lie
-    // in one row: their products are summed per lane and reduced over the
-    // wave when the row changes; a wave that straddles a row boundary adds
-    // that group's products with per-lane atomics.
+    // meet the 8 x values of their columns. When a wave's live groups at one
+    // k lie in one row (the usual case), one MFMA per x vector takes the
+    // wave's products: lane l supplies its weights as A row l % 16 and its x
+    // as B column l % 16 over the same 8 k, so the diagonal of the 16x16
+    // result holds the sums of each lane's own products (dead lanes supply
+    // zeros). The accumulator is reduced over the wave and added to y when
+    // the row changes. A wave that straddles a row boundary takes that
+    // group's products on the VALU and adds them with per-lane atomics.
+    // With one x vector its words are requested kXAhead groups ahead of use
+    // (a group's column is always below cols, so every read is in bounds,
+    // live group or not); with up to four there are no registers for that.
+    constexpr int kB = kMode == kModeGemv1 ? 1 : kGemvMaxBatch;
+    constexpr uint32_t kXAhead = kMode == kModeGemv1 ? 3 : 0;
+    const int nb = kMode == kModeGemv1 ? 1 : G.batch;
     const uint32_t cols = G.cols;
-    uint32_t el = static_cast<uint32_t>(a0) + i * kGroup;  // element of group k = 0
+    const uint32_t el = static_cast<uint32_t>(a0) + i * kGroup;  // element of group k = 0
     uint32_t row = el / cols;
     uint32_t col = el - row * cols;
     const uint32_t step = tpc * kGroup;
-    float acc[kGemvMaxBatch] = {0.0f, 0.0f, 0.0f, 0.0f};
+    uint4 xq[kXAhead + 1][kB];
+    uint32_t col_ld = col;  // column of the next group whose x is requested
+#pragma unroll
+    for (uint32_t k = 0; k < kXAhead && k < kStoreBatch; ++k) {
+        if (k > 0) advance_col(col_ld, step, cols);
+        gemv_load_x<kB>(xq[k], G, nb, col_ld);
+    }
+    f32x4 acc[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     uint32_t acc_row = 0xFFFFFFFFu;
 #pragma unroll
     for (uint32_t k = 0; k < kStoreBatch; ++k) {
+        if (k + kXAhead < kStoreBatch) {
+            if (k + kXAhead > 0) advance_col(col_ld, step, cols);
+            gemv_load_x<kB>(xq[(k + kXAhead) % (kXAhead + 1)], G, nb, col_ld);
+        }
         if (k > 0) {
             col += step;
             while (col >= cols) {
@@ -799,45 +1014,40 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
                 ++row;
             }
         }
+        const uint4(&xc)[kB] = xq[k % (kXAhead + 1)];
         const uint32_t v = k * tpc + i;
         const bool live = v < nfull;
-        float p[kGemvMaxBatch] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (live) {
-            const uint32_t o[4] = {bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, ev[k].x),
-                                   bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, ev[k].x),
-                                   bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, ev[k].y),
-                                   bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, ev[k].y)};
-#pragma unroll
-            for (int b = 0; b < kGemvMaxBatch; ++b) {
-                if (b >= G.batch) break;
-                const uint4 xv = *reinterpret_cast<const uint4*>(
-                    G.x + static_cast<int64_t>(b) * cols + col);
-                const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-                float s = 0.0f;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    s += __uint_as_float(o[q] << 16) * __uint_as_float(xw[q] << 16);
-                    s += __uint_as_float(o[q] & 0xFFFF0000u) * __uint_as_float(xw[q] & 0xFFFF0000u);
-                }
-                p[b] = s;
-            }
-        }
         const uint64_t lm = __builtin_amdgcn_ballot_w64(live);
         if (lm == 0) continue;
+        // Staged exponents read here rather than all at once: registers.
+        const uint2 e = *reinterpret_cast<const uint2*>(stage + (kWhole || live ? v : 0u) * kGroup);
+        uint4 w;
+        w.x = live ? bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, e.x) : 0u;
+        w.y = live ? bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, e.x) : 0u;
+        w.z = live ? bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, e.y) : 0u;
+        w.w = live ? bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, e.y) : 0u;
         const uint32_t r0 = __builtin_amdgcn_readlane(row, __builtin_ctzll(lm));
         if (__builtin_amdgcn_ballot_w64(live && row != r0) == 0) {
             if (r0 != acc_row) {
-                if (acc_row != 0xFFFFFFFFu) gemv_flush(G, acc, acc_row);
+                if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);
                 acc_row = r0;
             }
 #pragma unroll
-            for (int b = 0; b < kGemvMaxBatch; ++b) acc[b] += p[b];
+            for (int b = 0; b < kB; ++b) {
+                if (b >= nb) break;
+                const uint4 xz = live ? xc[b] : make_uint4(0u, 0u, 0u, 0u);
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, xz), acc[b], 0, 0, 0);
+            }
         } else if (live) {
-            for (int b = 0; b < G.batch; ++b)
-                atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + row, p[b]);
+#pragma unroll
+            for (int b = 0; b < kB; ++b) {
+                if (b >= nb) break;
+                atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + row, dot8_bf16(w, xc[b]));
+            }
         }
     }
-    if (acc_row != 0xFFFFFFFFu) gemv_flush(G, acc, acc_row);
+    if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);
 }
 
 // Window table and the first kLdsEscBlocks escape blocks of a table blob to LDS.
@@ -1169,7 +1379,7 @@ int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny) {
     if (t.n_symbols > INT32_MAX)
         return fail(AIMG_ERR_UNSUPPORTED, who + "more than 2^31 - 1 symbols");
     const bool need_sm = kMode != kModeU8;
-    const bool need_out = kMode != kModeGemv;
+    const bool need_out = kMode != kModeGemv && kMode != kModeGemv1;
     if (t.packed == nullptr || t.chunk_offsets == nullptr || t.chunk_nbytes == nullptr ||
         (need_out && t.out == nullptr) || t.table == nullptr ||
         (need_sm && t.sign_mantissa == nullptr))
@@ -1246,10 +1456,13 @@ extern "C" int aimg_decode_gemv_bf16(const aimg_tensor* t, int64_t rows, int64_t
         return fail(AIMG_ERR_INVALID_ARGUMENT,
                     "batch must be in 1.." + std::to_string(aimg::kGemvMaxBatch));
     if (x == nullptr || y == nullptr) return fail(AIMG_ERR_INVALID_ARGUMENT, "null x or y");
+    const uint32_t step = aimg::kThreads * 8;  // elements between a thread's groups
     const aimg::GemvArgs g{static_cast<const uint16_t*>(x), y, static_cast<uint32_t>(rows),
-                           static_cast<uint32_t>(cols), batch};
+                           static_cast<uint32_t>(cols), batch,
+                           step / static_cast<uint32_t>(cols), step % static_cast<uint32_t>(cols)};
     // The 8-weight groups take 16-byte x loads: they must lie inside one row
     // (cols % 8 == 0) and x must be 16-byte aligned.
     const bool vec_ok = cols % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    if (batch == 1) return aimg::launch<aimg::kModeGemv1>(t, 1, g, vec_ok, stream);
     return aimg::launch<aimg::kModeGemv>(t, 1, g, vec_ok, stream);
 }

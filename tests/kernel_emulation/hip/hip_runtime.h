@@ -196,6 +196,12 @@ struct __attribute__((aligned(16))) uint4 {
     uint32_t x, y, z, w;
 };
 inline uint2 make_uint2(uint32_t a, uint32_t b) { return {a, b}; }
+inline uint4 make_uint4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) { return {a, b, c, d}; }
+inline uint32_t __float_as_uint(float f) {
+    uint32_t v;
+    std::memcpy(&v, &f, 4);
+    return v;
+}
 inline float __uint_as_float(uint32_t v) {
     float f;
     std::memcpy(&f, &v, 4);
@@ -215,6 +221,13 @@ inline float atomicAdd(float* p, float v) {
 }
 inline int __ffs(int x) { return __builtin_ffs(x); }
 inline void __builtin_amdgcn_s_setprio(int) {}  // wave issue priority: no effect here
+// Matrix-core product: used by the fused GEMV only, which is not modelled.
+typedef __bf16 emu_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float emu_f32x4 __attribute__((ext_vector_type(4)));
+inline emu_f32x4 __builtin_amdgcn_mfma_f32_16x16x32_bf16(emu_bf16x8, emu_bf16x8, emu_f32x4 c, int, int, int) {
+    __builtin_trap();
+    return c;
+}
 
 template <typename K, typename... A>
 inline void emu_launch(K kernel, dim3 g, dim3 b, A... args) {

@@ -50,10 +50,14 @@ def test_down_proj_5120x17408(down_proj, batch):
 
 @pytest.mark.parametrize("batch", [1, 2, 3, 4])
 @pytest.mark.parametrize("shape,chunk", [((64, 96), 256), ((40, 1000), 4096), ((7, 1024), 16),
-                                         ((33, 1001), 512), ((96, 4104), 65536)])
+                                         ((33, 1001), 512), ((96, 4104), 65536),
+                                         ((1500, 200), 65536), ((260, 512), 65536),
+                                         ((130, 1032), 65536)])
 def test_small_shapes(shape, chunk, batch):
     """Sub-group chunks (16 symbols), rows shorter and longer than a chunk,
-    and cols % 8 != 0 (element-wise products)."""
+    cols % 8 != 0 (element-wise products), and 512-thread chunks whose
+    64-group wave steps span several rows (cols 200), exactly one (512) or
+    cross a row boundary now and then (1032)."""
     W = workloads.bf16_normal(shape, 5 + shape[1], 0.02, outlier_frac=1e-2)
     layer = compress_layer(W, chunk_size=chunk)
     x = _x(batch, shape[1], shape[0])
