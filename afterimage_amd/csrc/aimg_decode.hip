@@ -90,6 +90,11 @@ constexpr uint32_t kStagePadded =
 // decodes. A round of bf16 weights fills about 8 groups per thread; the rest
 // are loaded at the store, by waves that need them.
 constexpr uint32_t kSmAhead = 9;
+// Cache-policy operand of the bf16 output stores: non-temporal (streamed
+// past the caches' normal retention). The output is written once; 4.5%
+// faster on the 5120x17408 layer than the default policy, while the same
+// policy on the stream-word or sign/mantissa loads was 2.5% slower.
+constexpr int kCachePolicyNT = 2;
 static_assert(kSmAhead <= kStoreBatch, "kSmAhead");
 
 struct DevTensor {
@@ -962,7 +967,7 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
             o4[1] = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, ev[k].x);
             o4[2] = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, ev[k].y);
             o4[3] = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, ev[k].y);
-            __builtin_amdgcn_raw_buffer_store_b128(o4, rs, vo, 16u * k * tpc, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(o4, rs, vo, 16u * k * tpc, kCachePolicyNT);
         }
         return;
     }
