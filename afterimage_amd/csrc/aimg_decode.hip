@@ -1044,11 +1044,26 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
                 acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                     __builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, xz), acc[b], 0, 0, 0);
             }
-        } else if (live) {
+        } else {
+            // Several rows: one wave sum and one atomic per distinct row
+            // instead of one atomic per lane (small chunks put several
+            // chunks, and often several rows, in one wave step).
+            float p[kB];
 #pragma unroll
-            for (int b = 0; b < kB; ++b) {
-                if (b >= nb) break;
-                atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + row, dot8_bf16(w, xc[b]));
+            for (int b = 0; b < kB; ++b) p[b] = live ? dot8_bf16(w, xc[b]) : 0.0f;
+            uint64_t left = lm;  // live lanes whose products are not yet added
+            while (left != 0) {
+                const uint32_t rr = __builtin_amdgcn_readlane(row, __builtin_ctzll(left));
+                const bool mine = live && row == rr;
+                left &= ~__builtin_amdgcn_ballot_w64(mine);
+#pragma unroll
+                for (int b = 0; b < kB; ++b) {
+                    if (b >= nb) break;
+                    const float sum =
+                        __uint_as_float(wave_scan_incl_f32(__float_as_uint(mine ? p[b] : 0.0f)));
+                    if ((threadIdx.x & 63) == 63 && sum != 0.0f)
+                        atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + rr, sum);
+                }
             }
         }
     }
