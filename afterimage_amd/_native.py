@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before the library; see module doc)
 
 LIB_PATH = Path(__file__).resolve().parent / "libafterimage_decode.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 MAX_TENSORS = 32
 
 AIMG_OK = 0
@@ -67,6 +67,12 @@ _SIGNATURES = [
     ("aimg_decode_gemv_bf16", ctypes.c_int,
      [ctypes.POINTER(AimgTensor), ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
       ctypes.c_void_p, ctypes.c_void_p]),
+    ("aimg_recombine_bf16", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]),
+    ("aimg_cpu_decode_bf16", ctypes.c_int, [ctypes.POINTER(AimgTensor), ctypes.c_int, ctypes.c_int]),
+    ("aimg_cpu_decode_u8", ctypes.c_int, [ctypes.POINTER(AimgTensor), ctypes.c_int, ctypes.c_int]),
+    ("aimg_cpu_recombine_bf16", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]),
     ("aimg_pack_chunked", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
       ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64)]),

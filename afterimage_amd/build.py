@@ -32,7 +32,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]
-HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall"]
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-pthread"]
 
 
 def _torch_lib_dir() -> Path:
@@ -62,14 +62,16 @@ def build(verbose: bool = False) -> Path:
     inc = ["-I", str(INCLUDE), "-I", str(CSRC)]
     dev_obj = BUILD_DIR / "aimg_decode.o"
     host_obj = BUILD_DIR / "aimg_host.o"
+    cpu_obj = BUILD_DIR / "aimg_cpu.o"
     steps = [
         [hipcc, "-c", *HIP_FLAGS, *inc, str(CSRC / "aimg_decode.hip"), "-o", str(dev_obj)],
         ["g++", "-c", *HOST_FLAGS, *inc, str(CSRC / "aimg_host.cpp"), "-o", str(host_obj)],
+        ["g++", "-c", *HOST_FLAGS, *inc, str(CSRC / "aimg_cpu.cpp"), "-o", str(cpu_obj)],
     ]
     torch_lib = _torch_lib_dir()
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    steps.append(["g++", "-shared", "-o", str(tmp), str(dev_obj), str(host_obj),
-                  f"-L{torch_lib}", "-l:libamdhip64.so", "-Wl,--no-undefined"])
+    steps.append(["g++", "-shared", "-pthread", "-o", str(tmp), str(dev_obj), str(host_obj),
+                  str(cpu_obj), f"-L{torch_lib}", "-l:libamdhip64.so", "-Wl,--no-undefined"])
     for cmd in steps:
         if verbose:
             print(" ".join(cmd), flush=True)

@@ -1456,8 +1456,65 @@ int launch(const aimg_tensor* ts, int n, const GemvArgs& gemv, bool vec_ok, void
     return launch_batch<kMode>(tiny, s, true);
 }
 
+// Recombine of already-decoded exponents: out[i] = bf16 bits of (sm[i], e[i]).
+// kVec: the three pointers are 16-byte aligned, and each thread takes 16
+// elements per step (two 16-byte loads, two 16-byte stores); otherwise one
+// element per step.
+template <bool kVec>
+__global__ __launch_bounds__(256) void recombine_kernel(const uint8_t* e, const uint8_t* sm,
+                                                        uint16_t* out, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    int64_t done = 0;
+    if (kVec) {
+        const int64_t nvec = n / 16;
+        for (int64_t v = t0; v < nvec; v += stride) {
+            const uint4 ev = reinterpret_cast<const uint4*>(e)[v];
+            const uint4 sv = reinterpret_cast<const uint4*>(sm)[v];
+            const uint32_t ew[4] = {ev.x, ev.y, ev.z, ev.w};
+            const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+            v4u32 o[2];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                o[q / 2][2 * (q % 2)] = bf16_pair<0x01010000u, 0x010C000Cu>(sw[q], ew[q]);
+                o[q / 2][2 * (q % 2) + 1] = bf16_pair<0x03030202u, 0x030C020Cu>(sw[q], ew[q]);
+            }
+            v4u32* dst = reinterpret_cast<v4u32*>(out + 16 * v);
+            __builtin_nontemporal_store(o[0], dst);
+            __builtin_nontemporal_store(o[1], dst + 1);
+        }
+        done = nvec * 16;
+    }
+    for (int64_t i = done + t0; i < n; i += stride) out[i] = bf16_one(sm[i], e[i]);
+}
+
 }  // namespace
 }  // namespace aimg
+
+extern "C" int aimg_recombine_bf16(const uint8_t* exponent, const uint8_t* sign_mantissa,
+                                   void* out, int64_t n, void* stream) {
+    using aimg::fail;
+    if (n < 0) return fail(AIMG_ERR_INVALID_ARGUMENT, "n must be >= 0");
+    if (n == 0) return AIMG_OK;
+    if (exponent == nullptr || sign_mantissa == nullptr || out == nullptr)
+        return fail(AIMG_ERR_INVALID_ARGUMENT, "null pointer passed to aimg_recombine_bf16");
+    const bool vec = (reinterpret_cast<uintptr_t>(exponent) | reinterpret_cast<uintptr_t>(sign_mantissa) |
+                      reinterpret_cast<uintptr_t>(out)) % 16 == 0;
+    const int64_t per_thread = vec ? 16 : 1;
+    const int64_t want = (n / per_thread + 255) / 256;
+    const int64_t cap = static_cast<int64_t>(aimg::cu_count()) * 8;
+    const dim3 grid(static_cast<uint32_t>(want < 1 ? 1 : (want < cap ? want : cap))), block(256);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    auto* o = static_cast<uint16_t*>(out);
+    if (vec)
+        hipLaunchKernelGGL((aimg::recombine_kernel<true>), grid, block, 0, s, exponent, sign_mantissa, o, n);
+    else
+        hipLaunchKernelGGL((aimg::recombine_kernel<false>), grid, block, 0, s, exponent, sign_mantissa, o, n);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+        return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    return AIMG_OK;
+}
 
 extern "C" int aimg_decode_bf16(const aimg_tensor* tensors, int n_tensors, void* stream) {
     return aimg::launch<aimg::kModeBf16>(tensors, n_tensors, aimg::GemvArgs{}, true, stream);

@@ -8,7 +8,7 @@
 
 namespace aimg {
 
-constexpr int kAbiVersion = 6;
+constexpr int kAbiVersion = 7;
 constexpr uint32_t kTableMagic = 0x474D4941u;  // "AIMG"
 
 // Window table: for each 12-bit window, the codewords that lie wholly inside

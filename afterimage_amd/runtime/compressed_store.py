@@ -7,6 +7,8 @@ entropy-coded. Decompression runs one fused gfx950 kernel per slice: Huffman
 decode of the exponents and the bit recombine
 ``((sm & 0x80) << 8) | (e << 7) | (sm & 0x7F)`` write the bf16 output directly,
 so no exponent scratch tensor and no chain of elementwise torch kernels exist.
+With ``device="cpu"`` the same decode runs on the library's CPU threads, as the
+reference decodes on the CPU for a CPU device (compressed_store.py:171-180).
 """
 from __future__ import annotations
 
@@ -15,7 +17,7 @@ import dataclasses
 import numpy as np
 import torch
 
-from .device import DeviceTensor, decode_bf16, decode_gemv
+from .device import DeviceTensor, cpu_decode, decode_bf16, decode_gemv, recombine_bf16
 from .huffman_chunked import ChunkedEncoded, encode_chunked, lengths_from_counts, symbol_counts
 
 EXPONENT_SHIFT = 7
@@ -97,20 +99,20 @@ def compress_group(weights: list[torch.Tensor], chunk_size: int = 1024, max_bits
 
 def _recombine(exponent: torch.Tensor, sign_mantissa: torch.Tensor,
                shape: tuple) -> torch.Tensor:
-    """bf16 from decoded exponents and sign/mantissa bytes, in int16 throughout
-    (compressed_store.py:94-114): setting bit 15 of a value below 32768 is
-    subtracting 32768 in two's complement."""
-    e16 = exponent.to(torch.int16)
-    sm16 = sign_mantissa.to(torch.int16)
-    bits = (e16 << EXPONENT_SHIFT) | (sm16 & 0x7F)
-    bits = torch.where(sign_mantissa >= 128, bits - 32768, bits)
-    return bits.view(torch.bfloat16).reshape(shape)
+    """bf16 tensor of ``shape`` from decoded exponents and sign/mantissa bytes
+    (the role of compressed_store.py:94-114), in one native pass: a gfx950
+    kernel for GPU tensors, the library's host loop for CPU tensors. Exponents
+    of another integer dtype are taken modulo 256 (they are bytes)."""
+    e = exponent if exponent.dtype == torch.uint8 else exponent.to(torch.uint8)
+    sm = sign_mantissa if sign_mantissa.dtype == torch.uint8 else sign_mantissa.to(torch.uint8)
+    return recombine_bf16(e, sm).reshape(shape)
 
 
 def recombine_exponent_and_sign_mantissa(exponent, sign_mantissa, shape: tuple,
                                          device: str) -> torch.Tensor:
     """Combine already-decoded exponents with sign/mantissa bytes
-    (compressed_store.py:117-130)."""
+    (compressed_store.py:117-130): numpy arrays or tensors on any device are
+    moved to ``device`` first, then combined there."""
     exp = torch.as_tensor(exponent, device=device)
     sm = torch.as_tensor(sign_mantissa, device=device)
     return _recombine(exp, sm, shape)
@@ -137,15 +139,29 @@ def _slice_encoded(enc: ChunkedEncoded, c0: int, c1: int) -> ChunkedEncoded:
     )
 
 
+def _is_cpu(device) -> bool:
+    return torch.device(device).type == "cpu"
+
+
 def _gpu_device(device) -> torch.device:
     dev = torch.device(device)
     if dev.type != "cuda":
         raise RuntimeError(
-            "afterimage_amd decodes on the GPU only (device %r); there is no CPU "
-            "decode path in this package" % (str(device),))
+            "the gfx950 decoder runs on a GPU (device %r); use device='cpu' for the "
+            "CPU decoder" % (str(device),))
     if dev.index is None:
         dev = torch.device("cuda", torch.cuda.current_device())
     return dev
+
+
+def _decode_cpu_into(layer: CompressedLayer, c0: int, c1: int, out_flat: torch.Tensor,
+                     take: int) -> None:
+    """Decode chunks [c0, c1) of ``layer`` on the CPU into ``out_flat[:take]``."""
+    enc = layer.encoded
+    sub = enc if (c0 == 0 and c1 == enc.n_chunks) else _slice_encoded(enc, c0, c1)
+    s0 = c0 * enc.chunk_size
+    sm = layer.sign_mantissa.reshape(-1)[s0: s0 + take]
+    cpu_decode([(sub, sm, out_flat, take)])
 
 
 def _tables_for(enc: ChunkedEncoded, dev: torch.device):
@@ -177,11 +193,18 @@ def decompress_layer_gpu(layer: CompressedLayer, device: str = "cuda",
     written in place slice by slice. With ``reuse_decode_tables`` the tables
     are prepared once for the whole call; otherwise once per slice (both go
     through the content-keyed table cache). Work is ordered on the current
-    stream of ``device``; nothing here synchronises.
+    stream of ``device``; nothing here synchronises. On a CPU device the
+    library's CPU decoder writes the output directly (no slices are needed to
+    bound memory there) and the call returns when it is done.
     """
-    dev = _gpu_device(device)
     enc = layer.encoded
     n = enc.n_symbols
+    if _is_cpu(device):
+        out = torch.empty(n, dtype=torch.bfloat16)
+        if n:
+            _decode_cpu_into(layer, 0, enc.n_chunks, out, n)
+        return out.reshape(layer.shape)
+    dev = _gpu_device(device)
     out = torch.empty(n, dtype=torch.bfloat16, device=dev)
     if n == 0:
         return out.reshape(layer.shape)
@@ -208,7 +231,8 @@ def decompress_rows_gpu(layer: CompressedLayer, row_start: int, row_end: int,
     if len(layer.shape) != 2:
         raise ValueError("decompress_rows_gpu needs a 2D tensor, got shape %r"
                          % (layer.shape,))
-    dev = _gpu_device(device)
+    cpu = _is_cpu(device)
+    dev = torch.device("cpu") if cpu else _gpu_device(device)
     rows, cols = layer.shape
     row_start = max(0, row_start)
     row_end = min(rows, row_end)
@@ -222,8 +246,20 @@ def decompress_rows_gpu(layer: CompressedLayer, row_start: int, row_end: int,
     base = c0 * cs
     avail = min(enc.n_symbols, c1 * cs) - base
     flat = torch.empty(avail, dtype=torch.bfloat16, device=dev)
-    _decode_range_into(layer, c0, c1, flat, avail, dev, _tables_for(enc, dev))
+    if cpu:
+        _decode_cpu_into(layer, c0, c1, flat, avail)
+    else:
+        _decode_range_into(layer, c0, c1, flat, avail, dev, _tables_for(enc, dev))
     return flat[e0 - base:e1 - base].reshape(row_end - row_start, cols)
+
+
+def decompress_layer_cpu_reference(layer: CompressedLayer) -> torch.Tensor:
+    """The exact original bf16 tensor decoded on the CPU
+    (compressed_store.py:243-251). The reference uses its pure-Python reader
+    here; this package decodes with the library's CPU decoder, whose output is
+    the same on every valid stream (it reads the same validated table as the
+    GPU kernel and is checked against the reference's decoded vectors)."""
+    return decompress_layer_gpu(layer, device="cpu")
 
 
 def decompress_matvec_gpu(layer: CompressedLayer, x: torch.Tensor,

@@ -17,6 +17,7 @@ import ctypes
 import dataclasses
 import hashlib
 import threading
+import weakref
 
 import numpy as np
 import torch
@@ -27,24 +28,84 @@ MAX_TENSORS = _native.MAX_TENSORS
 
 
 class DecodeTables(tuple):
-    """Device decode tables for one codebook: ``(blob, max_bits, key)``."""
+    """Decode tables for one codebook.
 
-    __slots__ = ()
+    Unpacks like the reference's ``prepare_decode_tables`` result
+    (afterimage/runtime/gpu_decode_v2.py:71-76): ``sym_lut, len_lut = tables``
+    gives the flat LUTs as int32 tensors on the table's device (rebuilt from
+    the blob, and only when read). The decoder itself reads ``blob``: the
+    compact window table of ``aimg_build_table``, on the device (or on the
+    host for the CPU decoder), shared by every tensor with this codebook.
+    ``key`` is the SHA-256 of the codebook content; ``host_blob`` a host copy.
+    """
 
-    def __new__(cls, blob: torch.Tensor, max_bits: int, key: bytes):
-        return super().__new__(cls, (blob, max_bits, key))
+    def __new__(cls, blob: torch.Tensor, max_bits: int, key: bytes, host_blob: np.ndarray):
+        self = super().__new__(cls, ())
+        self.blob = blob
+        self.max_bits = int(max_bits)
+        self.key = key
+        self.host_blob = host_blob
+        self._luts = None
+        return self
 
-    @property
-    def blob(self) -> torch.Tensor:
-        return self[0]
+    def _flat(self) -> tuple[torch.Tensor, torch.Tensor]:
+        if self._luts is None:
+            sym, ln = flat_luts_from_blob(self.host_blob, self.max_bits)
+            dev = self.blob.device
+            self._luts = (torch.from_numpy(sym).to(dev), torch.from_numpy(ln).to(dev))
+        return self._luts
 
-    @property
-    def max_bits(self) -> int:
-        return self[1]
+    def __len__(self) -> int:
+        return 2
 
-    @property
-    def key(self) -> bytes:
-        return self[2]
+    def __iter__(self):
+        return iter(self._flat())
+
+    def __getitem__(self, i):
+        return self._flat()[i]
+
+    def __repr__(self) -> str:
+        return "DecodeTables(max_bits=%d, key=%s, device=%s)" % (
+            self.max_bits, self.key.hex()[:12], self.blob.device)
+
+
+def flat_luts_from_blob(blob: np.ndarray, max_bits: int) -> tuple[np.ndarray, np.ndarray]:
+    """The flat (sym_lut, len_lut) of width ``max_bits`` that a table blob was
+    built from, as int32 arrays (build_decode_lut's layout,
+    afterimage/runtime/huffman.py:128-150: entry i is the codeword window i
+    starts with; windows no codeword covers hold (0, 0))."""
+    b = np.asarray(blob, dtype=np.uint8)
+    hdr = b[:64].view(np.uint32)
+    n_esc = int(hdr[6])
+    wsyms = b[_SYMS_OFF:_META_OFF].view(np.uint32)
+    wmeta = b[_META_OFF:_LEN_OFF]
+    len_of = b[_LEN_OFF:_ESC_OFF].astype(np.int32)
+    esc = b[_ESC_OFF:_ESC_OFF + 2 * 16 * n_esc].view(np.uint16).reshape(n_esc, 16)
+    mb = int(max_bits)
+    i = np.arange(1 << mb, dtype=np.int64)
+    bits16 = (i << (16 - mb)) if mb <= 16 else i  # the window's first 16 bits
+    w12 = (bits16 >> 4).astype(np.int64)
+    meta = wmeta[w12]
+    first = (wsyms[w12] & 0xFF).astype(np.int32)
+    sym = np.where(meta != 0, first, 0).astype(np.int32)
+    ln = np.where(meta != 0, len_of[first], 0).astype(np.int32)
+    escw = meta == 0
+    blk = (wsyms[w12] & 0xFFFF).astype(np.int64)
+    use = escw & (blk != 0xFFFF) & (blk < n_esc)
+    if use.any():
+        v = esc[blk[use], (bits16[use] & 15)].astype(np.int32)
+        sym[use] = np.where(v >> 8 != 0, v & 0xFF, 0)
+        ln[use] = v >> 8
+    return sym, ln
+
+
+# Table blob layout (aimg_internal.h): 64-byte header, window symbols (uint32
+# per 12-bit window), window meta (uint8), code length per symbol (256 B),
+# escape blocks (16 uint16 entries each).
+_SYMS_OFF = 64
+_META_OFF = _SYMS_OFF + 4 * 4096
+_LEN_OFF = _META_OFF + 4096
+_ESC_OFF = _LEN_OFF + 256
 
 
 def codebook_key(sym_lut: np.ndarray, len_lut: np.ndarray, max_bits: int) -> bytes:
@@ -73,36 +134,93 @@ def build_table_blob(sym_lut: np.ndarray, len_lut: np.ndarray, max_bits: int) ->
 
 
 class _TableCache:
-    """Small LRU of device tables keyed by (device, codebook content)."""
+    """LRU of decode tables keyed by (device, codebook content), bounded by the
+    bytes of the tables it holds.
 
-    def __init__(self, capacity: int = 64):
-        self.capacity = capacity
+    A lookup first tries the LUT arrays' identity: the same pair of array
+    objects (held by weak reference) at the same width returns its tables
+    without reading the arrays again. Other arrays are keyed by a SHA-256 of
+    their content, so equal codebooks share one table and different ones
+    never collide. A LUT array changed in place after a lookup is not read
+    again; pass a new array for a new codebook.
+
+    Device tables are recorded on the current stream of every lookup, so an
+    evicted table's memory is not reused while a launch queued on that
+    stream may still read it.
+    """
+
+    def __init__(self, capacity_bytes: int = 64 << 20):
+        self.capacity_bytes = capacity_bytes
         self._items: collections.OrderedDict = collections.OrderedDict()
+        self._by_id: dict = {}
         self._lock = threading.Lock()
+        self._bytes = 0
         self.builds = 0
+        self.hashes = 0
 
-    def get(self, sym_lut, len_lut, max_bits: int, device) -> DecodeTables:
+    @staticmethod
+    def _device(device) -> torch.device:
         dev = torch.device(device)
         if dev.type == "cuda" and dev.index is None:
             dev = torch.device("cuda", torch.cuda.current_device())
-        key = codebook_key(sym_lut, len_lut, max_bits)
+        return dev
+
+    def get(self, sym_lut, len_lut, max_bits: int, device) -> DecodeTables:
+        dev = self._device(device)
+        ident = (id(sym_lut), id(len_lut), int(max_bits), str(dev))
         with self._lock:
-            hit = self._items.get((str(dev), key))
+            hit = self._by_id.get(ident)
             if hit is not None:
-                self._items.move_to_end((str(dev), key))
-                return hit
-        blob = build_table_blob(sym_lut, len_lut, max_bits)
-        tables = DecodeTables(torch.from_numpy(blob).to(dev), int(max_bits), key)
+                sref, lref, ckey = hit
+                tables = self._items.get(ckey)
+                if sref() is sym_lut and lref() is len_lut and tables is not None:
+                    self._items.move_to_end(ckey)
+                    self._record(tables, dev)
+                    return tables
+                del self._by_id[ident]
+        key = codebook_key(sym_lut, len_lut, max_bits)
+        ckey = (str(dev), key)
         with self._lock:
-            self.builds += 1
-            self._items[(str(dev), key)] = tables
-            while len(self._items) > self.capacity:
-                self._items.popitem(last=False)
+            self.hashes += 1
+            tables = self._items.get(ckey)
+        if tables is None:
+            host = build_table_blob(sym_lut, len_lut, max_bits)
+            blob = torch.from_numpy(host)
+            if dev.type != "cpu":
+                blob = blob.to(dev)
+            tables = DecodeTables(blob, int(max_bits), key, host)
+            with self._lock:
+                self.builds += 1
+                if ckey not in self._items:
+                    self._items[ckey] = tables
+                    self._bytes += blob.numel()
+                tables = self._items[ckey]
+                while self._bytes > self.capacity_bytes and len(self._items) > 1:
+                    _, old = self._items.popitem(last=False)
+                    self._bytes -= old.blob.numel()
+        with self._lock:
+            self._items.move_to_end(ckey)
+            try:
+                self._by_id[ident] = (weakref.ref(sym_lut), weakref.ref(len_lut), ckey)
+            except TypeError:  # arrays without weak references: content key only
+                pass
+            if len(self._by_id) > 4 * max(1, len(self._items)) + 64:
+                live = set(self._items)
+                self._by_id = {k: v for k, v in self._by_id.items()
+                               if v[2] in live and v[0]() is not None and v[1]() is not None}
+        self._record(tables, dev)
         return tables
+
+    @staticmethod
+    def _record(tables: DecodeTables, dev: torch.device) -> None:
+        if dev.type == "cuda":
+            tables.blob.record_stream(torch.cuda.current_stream(dev))
 
     def clear(self) -> None:
         with self._lock:
             self._items.clear()
+            self._by_id.clear()
+            self._bytes = 0
 
 
 TABLES = _TableCache()
@@ -271,3 +389,103 @@ def decode_gemv(t: DeviceTensor, x: torch.Tensor, rows: int, cols: int,
             d, rows, cols, x.data_ptr(), b, y.data_ptr(), _stream_handle(dev)))
     return y
 
+
+
+# ---------------------------------------------------------------------------
+# Host (CPU) decode through the same library: aimg_cpu_decode_bf16 / _u8.
+# ---------------------------------------------------------------------------
+
+def host_array(a, dtype) -> np.ndarray:
+    """A C-contiguous, aligned host array of ``dtype`` with a's values: ``a``
+    itself when it already is one (for example a view into a store buffer),
+    otherwise a copy. Accepts numpy arrays and CPU tensors."""
+    if isinstance(a, torch.Tensor):
+        a = a.detach().cpu().numpy()
+    return np.require(a, dtype=dtype, requirements=["C", "A"])
+
+
+def default_threads() -> int:
+    """Threads for a host decode: torch's intra-op thread count (which follows
+    OMP_NUM_THREADS), so the decoder shares the CPU budget torch was given."""
+    return max(1, torch.get_num_threads())
+
+
+def cpu_decode(parts, n_threads: int | None = None, exponents_only: bool = False) -> None:
+    """Decode on the CPU threads of the native library.
+
+    ``parts``: (enc, sign_mantissa, out, n_out) per tensor, where ``enc`` is a
+    ChunkedEncoded (host arrays), ``out`` a contiguous CPU tensor (bf16, or
+    uint8 with ``exponents_only``) of at least n_out elements, and
+    ``sign_mantissa`` the host bytes of elements [0, n_out) (ignored with
+    ``exponents_only``). Returns when the outputs are written."""
+    parts = list(parts)
+    if not parts:
+        return
+    keep = []
+    arr = (_native.AimgTensor * len(parts))()
+    for j, (enc, sm, out, n_out) in enumerate(parts):
+        if out.device.type != "cpu" or not out.is_contiguous() or out.numel() < n_out:
+            raise ValueError("output %d must be a contiguous CPU tensor of >= %d elements" % (j, n_out))
+        want = torch.uint8 if exponents_only else torch.bfloat16
+        if out.dtype != want:
+            raise ValueError("output %d must be %s" % (j, want))
+        if n_out > int(enc.n_chunks) * int(enc.chunk_size):
+            raise ValueError("tensor %d: %d outputs exceed its %d chunks" % (j, n_out, enc.n_chunks))
+        tables = TABLES.get(enc.sym_lut, enc.len_lut, enc.max_bits, "cpu")
+        packed = host_array(enc.packed, np.uint8)
+        offs = host_array(enc.chunk_offsets, np.int32)
+        nbytes = host_array(enc.chunk_nbytes, np.int32)
+        if offs.shape[0] < enc.n_chunks or nbytes.shape[0] < enc.n_chunks:
+            raise ValueError("tensor %d: chunk tables shorter than n_chunks" % j)
+        smh = None
+        if not exponents_only:
+            smh = host_array(sm, np.uint8).reshape(-1)
+            if smh.shape[0] < n_out:
+                raise ValueError("tensor %d needs %d sign/mantissa bytes, got %d"
+                                 % (j, n_out, smh.shape[0]))
+        keep.append((packed, offs, nbytes, smh, tables))
+        d = arr[j]
+        d.packed = packed.ctypes.data if packed.size else None
+        d.chunk_offsets = offs.ctypes.data
+        d.chunk_nbytes = nbytes.ctypes.data
+        d.sign_mantissa = smh.ctypes.data if smh is not None else None
+        d.out = out.data_ptr()
+        d.table = tables.blob.data_ptr()
+        d.packed_nbytes = int(packed.size)
+        d.n_symbols = int(n_out)
+        d.chunk_size = int(enc.chunk_size)
+        d.n_chunks = int(enc.n_chunks)
+    threads = default_threads() if n_threads is None else int(n_threads)
+    fn = _native.lib().aimg_cpu_decode_u8 if exponents_only else _native.lib().aimg_cpu_decode_bf16
+    _native.check(fn(arr, len(parts), threads))
+    del keep
+
+
+def recombine_bf16(exponent: torch.Tensor, sign_mantissa: torch.Tensor) -> torch.Tensor:
+    """bf16 bits ((sm & 0x80) << 8) | (e << 7) | (sm & 0x7F) of two uint8
+    tensors on one device (GPU: one kernel on the current stream; CPU: the
+    library's host loop). Returns a flat bf16 tensor on that device."""
+    e = exponent.reshape(-1)
+    sm = sign_mantissa.reshape(-1)
+    if e.dtype != torch.uint8 or sm.dtype != torch.uint8:
+        raise ValueError("exponent and sign_mantissa must be uint8")
+    if e.numel() != sm.numel():
+        raise ValueError("exponent has %d elements, sign_mantissa %d" % (e.numel(), sm.numel()))
+    if e.device != sm.device:
+        raise ValueError("exponent on %s, sign_mantissa on %s" % (e.device, sm.device))
+    e = e.contiguous()
+    sm = sm.contiguous()
+    out = torch.empty(e.numel(), dtype=torch.bfloat16, device=e.device)
+    if e.numel() == 0:
+        return out
+    lib = _native.lib()
+    if e.device.type == "cuda":
+        with torch.cuda.device(e.device):
+            _native.check(lib.aimg_recombine_bf16(e.data_ptr(), sm.data_ptr(), out.data_ptr(),
+                                                  e.numel(), _stream_handle(e.device)))
+    elif e.device.type == "cpu":
+        _native.check(lib.aimg_cpu_recombine_bf16(e.data_ptr(), sm.data_ptr(), out.data_ptr(),
+                                                  e.numel()))
+    else:
+        raise RuntimeError("recombine runs on a GPU or the CPU; got %s" % e.device)
+    return out

@@ -4,8 +4,10 @@
 
 ``block_chunks`` keeps its validation (a power of 2, checked before ``enc`` is
 touched) so callers and configs behave the same, but it does not shape the
-launch: the HIP kernel assigns a 256-thread workgroup per chunk and splits
-each chunk's bitstream across the threads itself.
+launch: the HIP kernel runs persistent 512-thread workgroups that split into
+sub-groups of 16 to 512 threads, one chunk per sub-group, sized from the
+chunk length, and each sub-group splits its chunk's bitstream across its
+threads.
 """
 from __future__ import annotations
 
@@ -20,20 +22,22 @@ def _require_gpu(device) -> torch.device:
     dev = torch.device(device)
     if dev.type != "cuda":
         raise RuntimeError(
-            "afterimage_amd decodes on the GPU only (device %r); there is no CPU "
-            "decode path in this package" % (str(device),))
+            "decode_gpu_v2 runs on a GPU (device %r); CPU decoding goes through "
+            "decompress_layer_gpu(..., device='cpu')" % (str(device),))
     return dev
 
 
 def prepare_decode_tables(enc, device: str = "cuda") -> DecodeTables:
-    """Device decode tables for ``enc``'s codebook (gpu_decode_v2.py:71-76).
+    """Decode tables for ``enc``'s codebook on ``device`` (gpu_decode_v2.py:71-76).
 
-    Tables are cached by codebook content, so tensors that share a codebook
-    share one device table; different codebooks never collide.
+    ``sym_lut, len_lut = tables`` unpacks as the reference's int32 LUT pair;
+    the decoder reads the compact table blob the same object carries. Tables
+    are cached by codebook content, so tensors that share a codebook share
+    one table, and different codebooks never collide.
     """
     if int(enc.sym_lut.max(initial=0)) > 255:
         raise AssertionError(_SYMBOL_MSG)
-    return TABLES.get(enc.sym_lut, enc.len_lut, enc.max_bits, _require_gpu(device))
+    return TABLES.get(enc.sym_lut, enc.len_lut, enc.max_bits, torch.device(device))
 
 
 def decode_gpu_v2(enc, block_chunks: int = 32, device: str = "cuda", *,

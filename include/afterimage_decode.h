@@ -127,6 +127,38 @@ int aimg_decode_u8(const aimg_tensor* tensors, int n_tensors, void* stream);
 int aimg_decode_gemv_bf16(const aimg_tensor* t, int64_t rows, int64_t cols, const void* x,
                           int batch, float* y, void* stream);
 
+/*
+ * out[i] = ((sm[i] & 0x80) << 8) | (exponent[i] << 7) | (sm[i] & 0x7F) for
+ * i < n, on the GPU (all three pointers device memory; out is uint16 bf16
+ * bits). Replaces recombine_exponent_and_sign_mantissa and _recombine
+ * (afterimage/runtime/compressed_store.py:94-130) for device tensors: one
+ * kernel instead of a chain of elementwise torch kernels. 16-byte aligned
+ * pointers take the vector path; any alignment is correct.
+ */
+int aimg_recombine_bf16(const uint8_t* exponent, const uint8_t* sign_mantissa, void* out,
+                        int64_t n, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Host decode (CPU threads).                                                */
+/* Replaces the reference's CPU path: _decode_exponent with device "cpu"     */
+/* (afterimage/runtime/compressed_store.py:161-183) over decode_chunks_numba */
+/* (afterimage/runtime/cpu_decode.py:67-113), and _recombine on the CPU.     */
+/* Every pointer of the aimg_tensor descriptors is HOST memory here, and     */
+/* `table` is the host blob of aimg_build_table. The result equals the GPU   */
+/* entry points' on every input. n_threads <= 0 uses every hardware thread.  */
+/* The call returns when the work is done.                                   */
+/* ------------------------------------------------------------------------- */
+
+/* BF16 rebuild, as aimg_decode_bf16 (no size limit on n_symbols). */
+int aimg_cpu_decode_bf16(const aimg_tensor* tensors, int n_tensors, int n_threads);
+
+/* Exponent bytes only, as aimg_decode_u8. */
+int aimg_cpu_decode_u8(const aimg_tensor* tensors, int n_tensors, int n_threads);
+
+/* Host recombine, as aimg_recombine_bf16 (one thread). */
+int aimg_cpu_recombine_bf16(const uint8_t* exponent, const uint8_t* sign_mantissa, void* out,
+                            int64_t n);
+
 /* ------------------------------------------------------------------------- */
 /* Encoder support (host).                                                   */
 /* ------------------------------------------------------------------------- */

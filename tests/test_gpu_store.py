@@ -184,11 +184,73 @@ def test_batched_block_launch_with_shared_codebooks():
     assert t0.blob.data_ptr() == t1.blob.data_ptr()
 
 
-def test_cpu_device_is_refused():
+def test_cpu_device_decodes_the_same_bits():
     torch.manual_seed(20)
-    layer = compress_layer((torch.randn(16, 16) * 0.02).to(torch.bfloat16))
-    with pytest.raises(RuntimeError, match="GPU only"):
-        decompress_layer_gpu(layer, device="cpu")
+    W = (torch.randn(160, 96) * 0.02).to(torch.bfloat16)
+    layer = compress_layer(W, chunk_size=512)
+    cpu = decompress_layer_gpu(layer, device="cpu")
+    gpu = decompress_layer_gpu(layer, device="cuda")
+    assert cpu.device.type == "cpu"
+    assert torch.equal(_bits(cpu), _bits(gpu)) and torch.equal(_bits(cpu), _bits(W))
+
+
+@pytest.mark.parametrize("name", ["single_symbol", "skewed_2sym", "dirichlet_6", "bf16_outliers_64k",
+                                  "scales_3p0", "uniform256"])
+@pytest.mark.parametrize("chunk_size", [64, 4096, 65536])
+def test_cpu_and_gpu_decoders_agree_on_random_bytes(name, chunk_size):
+    """Arbitrary bytes under real codebooks, including ones with windows that
+    start no codeword (single_symbol, whose code is '0'): the host and GPU
+    decoders read one table blob and must agree on every position."""
+    from tests.golden_data import case
+
+    from afterimage_amd.runtime.huffman_chunked import ChunkedEncoded
+
+    base = case(name)["encoded"]
+    g = np.random.default_rng(chunk_size)
+    n_chunks = 5
+    nbytes = g.integers(0, chunk_size // 2 + 8, n_chunks).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(nbytes)[:-1]]).astype(np.int32)
+    packed = g.integers(0, 256, int(nbytes.sum()) + 8, dtype=np.uint8)
+    enc = ChunkedEncoded(packed=packed, chunk_offsets=offsets, chunk_nbytes=nbytes,
+                         sym_lut=base.sym_lut, len_lut=base.len_lut, max_bits=base.max_bits,
+                         chunk_size=chunk_size, n_symbols=n_chunks * chunk_size - 3,
+                         shape=(n_chunks * chunk_size - 3,))
+    gpu = gd.decode_gpu_v2(enc).cpu().numpy()
+    cpu = torch.empty(enc.n_symbols, dtype=torch.uint8)
+    devmod.cpu_decode([(enc, None, cpu, enc.n_symbols)], exponents_only=True)
+    assert np.array_equal(gpu, cpu.numpy())
+
+
+def test_recombine_kernel_on_every_byte_pair_and_offsets():
+    from afterimage_amd.runtime.compressed_store import recombine_exponent_and_sign_mantissa
+
+    e = np.repeat(np.arange(256, dtype=np.uint8), 256)
+    sm = np.tile(np.arange(256, dtype=np.uint8), 256)
+    want = oracle.recombine(e, sm).view(np.int16)
+    got = recombine_exponent_and_sign_mantissa(e, sm, (256, 256), "cuda")
+    assert got.is_cuda and got.dtype == torch.bfloat16 and tuple(got.shape) == (256, 256)
+    assert np.array_equal(_bits(got).numpy().reshape(-1), want)
+    # Unaligned starts and ragged lengths take the element-wise kernel.
+    et = torch.from_numpy(e).cuda()
+    st = torch.from_numpy(sm).cuda()
+    for a, b in [(1, 65536), (3, 1000), (16, 65531), (0, 15), (7, 8)]:
+        out = devmod.recombine_bf16(et[a:b], st[a:b])
+        assert np.array_equal(_bits(out).numpy(), want[a:b]), (a, b)
+
+
+@pytest.mark.parametrize("misalign", [1, 3])
+def test_decode_from_store_views_config1(misalign):
+    """Config-1 layer from non-owning unaligned views, as read_many returns
+    them (afterimage/runtime/binstore.py:115-133)."""
+    from tests.store_views import store_views
+
+    W, layer = workloads.small_layer()
+    view_layer, views = store_views(layer, misalign)
+    assert all(not v.flags.owndata for v in views)
+    out = decompress_layer_gpu(view_layer)
+    assert torch.equal(_bits(out), _bits(W))
+    rows = decompress_rows_gpu(view_layer, 100, 357)
+    assert torch.equal(_bits(rows), _bits(W[100:357]))
 
 
 def test_small_layer_1024x3072_chunk4096():
@@ -233,3 +295,14 @@ def test_block_14b_decodes_in_one_launch_with_shared_tables(block14b):
     for (name, w, _), o in zip(block14b, outs):
         assert torch.equal(_bits(o), _bits(w).reshape(-1)), name
 
+
+
+def test_block_14b_decodes_from_store_views(block14b):
+    """Every tensor of the 14B-class block through the reference API from
+    non-owning unaligned views of one buffer per tensor."""
+    from tests.store_views import store_views
+
+    for name, w, layer in block14b:
+        view_layer, _ = store_views(layer, 5)
+        out = decompress_layer_gpu(view_layer, reuse_decode_tables=True)
+        assert torch.equal(_bits(out), _bits(w)), name
