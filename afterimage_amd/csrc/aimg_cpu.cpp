@@ -92,8 +92,8 @@ void decode_chunk(const HostTable& tb, const uint8_t* p, uint32_t nb, uint32_t l
         if (m != 0) {
             const uint32_t s = tb.syms[idx];
             std::memcpy(dst + k, &s, 4);
-            k += (m >> 6) + 1;
-            adv = m & 63u;
+            k += m >> 5;
+            adv = m & 31u;
         } else {
             const uint32_t blk = tb.syms[idx] & 0xFFFFu;
             uint32_t sym = tb.sym0, len = tb.min_len;

@@ -175,6 +175,17 @@ __device__ __forceinline__ const __attribute__((address_space(4))) TableHeader* 
 
 typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
 
+// A generic pointer to LDS holds the LDS offset in its low 32 bits. Reads
+// through the LDS-typed pointer built from that offset let the compiler fold
+// constant offsets into the LDS instructions (it does not for generic
+// pointers whose offset it cannot prove in range).
+using LdsOff = uint32_t;
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(3))) T* lds_ptr(const T* p) {
+    return (const __attribute__((address_space(3))) T*)(uintptr_t)static_cast<LdsOff>(
+        reinterpret_cast<uintptr_t>(p));
+}
+
 // Buffer resource over `nbytes` bytes at `base` (raw, stride 0): loads past
 // the end return zero and stores past it are dropped, instead of touching
 // memory outside the buffer.
@@ -185,7 +196,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, ui
 
 struct Tables {
     const uint32_t* syms;    // LDS window table: symbols / escape block
-    const uint8_t* meta;     // LDS window table: total | (count - 1) << 6
+    const uint8_t* meta;     // LDS window table: total | count << 5
     const uint8_t* len;      // LDS code length of each symbol
     const uint16_t* esc;     // LDS escape blocks (first kLdsEscBlocks)
     const __attribute__((address_space(1))) uint16_t* gesc;  // all escape blocks, global memory
@@ -332,8 +343,8 @@ template <bool kGlobalEsc>
 __device__ __forceinline__ void take(const Tables& tb, const Step& s, uint32_t* syms, uint32_t* adv,
                                      uint32_t* c) {
     *syms = s.syms;
-    *adv = s.meta & 63u;
-    *c = (s.meta >> 6) + 1;
+    *adv = s.meta & 31u;
+    *c = s.meta >> 5;
     if (__builtin_expect(any_lane(*adv == 0), 0)) {
         if (*adv == 0) {
             *syms = escape<kGlobalEsc>(tb, tb.syms[s.idx], s.w, adv);
@@ -1286,8 +1297,13 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             // shift of the last whole word.
             uint32_t rw[kSlotWords + 1];
             const uint32_t* slot_w = reinterpret_cast<const uint32_t*>(slot);
+            {
+                // Read through an LDS-typed pointer: one address register,
+                // the word offsets folded into the reads.
+                const auto* sl = lds_ptr(slot_w);
 #pragma unroll
-            for (uint32_t j = 0; j < kSlotWords + 1; ++j) rw[j] = slot_w[j];
+                for (uint32_t j = 0; j < kSlotWords + 1; ++j) rw[j] = sl[j];
+            }
             const uint32_t tv = __builtin_amdgcn_alignbyte(slot_w[nbody + 1], slot_w[nbody], head);
             __syncthreads();
             uint8_t* dst = stage + dpos;

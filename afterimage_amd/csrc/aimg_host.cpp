@@ -129,7 +129,7 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
         }
         if (k > 0) {
             wsyms[w] = syms;
-            wmeta[w] = static_cast<uint8_t>(pos | ((k - 1) << 6));
+            wmeta[w] = static_cast<uint8_t>(pos | (k << 5));
             continue;
         }
         // Escape window: one entry per value of the next four bits.

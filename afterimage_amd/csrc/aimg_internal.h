@@ -8,16 +8,15 @@
 
 namespace aimg {
 
-constexpr int kAbiVersion = 7;
+constexpr int kAbiVersion = 8;
 constexpr uint32_t kTableMagic = 0x474D4941u;  // "AIMG"
 
 // Window table: for each 12-bit window, the codewords that lie wholly inside
 // it when read one after another from its first bit (at most
 // kMaxSymsPerWindow), in two arrays:
 //   syms (uint32): the symbols, symbol j in bits 8j..8j+7 (unused bytes zero)
-//   meta (uint8):  bits 0..5 total bits those codewords take, bits 6..7 their
-//                  number minus one (a shift by the whole byte reads its
-//                  low 6 bits: the total)
+//   meta (uint8):  bits 0..4 total bits those codewords take (at most 12),
+//                  bits 5..7 their number (1..4)
 // Meta 0 marks an escape window, whose first codeword is longer than 12
 // bits or unused; its syms entry then holds the index of its escape block,
 // or kUnusedBlock when the stored LUT has no codeword there.

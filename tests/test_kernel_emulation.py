@@ -35,10 +35,13 @@ pytestmark = pytest.mark.skipif(not os.path.exists(CXX), reason="needs ROCm's cl
 def emu(tmp_path_factory):
     d = tmp_path_factory.mktemp("kernel_emulation")
     src = open(os.path.join(ROOT, "afterimage_amd", "csrc", "aimg_decode.hip")).read()
-    # Host spelling of two device-only constructs: address-space qualifiers
-    # and VGPR asm operands.
+    # Host spelling of three device-only constructs: address-space qualifiers,
+    # VGPR asm operands, and LDS offsets taken from generic pointers (a host
+    # pointer keeps all its bits).
     src = re.sub(r"__attribute__\(\(address_space\(\d+\)\)\)", "", src)
     src = src.replace('"+v"', '"+r"').replace('::"v"', '::"r"')
+    assert "using LdsOff = uint32_t;" in src
+    src = src.replace("using LdsOff = uint32_t;", "using LdsOff = uintptr_t;")
     (d / "aimg_decode_emu.cpp").write_text(src)
     flags = ["-std=c++20", "-g", "-O1", "-fsanitize=address", "-fno-omit-frame-pointer",
              "-I", os.path.join(HERE, "kernel_emulation"), "-I", os.path.join(ROOT, "include"),

@@ -184,8 +184,8 @@ def test_window_table_matches_canonical_code(name):
     for w in sorted(windows):
         want = _window_expectation(lengths, w)
         ent = int(wsyms[w])
-        total = int(wmeta[w]) & 63
-        count = (int(wmeta[w]) >> 6) + 1 if total else 0
+        total = int(wmeta[w]) & 31
+        count = int(wmeta[w]) >> 5 if total else 0
         if not want:
             # Escape window: its block gives the first codeword for every
             # value of the next four bits.
