@@ -45,38 +45,83 @@ class TensorLayout:
     max_bits: int
 
 
+@dataclasses.dataclass(frozen=True)
+class BlockPlan:
+    """Byte positions of a block's arrays in its buffer: per tensor
+    (sign_mantissa, packed, chunk_offsets, chunk_nbytes). Each tensor's
+    sign/mantissa bytes start ALIGN-aligned with its bitstream right after
+    them, and its chunk offsets start ALIGN-aligned with the lengths right
+    after them, so that a store reader fills each pair with one read."""
+
+    spans: tuple
+    sizes: tuple  # (sign_mantissa bytes, packed bytes, chunks) per tensor
+    nbytes: int
+
+
 class HostBlock:
     """One decoder block's compressed tensors packed into one pinned host
     buffer (a single H2D copy per block)."""
 
     def __init__(self, layers: list[CompressedLayer], pin: bool = True):
-        layout = []
-        pos = 0
-        pieces = []
+        arrays = []
         for layer in layers:
             enc = layer.encoded
-            arrays = (np.ascontiguousarray(enc.packed, dtype=np.uint8),
-                      np.ascontiguousarray(enc.chunk_offsets, dtype=np.int32),
-                      np.ascontiguousarray(enc.chunk_nbytes, dtype=np.int32),
-                      np.ascontiguousarray(layer.sign_mantissa.numpy(), dtype=np.uint8))
-            spans = []
-            for a in arrays:
-                spans.append(pos)
-                pieces.append((pos, a))
-                pos = _aligned(pos + a.nbytes)
-            layout.append(TensorLayout(
-                packed=(spans[0], arrays[0].nbytes),
-                chunk_offsets=(spans[1], arrays[1].shape[0]),
-                chunk_nbytes=(spans[2], arrays[2].shape[0]),
-                sign_mantissa=(spans[3], arrays[3].nbytes),
-                chunk_size=int(enc.chunk_size), n_symbols=int(enc.n_symbols),
-                shape=tuple(layer.shape), sym_lut=enc.sym_lut, len_lut=enc.len_lut,
-                max_bits=int(enc.max_bits)))
-        self.nbytes = max(pos, ALIGN)
-        self.buf = torch.empty(self.nbytes, dtype=torch.uint8, pin_memory=pin)
+            arrays.append((np.ascontiguousarray(layer.sign_mantissa.numpy(), dtype=np.uint8),
+                           np.ascontiguousarray(enc.packed, dtype=np.uint8),
+                           np.ascontiguousarray(enc.chunk_offsets, dtype=np.int32),
+                           np.ascontiguousarray(enc.chunk_nbytes, dtype=np.int32)))
+        plan = self.plan([(a[0].nbytes, a[1].nbytes, a[2].shape[0]) for a in arrays])
+        self._init_buffer(plan, pin)
         host = self.buf.numpy()
-        for start, a in pieces:
-            host[start:start + a.nbytes] = a.reshape(-1).view(np.uint8)
+        for span, group in zip(plan.spans, arrays):
+            for at, a in zip(span, group):
+                host[at: at + a.nbytes] = a.reshape(-1).view(np.uint8)
+        self.describe([(int(l.encoded.chunk_size), int(l.encoded.n_symbols), tuple(l.shape))
+                       for l in layers],
+                      [(l.encoded.sym_lut, l.encoded.len_lut, int(l.encoded.max_bits))
+                       for l in layers])
+
+    @staticmethod
+    def plan(sizes: list[tuple[int, int, int]]) -> BlockPlan:
+        """Layout for tensors of (sign/mantissa bytes, packed bytes, chunks)."""
+        spans = []
+        pos = 0
+        for n_sm, n_packed, n_chunks in sizes:
+            sm_at = pos
+            packed_at = sm_at + n_sm
+            offs_at = _aligned(packed_at + n_packed)
+            nbytes_at = offs_at + 4 * n_chunks
+            pos = _aligned(nbytes_at + 4 * n_chunks)
+            spans.append((sm_at, packed_at, offs_at, nbytes_at))
+        return BlockPlan(spans=tuple(spans), sizes=tuple(tuple(x) for x in sizes),
+                         nbytes=max(pos, ALIGN))
+
+    @classmethod
+    def allocate(cls, plan: BlockPlan, pin: bool = True) -> "HostBlock":
+        """An empty block with ``plan``'s buffer, to be filled (for example by
+        a store reader) and then described."""
+        self = cls.__new__(cls)
+        self._init_buffer(plan, pin)
+        return self
+
+    def _init_buffer(self, plan: BlockPlan, pin: bool) -> None:
+        self.plan_ = plan
+        self.nbytes = plan.nbytes
+        self.buf = torch.empty(self.nbytes, dtype=torch.uint8, pin_memory=pin)
+
+    def describe(self, metas: list[tuple[int, int, tuple]], luts: list) -> None:
+        """Record each tensor's (chunk_size, n_symbols, shape) and LUTs
+        (sym_lut, len_lut, max_bits) against the buffer layout."""
+        layout = []
+        for span, size, (chunk_size, n_symbols, shape), (sym, ln, mb) in zip(
+                self.plan_.spans, self.plan_.sizes, metas, luts):
+            sm_at, packed_at, offs_at, nbytes_at = span
+            n_sm, n_packed, n_chunks = size
+            layout.append(TensorLayout(
+                packed=(packed_at, n_packed), chunk_offsets=(offs_at, n_chunks),
+                chunk_nbytes=(nbytes_at, n_chunks), sign_mantissa=(sm_at, n_sm),
+                chunk_size=int(chunk_size), n_symbols=int(n_symbols), shape=tuple(shape),
+                sym_lut=sym, len_lut=ln, max_bits=int(mb)))
         self.layout = layout
 
     @property

@@ -37,3 +37,45 @@ def test_ring_respects_the_vram_budget(two_blocks):
     hbs = [HostBlock([l for _, _, l in blk]) for blk in two_blocks]
     with pytest.raises(ValueError, match="budget"):
         LayerRing(hbs, device="cuda", vram_budget=1 << 20)
+
+
+@pytest.fixture(scope="module")
+def store_two_full_blocks(tmp_path_factory):
+    """Two full 14B-class blocks (config-3 shapes, 65536-symbol chunks, seeds
+    3 and 4) written to a store on disk."""
+    from afterimage_amd.runtime.store import StoreWriter
+
+    d = tmp_path_factory.mktemp("store_14b")
+    keys, refs = [], []
+    with StoreWriter(d, model_id="block14b-x2", chunk_size=65536) as sw:
+        for b, seed in enumerate((3, 4)):
+            blk = workloads.block_14b(seed=seed)
+            names = []
+            for name, _, layer in blk:
+                sw.add_compressed("layers.%d.%s" % (b, name), layer)
+                names.append("layers.%d.%s" % (b, name))
+            keys.append(names)
+            refs.append([w.reshape(-1).view(torch.int16) for _, w, _ in blk])
+            del blk
+    return d, keys, refs
+
+
+def test_streamed_full_blocks_from_the_store_under_4gb(store_two_full_blocks):
+    """Config 4 at its real shapes: full 14B-class blocks read from the store
+    straight into pinned buffers (CRC-32 checked), then streamed through a
+    2-slot ring under a 4 GiB device budget for 6 layers; every tensor of
+    every layer bit-exact against the seeded originals."""
+    from afterimage_amd.runtime.store import StoreReader
+
+    d, keys, refs = store_two_full_blocks
+    with StoreReader(d) as rd:
+        hbs = [rd.host_block(k, pin=True, verify=True) for k in keys]
+    ring = LayerRing(hbs, device="cuda", slots=2, vram_budget=4 << 30)
+    assert ring.ring_bytes <= 4 << 30
+    want = [[r.cuda() for r in blk] for blk in refs]
+    seen = 0
+    for k, tensors in ring.stream(6):
+        for t, (got, w) in enumerate(zip(tensors, want[k % 2])):
+            assert torch.equal(_bits(got).reshape(-1), w), "layer %d tensor %d" % (k, t)
+        seen += 1
+    assert seen == 6

@@ -1,5 +1,5 @@
 """The streamed-block ring's host side: one pinned buffer per block holding
-every tensor's compressed arrays at aligned offsets."""
+every tensor's compressed arrays."""
 import numpy as np
 import pytest
 
@@ -13,8 +13,12 @@ def test_host_block_holds_every_array_at_aligned_offsets():
     buf = hb.buf.numpy()
     for (_, _, layer), t in zip(blk, hb.layout):
         enc = layer.encoded
-        for off, _ in (t.packed, t.chunk_offsets, t.chunk_nbytes, t.sign_mantissa):
-            assert off % ALIGN == 0
+        # Sign/mantissa bytes and chunk offsets start aligned; the bitstream
+        # and the chunk lengths follow them directly (one store read each).
+        s0, sn = t.sign_mantissa
+        o0, on = t.chunk_offsets
+        assert s0 % ALIGN == 0 and o0 % ALIGN == 0
+        assert t.packed[0] == s0 + sn and t.chunk_nbytes[0] == o0 + 4 * on
         p0, pn = t.packed
         assert np.array_equal(buf[p0:p0 + pn], enc.packed)
         o0, on = t.chunk_offsets
