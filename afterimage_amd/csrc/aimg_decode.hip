@@ -759,6 +759,27 @@ __device__ __forceinline__ float dot8_bf16(const uint4& w, const uint4& x) {
     return s;
 }
 
+// Adds each live lane's products p[b] (b < nb) to y[b][row of the lane] with
+// one wave sum and one atomic per distinct row, instead of one atomic per
+// lane. Called with every lane of the wave; dead lanes pass live = false.
+template <int kB>
+__device__ __forceinline__ void gemv_rows_add(const GemvArgs& G, int nb, const float (&p)[kB],
+                                              bool live, uint32_t row) {
+    uint64_t left = __ballot(live);  // live lanes whose products are not yet added
+    while (left != 0) {
+        const uint32_t rr = __builtin_amdgcn_readlane(row, __builtin_ctzll(left));
+        const bool mine = live && row == rr;
+        left &= ~__ballot(mine);
+#pragma unroll
+        for (int b = 0; b < kB; ++b) {
+            if (b >= nb) break;
+            const float sum = __uint_as_float(wave_scan_incl_f32(__float_as_uint(mine ? p[b] : 0.0f)));
+            if ((threadIdx.x & 63) == 63 && sum != 0.0f)
+                atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + rr, sum);
+        }
+    }
+}
+
 // Column col moved on by step elements of a row of cols.
 __device__ __forceinline__ void advance_col(uint32_t& col, uint32_t step, uint32_t cols) {
     col += step;
@@ -807,16 +828,15 @@ __device__ __forceinline__ void step_rc(uint32_t& row, uint32_t& col, const Gemv
 // most of the fused GEMV's time). Only rows shorter than 512 elements take
 // per-lane atomics. Liveness is applied as masks, so the step is straight
 // code. With one x vector its words are requested kXAhead steps ahead of
-// use; every x read is in bounds, since a column is always below cols.
-template <int kMode, int kGroup>
+// use; every x read is in bounds, since a column is always below cols. G's x
+// and y are those of the nb <= kB x vectors of this pass.
+template <int kMode, int kGroup, int kB>
 __device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch], const GemvArgs& G,
-                                                 const uint8_t* stage, uint32_t a0, uint32_t nfull,
-                                                 uint32_t i) {
+                                                 int nb, const uint8_t* stage, uint32_t a0,
+                                                 uint32_t nfull, uint32_t i) {
     static_assert(kThreads * kGroup == 4096, "step_rows / step_cols are for 4096 elements");
-    constexpr int kB = kMode == kModeGemv1 ? 1 : kGemvMaxBatch;
-    constexpr uint32_t kXAhead = kMode == kModeGemv1 ? 3 : 0;
+    constexpr uint32_t kXAhead = kB == 1 ? 3 : 0;
     constexpr uint32_t kSpan = 64 * kGroup;  // elements a wave holds at one step
-    const int nb = kMode == kModeGemv1 ? 1 : G.batch;
     const uint32_t cols = G.cols;
     const uint32_t lane = i & 63;
     const uint32_t wave_first = uniform(i - lane);  // first thread of this wave
@@ -898,7 +918,9 @@ __device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch],
                     __builtin_bit_cast(bf16x8, w_hi), __builtin_bit_cast(bf16x8, xz), acc[b], 0, 0, 0);
             }
         } else if (m != 0u) {
-            // Rows shorter than a wave's 512 elements: per-lane atomics.
+            // Rows shorter than a wave's 512 elements: per-lane atomics (a
+            // wave sum per row here, as in the small-chunk path, costs this
+            // kernel's other steps registers it does not have).
 #pragma unroll
             for (int b = 0; b < kB; ++b) {
                 if (b >= nb) break;
@@ -985,7 +1007,9 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
         return;
     }
     if constexpr (kWhole && (kMode == kModeGemv || kMode == kModeGemv1)) {
-        gemv_round_whole<kMode, kGroup>(sm, G, stage, static_cast<uint32_t>(a0), nfull, i);
+        constexpr int kB = kMode == kModeGemv1 ? 1 : kGemvMaxBatch;
+        gemv_round_whole<kMode, kGroup, kB>(sm, G, kMode == kModeGemv1 ? 1 : G.batch, stage,
+                                            static_cast<uint32_t>(a0), nfull, i);
         return;
     }
     // Fused GEMV: each group's 8 weights (one matrix row, as cols % 8 == 0)
@@ -995,8 +1019,8 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
     // as B column l % 16 over the same 8 k, so the diagonal of the 16x16
     // result holds the sums of each lane's own products (dead lanes supply
     // zeros). The accumulator is reduced over the wave and added to y when
-    // the row changes. A wave that straddles a row boundary takes that
-    // group's products on the VALU and adds them with per-lane atomics.
+    // the row changes. A step whose live groups span several rows takes the
+    // products on the VALU and adds one wave sum per distinct row.
     // With one x vector its words are requested kXAhead groups ahead of use
     // (a group's column is always below cols, so every read is in bounds,
     // live group or not); with up to four there are no registers for that.
@@ -1035,7 +1059,7 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
         const uint4(&xc)[kB] = xq[k % (kXAhead + 1)];
         const uint32_t v = k * tpc + i;
         const bool live = v < nfull;
-        const uint64_t lm = __builtin_amdgcn_ballot_w64(live);
+        const uint64_t lm = __ballot(live);
         if (lm == 0) continue;
         // Staged exponents read here rather than all at once: registers.
         const uint2 e = *reinterpret_cast<const uint2*>(stage + (kWhole || live ? v : 0u) * kGroup);
@@ -1045,7 +1069,7 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
         w.z = live ? bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, e.y) : 0u;
         w.w = live ? bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, e.y) : 0u;
         const uint32_t r0 = __builtin_amdgcn_readlane(row, __builtin_ctzll(lm));
-        if (__builtin_amdgcn_ballot_w64(live && row != r0) == 0) {
+        if (__ballot(live && row != r0) == 0) {
             if (r0 != acc_row) {
                 if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);
                 acc_row = r0;
@@ -1064,20 +1088,7 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
             float p[kB];
 #pragma unroll
             for (int b = 0; b < kB; ++b) p[b] = live ? dot8_bf16(w, xc[b]) : 0.0f;
-            uint64_t left = lm;  // live lanes whose products are not yet added
-            while (left != 0) {
-                const uint32_t rr = __builtin_amdgcn_readlane(row, __builtin_ctzll(left));
-                const bool mine = live && row == rr;
-                left &= ~__builtin_amdgcn_ballot_w64(mine);
-#pragma unroll
-                for (int b = 0; b < kB; ++b) {
-                    if (b >= nb) break;
-                    const float sum =
-                        __uint_as_float(wave_scan_incl_f32(__float_as_uint(mine ? p[b] : 0.0f)));
-                    if ((threadIdx.x & 63) == 63 && sum != 0.0f)
-                        atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + rr, sum);
-                }
-            }
+            gemv_rows_add<kB>(G, nb, p, live, row);
         }
     }
     if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);

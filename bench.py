@@ -9,8 +9,9 @@ launch that rebuilds the whole bf16 tensor in HBM. --workload block does the
 same for a whole 14B-class decoder block (9 tensors, one codebook per role)
 in one launch. Prints one JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload layer|block]
-                    [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+                    [--workload layer|block|gemv|ring|api] [--chunk-size N]
+                    [--batch B] [--no-cpu-baseline] [--cpu-threads T]
 """
 from __future__ import annotations
 
@@ -35,13 +36,36 @@ def _log(msg: str) -> None:
     print("[bench] " + msg, file=sys.stderr, flush=True)
 
 
+def _host_cpu() -> dict:
+    """This host's CPU as the baseline ran on it: model name, online CPUs,
+    the CPUs this process may use, and OpenMP's thread count (which
+    follows OMP_NUM_THREADS, the host's CPU share for one GPU)."""
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"model": model, "nproc": os.cpu_count(), "usable_cpus": usable,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
 def _cpu_baseline(layers, max_threads: int, what: str) -> dict:
     """The reference's CPU decode path (chunk decode + recombine), restated in
-    C/OpenMP in oracle/, timed on this host's cores on a bounded sample."""
+    C/OpenMP in oracle/, timed on this host's cores on a bounded sample: at
+    OpenMP's thread count (every CPU this process is given) unless
+    --cpu-threads asks for fewer, and on one thread."""
     import oracle
 
     oracle.build()
-    threads = max(1, min(max_threads, oracle.max_threads()))
+    threads = oracle.max_threads() if max_threads <= 0 else max(1, min(max_threads,
+                                                                    oracle.max_threads()))
     total_s = 0.0
     reps = []
     n = 0
@@ -72,6 +96,7 @@ def _cpu_baseline(layers, max_threads: int, what: str) -> dict:
         "one_thread_gbs": round(2 * sub.n_symbols / one["median_s"] / 1e9, 3),
         "one_thread_sample": "first %d chunks of the largest tensor (%d symbols)"
                              % (sub.n_chunks, sub.n_symbols),
+        "host": _host_cpu(),
     }
 
 
@@ -171,7 +196,7 @@ def _bench_ring(args) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8",
+        "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "%d layers of the 14B-class block (2 distinct blocks, seeds 3/4, "
                                "cycled), compressed in pinned host memory, H2D on a side stream, "
@@ -198,7 +223,7 @@ def _bench_gemv(args) -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    W, layer = workloads.single_layer(seed=2)
+    W, layer = workloads.single_layer(seed=2, chunk_size=args.chunk_size)
     rows, cols = W.shape
     b = args.batch
     g = np.random.default_rng(23)
@@ -241,6 +266,21 @@ def _bench_gemv(args) -> int:
     ev3.record(stream)
     torch.cuda.synchronize(dev)
     step_s = ev2.elapsed_time(ev3) / 1e3 / args.steps
+    # The decode kernel's own symbol rate on the same tensor (exponent bytes
+    # out, its smallest output): what the fused GEMV's decode loop is bound by.
+    from afterimage_amd.runtime.device import decode_u8
+
+    ex = torch.empty(layer.encoded.n_symbols, dtype=torch.uint8, device=dev)
+    for _ in range(args.warmup):
+        decode_u8([t], outs=[ex])
+    ev4 = torch.cuda.Event(enable_timing=True)
+    ev5 = torch.cuda.Event(enable_timing=True)
+    ev4.record(stream)
+    for _ in range(args.steps):
+        decode_u8([t], outs=[ex])
+    ev5.record(stream)
+    torch.cuda.synchronize(dev)
+    u8_s = ev4.elapsed_time(ev5) / 1e3 / args.steps
     enc = layer.encoded
     n = enc.n_symbols
     chunk_bytes = int(enc.chunk_nbytes.astype(np.int64).sum())
@@ -257,18 +297,82 @@ def _bench_gemv(args) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8",
+        "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "fused decode->GEMV, 5120x17408 bf16 weight (seed 2, 0.1%% "
-                               "outliers) x bf16 activation [%d, 17408] N(0,1) (seed 23), fp32 "
-                               "accumulate -> bf16" % b,
+                               "outliers, %d-symbol chunks) x bf16 activation [%d, 17408] N(0,1) "
+                               "(seed 23), fp32 accumulate -> bf16" % (enc.chunk_size, b),
                    "batch": b, "within_tolerance": ok, "tolerance": "rel 1e-2, abs 1e-3",
-                   "flops_per_step": 2 * n * b},
-        "roofline": {"bound": "hbm", "achieved": round(algo_bytes / step_s / 1e9, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(algo_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": algo_bytes,
-                     "kernel_us": round(step_s * 1e6, 2)},
+                   "flops_per_step": 2 * n * b, "chunk_size": enc.chunk_size},
+        # The GEMV moves 2.5x fewer bytes than the decode but runs its decode
+        # loop: its bound is the decode's symbol rate, measured here on the
+        # same tensor with exponent-byte output (the decode's smallest output).
+        "roofline": {"bound": "decode", "achieved": round(n / step_s / 1e9, 2),
+                     "peak": round(n / u8_s / 1e9, 2), "unit": "Gsymbols/s",
+                     "frac": round(u8_s / step_s, 4), "traffic": None,
+                     "kernel_us": round(step_s * 1e6, 2),
+                     "decode_u8_us": round(u8_s * 1e6, 2),
+                     "hbm_gbs": round(algo_bytes / step_s / 1e9, 1),
+                     "hbm_frac": round(algo_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "algorithmic_bytes_per_launch": algo_bytes},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+def _bench_api(args) -> int:
+    """The reference API path: decompress_layer_gpu on the 5120x17408 layer
+    from host arrays, as the reference engine calls it (pageable H2D of the
+    compressed arrays, decode table from the content-keyed cache, decode).
+    One step = one call; the value includes the PCIe copies."""
+    from afterimage_amd import workloads
+    from afterimage_amd.runtime.compressed_store import decompress_layer_gpu
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    W, layer = workloads.single_layer(seed=2, chunk_size=args.chunk_size)
+    enc = layer.encoded
+
+    def step():
+        return decompress_layer_gpu(layer, device="cuda:0", reuse_decode_tables=True)
+
+    for _ in range(args.warmup):
+        out = step()
+    torch.cuda.synchronize(dev)
+    ok = torch.equal(out.view(torch.int16).cpu(), W.view(torch.int16))
+    if not ok:
+        print("API decode differs from the original weights", file=sys.stderr)
+        return 1
+    del out
+    torch.cuda.synchronize(dev)
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize(dev)
+    wall = (time.perf_counter() - t_start) / args.steps
+    h2d = int(enc.packed.nbytes + layer.sign_mantissa.numel() + 8 * enc.n_chunks)
+    n = enc.n_symbols
+    rec = {
+        "metric": "decompress_layer_gpu from host arrays: decompressed BF16 GB/s (H2D included)",
+        "value": round(2 * n / wall / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "decompress_layer_gpu(layer, 'cuda:0', reuse_decode_tables=True) "
+                               "on the 5120x17408 weight (seed 2, 0.1%% outliers, %d-symbol "
+                               "chunks) held in host numpy arrays; default 2^25-element slices"
+                               % enc.chunk_size,
+                   "h2d_bytes_per_call": h2d, "bit_exact": ok, "chunk_size": enc.chunk_size},
+        "h2d_inclusive_gbs_compressed": round(h2d / wall / 1e9, 2),
+        "roofline": None,
         "cpu_baseline": None,
     }
     print(json.dumps(rec), flush=True)
@@ -280,15 +384,20 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=["layer", "block", "gemv", "ring"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "block", "gemv", "ring", "api"],
+                    default="layer",
                     help="layer: one 5120x17408 weight (the headline); block: a whole "
                          "14B-class decoder block in one launch; gemv: fused decode->GEMV "
                          "of the 5120x17408 weight with a [batch, 17408] activation; ring: 40 "
-                         "streamed blocks from pinned host memory through a 2-slot ring")
+                         "streamed blocks from pinned host memory through a 2-slot ring; api: "
+                         "decompress_layer_gpu from host arrays, H2D included")
     ap.add_argument("--layers", type=int, default=40, help="ring: layers streamed per step")
     ap.add_argument("--batch", type=int, default=1, help="gemv batch (1..4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="CPU-baseline threads (0: OpenMP's count, i.e. every CPU given)")
+    ap.add_argument("--chunk-size", type=int, default=65536,
+                    help="layer / gemv / api: symbols per chunk of the 5120x17408 weight")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of decoding, time a plain device copy of this many MiB "
                          "(the reference kernel for scaling HBM byte counters)")
@@ -309,6 +418,8 @@ def main() -> int:
         return _bench_gemv(args)
     if args.workload == "ring":
         return _bench_ring(args)
+    if args.workload == "api":
+        return _bench_api(args)
 
     from afterimage_amd import _native, workloads
     from afterimage_amd.runtime.device import DeviceTensor, _descriptor
@@ -318,12 +429,13 @@ def main() -> int:
     t0 = time.perf_counter()
     if args.workload == "layer":
         seed = 2
-        W, layer = workloads.single_layer(seed=seed)
+        W, layer = workloads.single_layer(seed=seed, chunk_size=args.chunk_size)
         items = [("layer", W, layer)]
-        config_key = "5120x17408/seed%d/chunk65536/outliers1e-3" % seed
-        description = ("bf16 5120x17408 weight decode, N(0,0.02) + 0.1% N(0,0.5) outliers "
-                       "(seed 2), per-tensor Huffman exponent codebook, 65536-symbol chunks "
-                       "(1360), inputs resident in HBM, one launch per step")
+        config_key = "5120x17408/seed%d/chunk%d/outliers1e-3" % (seed, args.chunk_size)
+        description = ("bf16 5120x17408 weight decode, N(0,0.02) + 0.1%% N(0,0.5) outliers "
+                       "(seed 2), per-tensor Huffman exponent codebook, %d-symbol chunks "
+                       "(%d), inputs resident in HBM, one launch per step"
+                       % (args.chunk_size, layer.encoded.n_chunks))
     else:
         seed = 3
         items = workloads.block_14b(seed=seed)
@@ -398,7 +510,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8",
+        "dtype": "bf16",
         "data": "synthetic",
         "config": {
             "workload": description,

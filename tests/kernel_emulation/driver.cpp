@@ -53,6 +53,31 @@ int main(int argc, char** argv) {
     t.n_symbols = n_symbols;
     t.chunk_size = chunk_size;
     t.n_chunks = (int32_t)n_chunks;
+    if (std::string(argv[2]) == "gemv") {
+        // y += W x for the rows x cols bf16 weight W, checked against
+        // expect_y.bin within rel 1e-2 / abs 1e-3 (the GPU tests' bar).
+        long long rows = 0, cols = 0, batch = 0;
+        FILE* g = fopen((d + "/gemv.txt").c_str(), "r");
+        if (!g || fscanf(g, "%lld %lld %lld", &rows, &cols, &batch) != 3) return 2;
+        fclose(g);
+        auto sm = readf(d + "/sm.bin"), xv = readf(d + "/x.bin"), ey = readf(d + "/expect_y.bin");
+        t.sign_mantissa = exact<uint8_t>(sm);
+        std::vector<uint8_t> yv(4 * batch * rows);
+        float* y = exact<float>(yv);
+        const void* x = exact<uint8_t>(xv);
+        const int rc = aimg_decode_gemv_bf16(&t, rows, cols, x, (int)batch, y, nullptr);
+        if (rc) { fprintf(stderr, "gemv rc=%d: %s\n", rc, aimg_last_error()); return 6; }
+        const float* want = reinterpret_cast<const float*>(ey.data());
+        size_t bad = 0;
+        for (long long k = 0; k < batch * rows; ++k) {
+            const double diff = y[k] > want[k] ? y[k] - want[k] : want[k] - y[k];
+            const double aw = want[k] < 0 ? -want[k] : want[k];
+            bad += diff > 1e-3 + 1e-2 * aw;
+        }
+        printf("%s gemv: %s (%zu of %lld outside tolerance)\n", d.c_str(), bad ? "MISMATCH" : "ok", bad,
+               batch * rows);
+        return bad ? 1 : 0;
+    }
     std::vector<uint8_t> outv(n_symbols * (bf16 ? 2 : 1));
     void* out = exact<uint8_t>(outv);
     memset(out, 0xAB, outv.size());

@@ -5,12 +5,12 @@
 //
 // Model: a block runs as one std::thread per work-item; blocks run one after
 // another; __shared__ data are function statics (one block at a time).
-// __syncthreads is a block barrier. Wave shuffles exchange values through a
-// per-wave buffer between per-wave barriers, so they must be reached by all
-// 64 lanes (the kernel calls them in uniform control flow only). Ballot
-// returns the calling lane's own bit: the kernel uses it as "does any lane
-// need this?", for which the per-lane answer gives the same results
-// (the fused GEMV path relies on true wave ballots and is not modelled).
+// __syncthreads is a block barrier. Wave shuffles, readlane, HIP's __ballot
+// and the MFMA exchange values through a per-wave buffer between per-wave
+// barriers, so they must be reached by all 64 lanes (the kernel calls them in
+// uniform control flow only). The compiler builtin ballot returns the calling
+// lane's own bit: the kernel uses it, inside divergent loops too, as "does any
+// lane need this?", for which the per-lane answer gives the same results.
 #pragma once
 #include <barrier>
 #include <cstdint>
@@ -79,6 +79,16 @@ inline T wave_xchg(T v, unsigned src) {
     std::memcpy(&out, &r, sizeof(T));
     return out;
 }
+// Every lane's v, gathered by every lane of the wave (out[k] from lane k).
+inline void wave_all(uint64_t v, uint64_t* out) {
+    Block& B = *g_block;
+    const unsigned w = threadIdx.x >> 6;
+    B.wave[w]->arrive_and_wait();
+    B.xbuf[threadIdx.x] = v;
+    B.wave[w]->arrive_and_wait();
+    for (unsigned k = 0; k < 64; ++k) out[k] = B.xbuf[w * 64 + k];
+    B.wave[w]->arrive_and_wait();
+}
 }  // namespace emu
 
 inline void __syncthreads() { emu::g_block->bar.arrive_and_wait(); }
@@ -128,9 +138,10 @@ inline unsigned long long __ballot(int p) {
 }
 
 inline uint64_t __builtin_amdgcn_ballot_w64(bool p) { return p ? (1ull << emu::lane()) : 0ull; }
-// Same signatures as the compiler builtins (int in, int out).
+// Same signatures as the compiler builtins (int in, int out). readfirstlane
+// is applied to wave-uniform values only, so the lane's own value is it.
 inline int __builtin_amdgcn_readfirstlane(int v) { return v; }
-inline int __builtin_amdgcn_readlane(int v, int) { return v; }
+inline int __builtin_amdgcn_readlane(int v, int l) { return emu::wave_xchg(v, (unsigned)l & 63u); }
 inline uint32_t __builtin_amdgcn_alignbyte(uint32_t a, uint32_t b, uint32_t s) {
     return (uint32_t)((((uint64_t)a << 32) | b) >> (8 * (s & 3)));
 }
@@ -221,12 +232,36 @@ inline float atomicAdd(float* p, float v) {
 }
 inline int __ffs(int x) { return __builtin_ffs(x); }
 inline void __builtin_amdgcn_s_setprio(int) {}  // wave issue priority: no effect here
-// Matrix-core product: used by the fused GEMV only, which is not modelled.
+// v_mfma_f32_16x16x32_bf16, D = A B + C with A 16x32, B 32x16, fp32 sums.
+// Lane l supplies A[l % 16][8 (l / 16) + j] and B[8 (l / 16) + j][l % 16]
+// (j < 8, its 8 bf16 operands) and receives D[4 (l / 16) + r][l % 16], r < 4.
 typedef __bf16 emu_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float emu_f32x4 __attribute__((ext_vector_type(4)));
-inline emu_f32x4 __builtin_amdgcn_mfma_f32_16x16x32_bf16(emu_bf16x8, emu_bf16x8, emu_f32x4 c, int, int, int) {
-    __builtin_trap();
-    return c;
+inline float emu_bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+inline emu_f32x4 __builtin_amdgcn_mfma_f32_16x16x32_bf16(emu_bf16x8 a, emu_bf16x8 b, emu_f32x4 c, int, int,
+                                                         int) {
+    uint16_t ab[16];
+    std::memcpy(ab, &a, 16);
+    std::memcpy(ab + 8, &b, 16);
+    uint64_t mine[4];
+    std::memcpy(mine, ab, 32);
+    uint16_t all[64][16];
+    for (int q = 0; q < 4; ++q) {
+        uint64_t got[64];
+        emu::wave_all(mine[q], got);
+        for (unsigned src = 0; src < 64; ++src) std::memcpy(&all[src][4 * q], &got[src], 8);
+    }
+    const unsigned l = emu::lane(), col = l & 15u;
+    emu_f32x4 d;
+    for (int r = 0; r < 4; ++r) {
+        const unsigned row = 4 * (l >> 4) + r;
+        float sum = c[r];
+        for (unsigned k = 0; k < 32; ++k)
+            sum += emu_bf16_to_f32(all[row + 16 * (k >> 3)][k & 7]) *
+                   emu_bf16_to_f32(all[col + 16 * (k >> 3)][8 + (k & 7)]);
+        d[r] = sum;
+    }
+    return d;
 }
 
 template <typename K, typename... A>

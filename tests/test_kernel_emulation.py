@@ -7,8 +7,9 @@ escape blocks beyond the LDS share, and the tiny-buffer kernel.
 This checks memory safety on the CPU before any GPU run: each device buffer
 is a heap block of exactly its size, so an access past any of them, or past
 the kernel's LDS block, fails the run with the offending source line. The
-outputs are compared with the known weights / exponents as well. The fused
-GEMV mode depends on true wave ballots and is covered by the GPU tests.
+outputs are compared with the known weights / exponents as well; the fused
+GEMV's y within the GPU tests' tolerance of a float64 product (the stand-in
+models the MFMA from its lane layout, and true wave ballots).
 """
 import os
 import re
@@ -91,6 +92,38 @@ def _bf16(emu, name, W, chunk_size):
     _write(emu[1] / name, layer.encoded, W.reshape(-1).view(torch.int16).numpy(),
            layer.sign_mantissa.numpy())
     _run(emu, name, "bf16")
+
+
+def _gemv(emu, name, rows, cols, chunk_size, batch, seed):
+    W = workloads.bf16_normal((rows, cols), seed, 0.02, outlier_frac=1e-3)
+    layer = compress_layer(W, chunk_size=chunk_size)
+    g = np.random.default_rng(seed + 1)
+    x = torch.from_numpy(g.standard_normal((batch, cols), dtype=np.float32)).to(torch.bfloat16)
+    want = (x.double() @ W.double().t()).float()
+    d = emu[1] / name
+    _write(d, layer.encoded, np.zeros(1, np.uint8), layer.sign_mantissa.numpy())
+    x.view(torch.int16).numpy().tofile(os.path.join(d, "x.bin"))
+    want.numpy().tofile(os.path.join(d, "expect_y.bin"))
+    with open(os.path.join(d, "gemv.txt"), "w") as f:
+        f.write("%d %d %d\n" % (rows, cols, batch))
+    _run(emu, name, "gemv")
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_gemv_16_thread_chunks_spanning_rows(emu, batch):
+    # 64-symbol chunks of 40-column rows: several chunks, and rows, per wave step.
+    _gemv(emu, "gemv16_b%d" % batch, 96, 40, 64, batch, 3)
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_gemv_512_thread_chunks_with_row_crossings(emu, batch):
+    # 32768-symbol chunks (512 threads) over 1000-column rows: wave steps of
+    # 512 elements cross a row boundary about every other step.
+    _gemv(emu, "gemv512_b%d" % batch, 70, 1000, 32768, batch, 5)
+
+
+def test_gemv_512_thread_chunks_rows_shorter_than_a_wave_step(emu):
+    _gemv(emu, "gemv512_short", 300, 200, 32768, 2, 7)
 
 
 def test_u8_small_chunks_16_threads_per_chunk(emu):
