@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before the library; see module doc)
 
 LIB_PATH = Path(__file__).resolve().parent / "libafterimage_decode.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 MAX_TENSORS = 32
 
 AIMG_OK = 0
@@ -43,6 +43,8 @@ class AimgTensor(ctypes.Structure):
         ("sign_mantissa", ctypes.c_void_p),
         ("out", ctypes.c_void_p),
         ("table", ctypes.c_void_p),
+        ("index", ctypes.c_void_p),
+        ("index_nbytes", ctypes.c_int64),
         ("packed_nbytes", ctypes.c_int64),
         ("n_symbols", ctypes.c_int64),
         ("chunk_size", ctypes.c_int32),
@@ -60,6 +62,10 @@ _SIGNATURES = [
     ("aimg_table_nbytes", ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)]),
     ("aimg_build_table", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]),
+    ("aimg_index_nbytes", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),
+    ("aimg_build_index", ctypes.c_int,
+     [ctypes.POINTER(AimgTensor), ctypes.c_int, ctypes.c_void_p]),
     ("aimg_decode_bf16", ctypes.c_int,
      [ctypes.POINTER(AimgTensor), ctypes.c_int, ctypes.c_void_p]),
     ("aimg_decode_u8", ctypes.c_int,

@@ -64,12 +64,11 @@ constexpr uint32_t kOverlapBits = 32;
 // different LDS banks. 168-bit segments at the 2-bit shortest code of bf16
 // weights make a 64Ki-symbol chunk (about 171K bits) two rounds of 512
 // segments.
-constexpr uint32_t kSlotCap = 84;
+constexpr uint32_t kSlotCap = kSegCodewords;
 constexpr uint32_t kSlotWords = kSlotCap / 4;  // compaction reads these and one more
 constexpr uint32_t kSlotBytes = 92;
 static_assert(kSlotCap % 4 == 0 && kSlotBytes >= kSlotCap + 4, "slot room for the word after the cap");
 static_assert(kSlotBytes % 4 == 0 && (kSlotBytes / 4) % 2 == 1, "slot stride: an odd number of words");
-constexpr uint32_t kMaxSegBits = 168;
 constexpr uint32_t kLeadBytes = 16;  // room for a carried partial vector group
 constexpr uint32_t kTileSlackWords = 4;
 constexpr uint32_t kTileWords = kThreads * kMaxSegBits / 32 + kTileSlackWords * kMaxGroups;
@@ -111,6 +110,10 @@ struct DevTensor {
     int32_t chunk_size;
     int32_t tpc;         // threads per chunk (power of two, 16..512)
     uint32_t packed_n32;  // packed_nbytes, capped at 2^32 - 1 (buffer loads)
+    uint8_t* index;       // segment index, or null
+    uint32_t index_n32;   // index bytes, capped at 2^32 - 1
+    uint32_t ix_entries;  // byte offset of the index entries
+    int32_t n_chunks;
 };
 
 // What a launch makes of the decoded exponents.
@@ -119,7 +122,12 @@ enum Mode : int {
     kModeBf16 = 1,  // bf16 weights
     kModeGemv = 2,  // y += W x with W decoded on the fly and never written
     kModeGemv1 = 3, // kModeGemv for one x vector (batch 1)
+    kModeIndex = 4, // the segment index: each segment's first boundary and codewords
 };
+// Modes that combine the exponents with sign/mantissa bytes.
+constexpr bool needs_sm(int mode) { return mode != kModeU8 && mode != kModeIndex; }
+// Job::ib of a chunk decoded without the index.
+constexpr uint32_t kNoIndex = 0xFFFFFFFFu;
 constexpr int kGemvMaxBatch = 4;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -390,14 +398,37 @@ __device__ __forceinline__ void slot_put(uint8_t* q, uint32_t syms) {
     w[1] = static_cast<uint32_t>(v >> 32);
 }
 
+// Place the symbols of one lookup at q in a stage area that is zero where
+// nothing was placed, by OR into the word holding q and the word after it:
+// neighbouring segments share the words at their ends, so both are atomic.
+__device__ __forceinline__ void stage_or(uint8_t* q, uint32_t syms) {
+    const uint32_t b = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(q)) & 3u;
+    const uint64_t v = static_cast<uint64_t>(syms) << (8 * b);
+    uint32_t* w = reinterpret_cast<uint32_t*>(q - b);
+    __hip_atomic_fetch_or(w, static_cast<uint32_t>(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_fetch_or(w + 1, static_cast<uint32_t>(v >> 32), __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+template <bool kDirect>
+__device__ __forceinline__ void put(uint8_t* q, uint32_t syms) {
+    if (kDirect) {
+        stage_or(q, syms);
+    } else {
+        slot_put(q, syms);
+    }
+}
+
 // Parse codewords from true boundary p while they start before x, placing
-// their symbols in the slot (first word zero). Returns the first boundary at
-// or after x and the number of codewords. Every codeword (or unused window)
-// takes at least min_len bits, so a segment of at most kSlotCap * min_len
-// bits never holds more than kSlotCap codewords, and every write stays
-// inside the slot. The last lookup's symbols that start at or after x are
-// masked off before it is placed.
-template <bool kGlobalEsc>
+// their symbols from `slot` on. Returns the first boundary at or after x and
+// the number of codewords. Every codeword (or unused window) takes at least
+// min_len bits, so a segment of at most kSlotCap * min_len bits never holds
+// more than kSlotCap codewords, and every write stays within kSlotCap + 4
+// bytes of `slot`. The last lookup's symbols that start at or after x are
+// masked off before it is placed. kDirect: `slot` is the segment's place in
+// a zeroed stage area (stage_or); otherwise a private slot whose first word
+// is zero (slot_put).
+template <bool kGlobalEsc, bool kDirect>
 __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint32_t p,
                                           uint32_t x, uint8_t* slot) {
     if (p >= x) return {p, 0u};
@@ -411,7 +442,7 @@ __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint3
         // The next step's meta and pair go out before this step's symbols
         // are placed, its symbols after.
         Step t = lookup<false>(below, tb, pn, pn - s.m, s.next);
-        slot_put(q, syms);
+        put<kDirect>(q, syms);
         q += c;
         t.syms = tb.syms[t.idx];
         s = t;
@@ -420,7 +451,7 @@ __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint3
     }
     uint32_t kept;  // 1..4
     const uint32_t e = cut_window(tb, s.p, s.p + adv, syms, c, x, &kept);
-    slot_put(q, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
+    put<kDirect>(q, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
     return {e, static_cast<uint32_t>(q - slot) + kept};
 }
 
@@ -466,12 +497,28 @@ struct Job {
     uint32_t nb;   // chunk bytes
     uint32_t lim;  // output symbols of the chunk
     uint32_t nr;   // rounds
+    uint32_t ib;   // index entry of the chunk's first segment, or kNoIndex
 };
 
+// Whether tensor T's segment index is complete and was built for its
+// table: same segment length and table checksum (kModeIndex, which writes
+// the index, needs only the plan of the index built before it).
+template <int kMode>
+__device__ __forceinline__ bool index_usable(const DevTensor& T, uint32_t S) {
+    const uint8_t* ix = uniform(T.index);
+    if (ix == nullptr) return false;
+    const auto* h = (const __attribute__((address_space(4))) IndexHeader*)(ix);
+    if (h->magic != kIndexMagic || h->ok != 1u) return false;
+    if (kMode == kModeIndex) return true;
+    return h->version == static_cast<uint32_t>(kAbiVersion) && h->seg_bits == S &&
+           h->table_checksum == header_of(uniform(T.table))->checksum &&
+           h->n_chunks == static_cast<uint32_t>(T.n_chunks);
+}
+
 // kLg > 0: every tensor of the launch has 1 << kLg threads per chunk.
-template <uint32_t kLg>
+template <int kMode, uint32_t kLg>
 __device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, uint32_t tid) {
-    Job J{-1, 0u, kMaxSegBits, 0, 0u, 0u, 0u, 0u};
+    Job J{-1, 0u, kMaxSegBits, 0, 0u, 0u, 0u, 0u, kNoIndex};
     if (item >= args.total_items) return J;
     int d = 0;
     while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
@@ -481,26 +528,35 @@ __device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, ui
     const uint32_t n_groups = kThreads >> J.lg;
     J.c = (item - T.item_begin) * n_groups + (tid >> J.lg);
     // Segment length: at most kSlotCap codewords of the shortest length.
-    const uint32_t min_len = header_of(uniform(T.table))->min_len;
-    const uint32_t S = kSlotCap * (min_len >= 1 ? min_len : 1u);
-    J.S = (S < kMaxSegBits ? S : kMaxSegBits) & ~7u;
+    J.S = segment_bits(header_of(uniform(T.table))->min_len);
+    // The same for every sub-group of the item (a workgroup-wide choice).
+    const bool use_ix = index_usable<kMode>(T, J.S);
+    const __attribute__((address_space(4))) uint32_t* ix_base =
+        use_ix ? (const __attribute__((address_space(4))) uint32_t*)(uniform(T.index) +
+                                                                       sizeof(IndexHeader))
+               : nullptr;
     // A wave holds 64 >> lg sub-groups (one when lg >= 6), on consecutive
     // chunks. Their offsets and lengths come through scalar loads, so no wait
     // for them waits for the vector stores in flight; each lane keeps its own.
     const int64_t c_wave = (item - T.item_begin) * n_groups + (uniform(tid & ~63u) >> J.lg);
     const uint32_t per_wave = J.lg >= 6 ? 1u : 64u >> J.lg;
     int64_t off = 0, nb = 0;
+    uint32_t ib = 0;
 #pragma unroll
     for (uint32_t k = 0; k < 64 / kMinTpc; ++k) {
         if (k < per_wave && c_wave + k < T.n_jobs) {
             const int64_t o = load_uniform(T.offsets + c_wave + k);
             const int64_t n = load_uniform(T.nbytes + c_wave + k);
+            const uint32_t b = use_ix ? ix_base[c_wave + k] : 0u;
             if (J.c == c_wave + k) {
                 off = o;
                 nb = n;
+                ib = b;
             }
         }
     }
+    // kNoIndex marks "no index" for the whole item, so no entry may equal it.
+    J.ib = use_ix ? (ib < kNoIndex ? ib : kNoIndex - 1u) : kNoIndex;
     if (J.c < T.n_jobs) {
         off = off < 0 ? 0 : (off > T.packed_nbytes ? T.packed_nbytes : off);
         nb = nb < 0 ? 0 : (nb > T.packed_nbytes - off ? T.packed_nbytes - off : nb);
@@ -524,10 +580,20 @@ __device__ __forceinline__ uint32_t round_len(const Job& J, uint32_t r) {
 }
 
 // A thread's stream words of one round, in flight in registers until they
-// are written to the LDS tile: words k * tpc + i of the round.
+// are written to the LDS tile: words k * tpc + i of the round; and, for a
+// chunk decoded with its segment index, the index entry of the thread's
+// segment of that round.
 struct Fetch {
     uint32_t raw[kTileBatch];
+    uint32_t ent;
 };
+
+// The index entries of tensor T as a buffer (reads past its end return 0,
+// writes past it are dropped).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t index_entries(const DevTensor& T) {
+    const uint32_t at = T.ix_entries < T.index_n32 ? T.ix_entries : T.index_n32;
+    return buffer_of(T.index + at, T.index_n32 - at);
+}
 
 // Word 0 of sub-group g's tile (the tile is filled downwards, see Reader).
 __device__ __forceinline__ uint32_t* tile_top(uint32_t* s_tile, uint32_t g, uint32_t lg) {
@@ -543,12 +609,15 @@ __device__ __forceinline__ uint32_t last_word(const DevTensor& T) {
 // kTiny: the packed buffer has fewer than 4 bytes, so its words are read
 // byte by byte. Such tensors go to a kernel of their own, which keeps these
 // loads and their waits out of every other kernel's round loop.
-template <bool kTiny>
+template <int kMode, bool kTiny>
 __device__ __forceinline__ void fetch_issue(Fetch& F, const LaunchArgs& args, const Job& J,
                                             uint32_t r, uint32_t tid) {
     if (round_len(J, r) == 0) return;
     const DevTensor& T = args.t[J.d];
     const uint32_t tpc = 1u << J.lg;
+    if (kMode != kModeIndex && !kTiny && J.ib != kNoIndex)
+        F.ent = __builtin_amdgcn_raw_buffer_load_b16(
+            index_entries(T), 2u * (J.ib + r * tpc + (tid & (tpc - 1))), 0, 0);
     const uint32_t b0 = ((r * J.S) << J.lg) / 8 + 4 * (tid & (tpc - 1));
     // All words are requested before any is used; words past the chunk read
     // an in-buffer word and are zeroed when written.
@@ -577,6 +646,7 @@ __device__ __forceinline__ void fetch_commit(const Fetch& F, const LaunchArgs& a
                                              uint32_t r, uint32_t tid, uint32_t* s_tile) {
 #pragma unroll
     for (uint32_t k = 0; k < kTileBatch; ++k) consume(F.raw[k]);
+    consume(F.ent);
     const uint32_t RB = round_len(J, r);
     if (RB == 0) return;
     const DevTensor& T = args.t[J.d];
@@ -687,7 +757,7 @@ __device__ __forceinline__ void store_one(const DevTensor& T, const GemvArgs& G,
         static_cast<uint8_t*>(T.out)[el] = static_cast<uint8_t>(e);
     } else if (kMode == kModeBf16) {
         static_cast<uint16_t*>(T.out)[el] = bf16_one(T.sm[el], e);
-    } else {
+    } else if (kMode == kModeGemv || kMode == kModeGemv1) {
         const float w = bf16_to_f32(bf16_one(T.sm[el], e));
         const uint32_t row = static_cast<uint32_t>(el / G.cols);
         const uint32_t col = static_cast<uint32_t>(el - static_cast<int64_t>(row) * G.cols);
@@ -701,7 +771,7 @@ __device__ __forceinline__ void store_one(const DevTensor& T, const GemvArgs& G,
 // (groups k * tpc + i of the round), requested ahead of use.
 template <int kMode>
 struct SmBatch {
-    uint2 v[kMode != kModeU8 ? kSmAhead : 1];
+    uint2 v[needs_sm(kMode) ? kSmAhead : 1];
 };
 
 // Buffer loads (zero past the tensor's last byte), so the batch needs no
@@ -709,7 +779,7 @@ struct SmBatch {
 template <int kMode, int kGroup>
 __device__ __forceinline__ void sm_issue(SmBatch<kMode>& B, const DevTensor& T, int64_t a0,
                                          uint32_t i, uint32_t tpc) {
-    if (kMode == kModeU8 || kGroup == 1) return;
+    if (!needs_sm(kMode) || kGroup == 1) return;
     const __amdgpu_buffer_rsrc_t rs = buffer_of(T.sm, static_cast<uint32_t>(T.n_symbols));
     const uint32_t v0 = static_cast<uint32_t>(a0) + i * kGroup;
 #pragma unroll
@@ -1160,9 +1230,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     // Software pipeline: the stream words of the next round (or of the next
     // item's first round) are in flight while the current round decodes.
     // The first item's words and table load together.
-    Job cur = make_job<kLg>(args, blockIdx.x, tid);
+    Job cur = make_job<kMode, kLg>(args, blockIdx.x, tid);
     Fetch F;
-    fetch_issue<kTiny>(F, args, cur, 0, tid);
+    fetch_issue<kMode, kTiny>(F, args, cur, 0, tid);
     loaded = uniform(args.t[uniform(static_cast<uint32_t>(cur.d))].table);
     load_table(loaded, tid, s_wsyms, s_wmeta, s_len, s_esc);
     fetch_commit<kTiny>(F, args, cur, 0, tid, s_tile);
@@ -1176,7 +1246,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         const uint32_t i_item = tid & (tpc - 1);
         const uint32_t n_groups = kThreads >> lg;
         const uint32_t S = uniform(cur.S);
-        const Job nxt = make_job<kLg>(args, item + gridDim.x, tid);
+        const Job nxt = make_job<kMode, kLg>(args, item + gridDim.x, tid);
 
         const auto* hdr = header_of(table);
         tb.sym0 = hdr->sym0;
@@ -1205,9 +1275,96 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         for (uint32_t k = 0; k < n_groups; ++k) NR = NR > s_gval[k] ? NR : s_gval[k];
         NR = uniform(NR);
 
-        uint32_t p0 = 0;    // true start of the next round, relative to its first bit
         int64_t ob = 0;     // chunk-local symbols placed so far
         uint32_t lead = 0;  // placed symbols still staged at the front of the region
+        // Chunks with a usable segment index (the same for the whole item).
+        const bool use_idx = kMode != kModeIndex && !kTiny && uniform(cur.ib) != kNoIndex;
+        if (use_idx) {
+            // Each segment's first boundary and codeword count come from the
+            // index, so the round's placement is known before it decodes:
+            // each thread decodes from its true start and ORs its symbols
+            // straight into their place in the stage area, which is zero
+            // wherever nothing is placed. No look-ahead, agreement check or
+            // compaction.
+            for (uint32_t j = tid; j < kStageBytes / 16; j += kThreads)
+                reinterpret_cast<uint4*>(s_stage)[j] = make_uint4(0u, 0u, 0u, 0u);
+            for (uint32_t r = 0; r < NR; ++r) {
+                uint32_t i = i_item;
+                asm volatile("" : "+v"(i));
+                const bool last = r + 1 == NR;
+                const Job& fj = last ? nxt : cur;
+                const uint32_t fr = last ? 0u : r + 1;
+                const uint32_t ent = F.ent;  // this round's entry, fetched with its words
+                __builtin_amdgcn_s_setprio(3);
+                fetch_issue<kMode, kTiny>(F, args, fj, fr, tid);
+                SmBatch<kMode> smb;
+                sm_issue<kMode, kGroup>(smb, T, chunk_base + ob - lead, i, tpc);
+                const uint32_t RB = round_len(cur, r);
+                const bool g_active = RB != 0;
+                const uint32_t seg_lo = i * S;
+                const bool active = seg_lo < RB;
+                const uint32_t seg_hi = active ? (seg_lo + S < RB ? seg_lo + S : RB) : 0u;
+                // Counts above kSlotCap only come from a foreign index; the
+                // clamp keeps every placement inside the stage area.
+                const uint32_t ecnt = ent >> 4;
+                const uint32_t cnt = active ? (ecnt < kSlotCap ? ecnt : kSlotCap) : 0u;
+                __builtin_amdgcn_s_setprio(1);
+                const uint32_t excl = block_scan_excl(cnt, s_wsum);
+                if (i == 0) s_gpre[g] = excl;
+                if (tid == kThreads - 1) s_gpre[n_groups] = excl + cnt;
+                __syncthreads();
+                const uint32_t o = excl - s_gpre[g];
+                const uint32_t gtot = s_gpre[g + 1] - s_gpre[g];
+                const int64_t still = lim - ob;
+                const uint32_t want =
+                    g_active ? (gtot < still ? gtot : static_cast<uint32_t>(still)) : 0u;
+                const uint32_t avail = lead + want;
+                const uint32_t nfull = avail / kGroup;
+                const int64_t a0 = chunk_base + ob - lead;
+                __builtin_amdgcn_s_setprio(0);
+                if (active) {
+                    const uint32_t f = seg_lo + (ent & 15u);
+                    uint8_t* dst = stage + lead + o;
+                    if (global_esc) {
+                        decode_run<true, true>(below, tb, f, seg_hi, dst);
+                    } else {
+                        decode_run<false, true>(below, tb, f, seg_hi, dst);
+                    }
+                }
+                __syncthreads();  // the round is placed; the tile takes the next words
+                fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
+                __builtin_amdgcn_s_setprio(2);
+                store_round<kMode, kGroup, kLg == kLgThreads>(smb, T, args.gemv, stage, a0, nfull,
+                                                              i, tpc);
+                ob += want;
+                // The partial vector group (rem < 16 bytes at a multiple of
+                // kGroup) moves to the front; all else placed is cleared.
+                const uint32_t rem = avail - nfull * kGroup;
+                uint2 k0 = make_uint2(0u, 0u), k1 = make_uint2(0u, 0u);
+                if (i == 0 && rem != 0) {
+                    const uint2* src = reinterpret_cast<const uint2*>(stage + nfull * kGroup);
+                    k0 = src[0];
+                    k1 = src[1];
+                    const uint64_t a = static_cast<uint64_t>(k0.x) | static_cast<uint64_t>(k0.y) << 32;
+                    const uint64_t b = static_cast<uint64_t>(k1.x) | static_cast<uint64_t>(k1.y) << 32;
+                    const uint64_t am = rem >= 8 ? a : a & ((uint64_t{1} << (8 * rem)) - 1);
+                    const uint64_t bm = rem <= 8 ? 0 : b & ((uint64_t{1} << (8 * (rem - 8))) - 1);
+                    k0 = make_uint2(static_cast<uint32_t>(am), static_cast<uint32_t>(am >> 32));
+                    k1 = make_uint2(static_cast<uint32_t>(bm), static_cast<uint32_t>(bm >> 32));
+                }
+                const uint32_t placed = (lead + gtot + 4 + 15) & ~15u;
+                const uint32_t zend = placed < region ? placed : region;
+                __syncthreads();
+                for (uint32_t z = 16 + 16 * i; z < zend; z += 16 * tpc)
+                    *reinterpret_cast<uint4*>(stage + z) = make_uint4(0u, 0u, 0u, 0u);
+                if (i == 0) {
+                    reinterpret_cast<uint2*>(stage)[0] = k0;
+                    reinterpret_cast<uint2*>(stage)[1] = k1;
+                }
+                lead = rem;
+            }
+        } else {
+        uint32_t p0 = 0;    // true start of the next round, relative to its first bit
         for (uint32_t r = 0; r < NR; ++r) {
             // Offsets derived from the thread index are cheap to recompute;
             // keeping them live across the round costs registers.
@@ -1222,7 +1379,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             // agreement check and scan after, and the decode loops last (each
             // setting measured; 6.5% faster than equal priorities).
             __builtin_amdgcn_s_setprio(3);
-            fetch_issue<kTiny>(F, args, fj, fr, tid);
+            fetch_issue<kMode, kTiny>(F, args, fj, fr, tid);
             // Sign/mantissa bytes of every group this round can fill (its
             // output starts at a known element; its length is known only
             // after decoding), requested now so the store never waits.
@@ -1241,10 +1398,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 Adv a;
                 if (global_esc) {
                     f = i == 0 ? p0 : advance<true>(below, tb, seg_lo - kOverlapBits, seg_lo);
-                    a = decode_run<true>(below, tb, f, seg_hi, slot);
+                    a = decode_run<true, false>(below, tb, f, seg_hi, slot);
                 } else {
                     f = i == 0 ? p0 : advance<false>(below, tb, seg_lo - kOverlapBits, seg_lo);
-                    a = decode_run<false>(below, tb, f, seg_hi, slot);
+                    a = decode_run<false, false>(below, tb, f, seg_hi, slot);
                 }
                 e = a.p;
                 cnt = a.n;
@@ -1273,14 +1430,26 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 if (bad) {
                     f = ep;
                     start_slot(slot);
-                    const Adv a = global_esc ? decode_run<true>(below, tb, f, seg_hi, slot)
-                                             : decode_run<false>(below, tb, f, seg_hi, slot);
+                    const Adv a = global_esc ? decode_run<true, false>(below, tb, f, seg_hi, slot)
+                                             : decode_run<false, false>(below, tb, f, seg_hi, slot);
                     e = a.p;
                     cnt = a.n;
                 }
             }
             const uint32_t n_active = g_active ? (RB + S - 1) / S : 1u;
             if (i == n_active - 1) s_glast[g] = e;
+            if constexpr (kMode == kModeIndex) {
+                // Index build: each segment's first boundary (0..15 bits
+                // past its start) and codeword count; no output.
+                if (active && cur.ib != kNoIndex)
+                    __builtin_amdgcn_raw_buffer_store_b16(
+                        static_cast<uint16_t>((cnt << 4) | (f - seg_lo)), index_entries(T),
+                        2u * (cur.ib + r * tpc + i), 0, 0);
+                fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
+                __syncthreads();
+                if (g_active) p0 = s_glast[g] - RB;
+                continue;
+            }
 
             const uint32_t excl = block_scan_excl(cnt, s_wsum);
             if (i == 0) s_gpre[g] = excl;
@@ -1343,19 +1512,22 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             lead = rem;
             if (g_active) p0 = e_last - RB;
         }
+        }
         if (NR == 0) {
-            fetch_issue<kTiny>(F, args, nxt, 0, tid);
+            fetch_issue<kMode, kTiny>(F, args, nxt, 0, tid);
             fetch_commit<kTiny>(F, args, nxt, 0, tid, s_tile);
         }
 
         // Symbols carried out of the last round, then positions no codeword
         // of the chunk reached: those decode from zero bits, i.e. to sym_lut[0].
         __syncthreads();
-        const int64_t t0 = chunk_base + ob - lead;
-        const int64_t n_tail = lim - (ob - lead);
-        for (int64_t k = i_item; k < n_tail; k += tpc) {
-            const uint32_t ex = k < lead ? stage[k] : tb.sym0;
-            store_one<kMode>(T, args.gemv, t0 + k, ex);
+        if constexpr (kMode != kModeIndex) {
+            const int64_t t0 = chunk_base + ob - lead;
+            const int64_t n_tail = lim - (ob - lead);
+            for (int64_t k = i_item; k < n_tail; k += tpc) {
+                const uint32_t ex = k < lead ? stage[k] : tb.sym0;
+                store_one<kMode>(T, args.gemv, t0 + k, ex);
+            }
         }
         cur = nxt;
     }
@@ -1400,6 +1572,15 @@ int launch_batch(Batch& B, hipStream_t s, bool tiny) {
     const int64_t grid = B.items < slots ? B.items : slots;
     const dim3 gdim(static_cast<uint32_t>(grid)), bdim(kThreads);
     constexpr int kVecGroup = kMode == kModeU8 ? 16 : 8;
+    if constexpr (kMode == kModeIndex) {
+        // No output: one kernel per sub-group geometry.
+        if (tiny)
+            hipLaunchKernelGGL((decode_kernel<kMode, 1, true, 0>), gdim, bdim, 0, s, B.args);
+        else if (B.full)
+            hipLaunchKernelGGL((decode_kernel<kMode, 1, false, kLgThreads>), gdim, bdim, 0, s, B.args);
+        else
+            hipLaunchKernelGGL((decode_kernel<kMode, 1, false, 0>), gdim, bdim, 0, s, B.args);
+    } else {
     if (tiny) {
         hipLaunchKernelGGL((decode_kernel<kMode, 1, true, 0>), gdim, bdim, 0, s, B.args);
     } else if (B.vec && B.full) {
@@ -1408,6 +1589,7 @@ int launch_batch(Batch& B, hipStream_t s, bool tiny) {
         hipLaunchKernelGGL((decode_kernel<kMode, kVecGroup, false, 0>), gdim, bdim, 0, s, B.args);
     } else {
         hipLaunchKernelGGL((decode_kernel<kMode, 1, false, 0>), gdim, bdim, 0, s, B.args);
+    }
     }
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess)
@@ -1427,8 +1609,8 @@ int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny) {
     if (t.n_symbols == 0) return AIMG_OK;
     if (t.n_symbols > INT32_MAX)
         return fail(AIMG_ERR_UNSUPPORTED, who + "more than 2^31 - 1 symbols");
-    const bool need_sm = kMode != kModeU8;
-    const bool need_out = kMode != kModeGemv && kMode != kModeGemv1;
+    const bool need_sm = needs_sm(kMode);
+    const bool need_out = kMode == kModeU8 || kMode == kModeBf16;
     if (t.packed == nullptr || t.chunk_offsets == nullptr || t.chunk_nbytes == nullptr ||
         (need_out && t.out == nullptr) || t.table == nullptr ||
         (need_sm && t.sign_mantissa == nullptr))
@@ -1452,6 +1634,18 @@ int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny) {
                         ? UINT32_MAX : static_cast<uint32_t>(t.packed_nbytes);
     dt.n_symbols = t.n_symbols;
     dt.chunk_size = t.chunk_size;
+    dt.n_chunks = t.n_chunks;
+    // An index too small for its header and chunk bases, or misaligned, is
+    // not one (the decoders ignore it; aimg_build_index refuses it).
+    const size_t ix_at = index_entries_offset(t.n_chunks);
+    const bool ix_ok = t.index != nullptr && t.index_nbytes >= static_cast<int64_t>(ix_at) &&
+                       reinterpret_cast<uintptr_t>(t.index) % 16 == 0;
+    dt.index = ix_ok ? static_cast<uint8_t*>(t.index) : nullptr;
+    dt.index_n32 = !ix_ok ? 0u
+                   : t.index_nbytes > static_cast<int64_t>(UINT32_MAX) ? UINT32_MAX
+                   : static_cast<uint32_t>(t.index_nbytes);
+    dt.ix_entries = ix_ok && ix_at < UINT32_MAX ? static_cast<uint32_t>(ix_at) : 0u;
+    if (ix_ok && ix_at >= UINT32_MAX) dt.index = nullptr;
     dt.tpc = static_cast<int32_t>(threads_per_chunk(t.chunk_size));
     if (dt.tpc != kThreads) B.full = false;
     // Chunks past the last output element hold nothing to write.
@@ -1481,6 +1675,53 @@ int launch(const aimg_tensor* ts, int n, const GemvArgs& gemv, bool vec_ok, void
     const int rc = launch_batch<kMode>(normal, s, false);
     if (rc != AIMG_OK) return rc;
     return launch_batch<kMode>(tiny, s, true);
+}
+
+// First step of an index build, one workgroup per tensor: chunk c's
+// segments (ceil(8 * nbytes / S), for the chunk's bytes clamped to the
+// packed buffer as the decode kernels clamp them) get entries base[c] ..
+// base[c + 1] - 1, and the header records the segment length, the table's
+// checksum and whether every entry fits the index.
+__global__ __launch_bounds__(kThreads) void index_plan_kernel(const LaunchArgs args) {
+    __shared__ uint32_t s_wsum[kWaves];
+    const DevTensor& T = args.t[blockIdx.x];
+    uint8_t* const ix = T.index;
+    if (ix == nullptr) return;
+    const auto* th = header_of(T.table);
+    const uint32_t S = segment_bits(th->min_len);
+    uint32_t* const base = reinterpret_cast<uint32_t*>(ix + sizeof(IndexHeader));
+    const uint64_t cap = T.ix_entries < T.index_n32 ? (T.index_n32 - T.ix_entries) / 2 : 0;
+    uint64_t run = 0;
+    for (int64_t c0 = 0; c0 < T.n_chunks; c0 += kThreads) {
+        const int64_t c = c0 + threadIdx.x;
+        uint32_t nseg = 0;
+        if (c < T.n_jobs) {
+            int64_t off = T.offsets[c], nb = T.nbytes[c];
+            off = off < 0 ? 0 : (off > T.packed_nbytes ? T.packed_nbytes : off);
+            nb = nb < 0 ? 0 : (nb > T.packed_nbytes - off ? T.packed_nbytes - off : nb);
+            nseg = static_cast<uint32_t>((nb * 8 + S - 1) / S);
+        }
+        const uint32_t excl = block_scan_excl(nseg, s_wsum);
+        uint32_t tot = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) tot += s_wsum[w];
+        const uint64_t at = run + excl;
+        if (c < T.n_chunks) base[c] = at < kNoIndex ? static_cast<uint32_t>(at) : kNoIndex - 1u;
+        run += tot;
+        __syncthreads();  // s_wsum is written again by the next block's scan
+    }
+    if (threadIdx.x == 0) {
+        base[T.n_chunks] = run < kNoIndex ? static_cast<uint32_t>(run) : kNoIndex - 1u;
+        IndexHeader h{};
+        h.magic = kIndexMagic;
+        h.version = static_cast<uint32_t>(kAbiVersion);
+        h.seg_bits = S;
+        h.table_checksum = th->checksum;
+        h.ok = run <= cap ? 1u : 0u;
+        h.n_chunks = static_cast<uint32_t>(T.n_chunks);
+        h.capacity = static_cast<uint32_t>(cap < kNoIndex ? cap : kNoIndex - 1u);
+        *reinterpret_cast<IndexHeader*>(ix) = h;
+    }
 }
 
 // Recombine of already-decoded exponents: out[i] = bf16 bits of (sm[i], e[i]).
@@ -1541,6 +1782,47 @@ extern "C" int aimg_recombine_bf16(const uint8_t* exponent, const uint8_t* sign_
     if (err != hipSuccess)
         return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
     return AIMG_OK;
+}
+
+extern "C" int aimg_build_index(const aimg_tensor* tensors, int n_tensors, void* stream) {
+    using aimg::fail;
+    if (tensors == nullptr && n_tensors > 0) return fail(AIMG_ERR_INVALID_ARGUMENT, "tensors is null");
+    if (n_tensors < 0 || n_tensors > AIMG_MAX_TENSORS)
+        return fail(AIMG_ERR_INVALID_ARGUMENT,
+                    "n_tensors must be in 0.." + std::to_string(AIMG_MAX_TENSORS));
+    // Tensors that have an index; each must be able to hold its header and
+    // chunk bases. Tensors with no symbols have nothing to index.
+    aimg::Batch normal, tiny;
+    aimg::LaunchArgs plan{};
+    int n_plan = 0;
+    for (int i = 0; i < n_tensors; ++i) {
+        const aimg_tensor& t = tensors[i];
+        if (t.index == nullptr) continue;
+        if (t.n_chunks < 0 ||
+            t.index_nbytes < static_cast<int64_t>(aimg::index_entries_offset(t.n_chunks)))
+            return fail(AIMG_ERR_INVALID_ARGUMENT, "tensor " + std::to_string(i) +
+                                                       ": index_nbytes is below aimg_index_nbytes");
+        if (reinterpret_cast<uintptr_t>(t.index) % 16 != 0)
+            return fail(AIMG_ERR_INVALID_ARGUMENT,
+                        "tensor " + std::to_string(i) + ": index must be 16-byte aligned");
+        const int n0 = normal.m, t0 = tiny.m;
+        const int rc = aimg::add_tensor<aimg::kModeIndex>(t, i, normal, tiny);
+        if (rc != AIMG_OK) return rc;
+        if (normal.m > n0) plan.t[n_plan++] = normal.args.t[normal.m - 1];
+        if (tiny.m > t0) plan.t[n_plan++] = tiny.args.t[tiny.m - 1];
+    }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n_plan > 0) {
+        plan.n_tensors = n_plan;
+        hipLaunchKernelGGL(aimg::index_plan_kernel, dim3(static_cast<uint32_t>(n_plan)),
+                           dim3(aimg::kThreads), 0, s, plan);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess)
+            return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    }
+    const int rc = aimg::launch_batch<aimg::kModeIndex>(normal, s, false);
+    if (rc != AIMG_OK) return rc;
+    return aimg::launch_batch<aimg::kModeIndex>(tiny, s, true);
 }
 
 extern "C" int aimg_decode_bf16(const aimg_tensor* tensors, int n_tensors, void* stream) {

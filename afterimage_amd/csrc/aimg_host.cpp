@@ -161,7 +161,33 @@ extern "C" int aimg_build_table(const int32_t* sym_lut, const int8_t* len_lut, i
     hdr.sym0 = static_cast<uint32_t>(sym_lut[0]);
     hdr.len0 = static_cast<uint32_t>(len_lut[0]);
     hdr.n_esc_blocks = n_blocks;
+    // FNV-1a over the tables: a segment index records the checksum of the
+    // table it was built with, and is used only with a table that matches.
+    uint32_t h = 2166136261u;
+    for (size_t k = sizeof(hdr); k < need; ++k) h = (h ^ blob[k]) * 16777619u;
+    hdr.checksum = h;
     std::memcpy(blob, &hdr, sizeof(hdr));
+    return AIMG_OK;
+}
+
+extern "C" int aimg_index_nbytes(const void* host_table, int64_t packed_nbytes, int32_t n_chunks,
+                                 size_t* nbytes) {
+    if (host_table == nullptr || nbytes == nullptr)
+        return fail(AIMG_ERR_INVALID_ARGUMENT, "null pointer passed to aimg_index_nbytes");
+    if (packed_nbytes < 0 || n_chunks < 0)
+        return fail(AIMG_ERR_INVALID_ARGUMENT, "packed_nbytes and n_chunks must be >= 0");
+    aimg::TableHeader hdr;
+    std::memcpy(&hdr, host_table, sizeof(hdr));
+    if (hdr.magic != aimg::kTableMagic || hdr.version != static_cast<uint32_t>(aimg::kAbiVersion))
+        return fail(AIMG_ERR_BAD_TABLE, "table blob has a wrong magic or version "
+                                        "(build it with aimg_build_table)");
+    // Chunks laid out back to back have ceil(8 * nbytes / S) segments each,
+    // at most 8 * packed_nbytes / S + 1 together per chunk.
+    const int64_t seg = aimg::segment_bits(hdr.min_len);
+    const int64_t entries = (packed_nbytes * 8 + seg - 1) / seg + n_chunks;
+    if (entries > static_cast<int64_t>(UINT32_MAX))
+        return fail(AIMG_ERR_UNSUPPORTED, "index of more than 2^32 - 1 segments");
+    *nbytes = aimg::index_entries_offset(n_chunks) + 2 * static_cast<size_t>(entries);
     return AIMG_OK;
 }
 

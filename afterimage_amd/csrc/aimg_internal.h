@@ -8,7 +8,7 @@
 
 namespace aimg {
 
-constexpr int kAbiVersion = 8;
+constexpr int kAbiVersion = 9;
 constexpr uint32_t kTableMagic = 0x474D4941u;  // "AIMG"
 
 // Window table: for each 12-bit window, the codewords that lie wholly inside
@@ -43,7 +43,8 @@ struct TableHeader {
     uint32_t sym0;          // sym_lut[0]: what an all-zero window decodes to
     uint32_t len0;          // len_lut[0]
     uint32_t n_esc_blocks;  // escape blocks that follow the window table
-    uint32_t reserved[9];
+    uint32_t checksum;      // FNV-1a of every byte after the header
+    uint32_t reserved[8];
 };
 static_assert(sizeof(TableHeader) == 64, "header is 64 bytes");
 
@@ -55,6 +56,46 @@ constexpr size_t kEscOffset = kLenOffset + 256;
 // Fixed blob size: room for the largest possible escape-block count.
 inline size_t table_nbytes() {
     return kEscOffset + sizeof(uint16_t) * kEscBlockEntries * kMaxEscBlocks;
+}
+
+// Segment index of one tensor (aimg_build_index): for every segment of
+// seg_bits bits of every chunk (segment k of chunk c covers chunk bits
+// [k * seg_bits, (k + 1) * seg_bits)), the first codeword boundary at or
+// after the segment start, as an offset 0..15 from it, and the number of
+// codewords that start inside the segment, in one uint16:
+//   offset | count << 4.
+// Layout: the header, uint32 base[n_chunks + 1] (entry of segment 0 of
+// chunk c; base[n_chunks] = entries used), then uint16 entries[capacity].
+// seg_bits and the table checksum tie the index to the table it was built
+// with; ok is 1 when every chunk's entries fit the capacity.
+constexpr uint32_t kIndexMagic = 0x58444941u;  // "AIDX"
+
+struct IndexHeader {
+    uint32_t magic;
+    uint32_t version;
+    uint32_t seg_bits;
+    uint32_t table_checksum;
+    uint32_t ok;
+    uint32_t n_chunks;
+    uint32_t capacity;  // entries
+    uint32_t reserved[9];
+};
+static_assert(sizeof(IndexHeader) == 64, "index header is 64 bytes");
+
+// Offset of the entries of an index over n_chunks chunks (16-byte aligned).
+constexpr size_t index_entries_offset(int64_t n_chunks) {
+    return (sizeof(IndexHeader) + sizeof(uint32_t) * static_cast<size_t>(n_chunks + 1) + 15) &
+           ~static_cast<size_t>(15);
+}
+
+// Segment length for a code whose shortest codeword has min_len bits: at
+// most kSegCodewords codewords start in a segment, and it is at most
+// kMaxSegBits bits and a whole number of bytes.
+constexpr uint32_t kSegCodewords = 84;
+constexpr uint32_t kMaxSegBits = 168;
+constexpr uint32_t segment_bits(uint32_t min_len) {
+    const uint32_t s = kSegCodewords * (min_len >= 1 ? min_len : 1u);
+    return (s < kMaxSegBits ? s : kMaxSegBits) & ~7u;
 }
 
 int fail(int code, const std::string& msg);

@@ -9,6 +9,12 @@ on the current torch stream. No host synchronisation happens here.
 Decode tables are keyed by codebook content (the stored LUT bytes and width),
 so tensors that share a codebook share one device table, and a tensor can
 never be decoded with another codebook's table.
+
+A resident tensor may also carry a segment index (``build_index``): each
+168-bit segment's first codeword boundary and codeword count, 2 bytes per
+segment, built once by the GPU from the tensor itself. Decodes of a tensor
+with an index skip the speculative segment start, the agreement check and the
+compaction of the kernel's rounds; the output is the same.
 """
 from __future__ import annotations
 
@@ -238,17 +244,59 @@ class DeviceTensor:
     chunk_size: int
     n_symbols: int
     shape: tuple[int, ...]
+    index: torch.Tensor | None = None  # uint8 segment index (build_index), or None
 
     @property
     def n_chunks(self) -> int:
         return int(self.chunk_offsets.shape[0])
 
     @property
+    def index_nbytes(self) -> int:
+        """Bytes of this tensor's segment index (header, chunk bases and one
+        2-byte entry per segment)."""
+        n = ctypes.c_size_t(0)
+        _native.check(_native.lib().aimg_index_nbytes(
+            self.tables.host_blob.ctypes.data, int(self.packed.numel()), self.n_chunks,
+            ctypes.byref(n)))
+        return int(n.value)
+
+    @property
+    def index_bytes_read(self) -> int:
+        """Index bytes a decode reads: the chunk bases and the entries of the
+        chunks' segments (0 without an index)."""
+        if self.index is None:
+            return 0
+        seg = segment_bits(self.tables.host_blob)
+        nb = self.chunk_nbytes.to(torch.int64)
+        return int(4 * self.n_chunks + 2 * ((nb * 8 + seg - 1) // seg).sum().item())
+
+    @property
     def algorithmic_bytes(self) -> int:
         """Bytes one bf16 decode must move: chunk bitstreams, offsets and
-        lengths, sign/mantissa read, window table, and the bf16 write."""
+        lengths, sign/mantissa read, window table, the segment index when the
+        tensor has one, and the bf16 write."""
         return (int(self.chunk_nbytes.sum().item()) + 8 * self.n_chunks
-                + self.n_symbols + (5 * 4096 + 256) + 2 * self.n_symbols)
+                + self.n_symbols + (5 * 4096 + 256) + self.index_bytes_read
+                + 2 * self.n_symbols)
+
+    def build_index(self) -> "DeviceTensor":
+        """Build this tensor's segment index on the current stream (one pass
+        over its bitstreams); later decodes use it. Returns self."""
+        dev = self.packed.device
+        if dev.type != "cuda":
+            raise RuntimeError("the segment index is built on the GPU; tensor is on %s" % dev)
+        ix = torch.empty(self.index_nbytes, dtype=torch.uint8, device=dev)
+        d = (_native.AimgTensor * 1)()
+        d[0] = _descriptor(self, None, self.n_symbols)
+        d[0].index = ix.data_ptr()
+        d[0].index_nbytes = int(ix.numel())
+        with torch.cuda.device(dev):
+            _native.check(_native.lib().aimg_build_index(d, 1, _stream_handle(dev)))
+        self.index = ix
+        return self
+
+    def drop_index(self) -> None:
+        self.index = None
 
     @classmethod
     def from_encoded(cls, enc, sign_mantissa, device, tables: DecodeTables | None = None):
@@ -272,14 +320,24 @@ def _stream_handle(device) -> int:
     return torch.cuda.current_stream(torch.device(device)).cuda_stream
 
 
-def _descriptor(t: DeviceTensor, out: torch.Tensor, n_out: int) -> _native.AimgTensor:
+def segment_bits(host_blob: np.ndarray) -> int:
+    """Bits per decode segment for a table blob: 84 codewords of its shortest
+    length, at most 168, a whole number of bytes."""
+    min_len = max(1, int(np.frombuffer(host_blob[12:16].tobytes(), np.uint32)[0]))
+    return min(84 * min_len, 168) & ~7
+
+
+def _descriptor(t: DeviceTensor, out: torch.Tensor | None, n_out: int) -> _native.AimgTensor:
     d = _native.AimgTensor()
     d.packed = t.packed.data_ptr()
     d.chunk_offsets = t.chunk_offsets.data_ptr()
     d.chunk_nbytes = t.chunk_nbytes.data_ptr()
     d.sign_mantissa = t.sign_mantissa.data_ptr() if t.sign_mantissa is not None else None
-    d.out = out.data_ptr()
+    d.out = out.data_ptr() if out is not None else None
     d.table = t.tables.blob.data_ptr()
+    if t.index is not None:
+        d.index = t.index.data_ptr()
+        d.index_nbytes = int(t.index.numel())
     d.packed_nbytes = int(t.packed.numel())
     d.n_symbols = int(n_out)
     d.chunk_size = int(t.chunk_size)

@@ -4,14 +4,16 @@ Default workload (the headline): one 5120x17408 bf16 weight (N(0, 0.02) with
 0.1% N(0, 0.5) outliers, seed 2), compressed with a per-tensor
 canonical-Huffman exponent codebook in chunks of 65536 symbols (1360 chunks).
 Its compressed form (bitstreams, chunk offsets/lengths, sign/mantissa bytes,
-decode table) is resident in HBM before timing starts. One step = one kernel
-launch that rebuilds the whole bf16 tensor in HBM. --workload block does the
-same for a whole 14B-class decoder block (9 tensors, one codebook per role)
-in one launch. Prints one JSON line.
+decode table, and the segment index built once when the layer became
+resident) is in HBM before timing starts. One step = one kernel launch that
+rebuilds the whole bf16 tensor in HBM. The same launch without the index is
+timed as well ("no_index"). --workload block does the same for a whole
+14B-class decoder block (9 tensors, one codebook per role) in one launch.
+Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
                     [--workload layer|block|gemv|ring|api] [--chunk-size N]
-                    [--batch B] [--no-cpu-baseline] [--cpu-threads T]
+                    [--batch B] [--no-index] [--no-cpu-baseline] [--cpu-threads T]
 """
 from __future__ import annotations
 
@@ -394,6 +396,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=40, help="ring: layers streamed per step")
     ap.add_argument("--batch", type=int, default=1, help="gemv batch (1..4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-index", action="store_true",
+                    help="layer/block: time the decode without segment indexes only")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="CPU-baseline threads (0: OpenMP's count, i.e. every CPU given)")
     ap.add_argument("--chunk-size", type=int, default=65536,
@@ -451,14 +455,66 @@ def main() -> int:
             sum(l.encoded.packed.nbytes for l in layers) / 1e6))
     dts = [DeviceTensor.from_encoded(l.encoded, l.sign_mantissa, dev) for l in layers]
     outs = [torch.empty(l.encoded.n_symbols, dtype=torch.bfloat16, device=dev) for l in layers]
-    desc = (_native.AimgTensor * len(dts))()
-    for j, (dt, o) in enumerate(zip(dts, outs)):
-        desc[j] = _descriptor(dt, o, o.numel())
     lib = _native.lib()
     stream = torch.cuda.current_stream(dev)
     handle = ctypes.c_void_p(stream.cuda_stream)
     decode = lib.aimg_decode_bf16
     n_desc = len(dts)
+
+    def descriptors():
+        d = (_native.AimgTensor * len(dts))()
+        for j, (dt, o) in enumerate(zip(dts, outs)):
+            d[j] = _descriptor(dt, o, o.numel())
+        return d
+
+    def bit_exact() -> bool:
+        torch.cuda.synchronize(dev)
+        return all(torch.equal(o.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
+                   for (_, W, _), o in zip(items, outs))
+
+    def launches(d, k: int) -> float:
+        """Seconds per launch of k back-to-back launches, by HIP events."""
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(dev)
+        e0.record(stream)
+        for _ in range(k):
+            rc = decode(d, n_desc, handle)
+            if rc:
+                _native.check(rc)
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        return e0.elapsed_time(e1) / 1e3 / k
+
+    # Without segment indexes first (the path any caller gets), then, unless
+    # --no-index, build each tensor's index once (a resident layer's load
+    # step) and time the decode that uses it.
+    plain = descriptors()
+    launches(plain, max(1, args.warmup))
+    if not bit_exact():
+        print("decoded output (no index) differs from the original weights", file=sys.stderr)
+        return 1
+    no_index_s = launches(plain, min(args.steps, 100))
+    index_info = None
+    if not args.no_index:
+        for o in outs:
+            o.fill_(0)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for dt in dts:
+            dt.build_index()
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        ix_bytes = sum(dt.index.numel() for dt in dts)
+        comp = sum(dt.packed.numel() + dt.sign_mantissa.numel() for dt in dts)
+        index_info = {
+            "build_us": round(e0.elapsed_time(e1) * 1e3, 1),
+            "bytes": ix_bytes,
+            "bytes_read_per_launch": sum(dt.index_bytes_read for dt in dts),
+            "frac_of_compressed": round(ix_bytes / comp, 4),
+        }
+    desc = descriptors()
 
     def step():
         rc = decode(desc, n_desc, handle)
@@ -467,14 +523,12 @@ def main() -> int:
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize(dev)
     # Bit-exactness of the benchmarked outputs (outside the timed region).
-    ok = all(torch.equal(o.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
-             for (_, W, _), o in zip(items, outs))
+    ok = bit_exact()
     if not ok:
         print("decoded output differs from the original weights", file=sys.stderr)
         return 1
-    _log("warmup done, output bit-exact")
+    _log("warmup done, output bit-exact (index %s)" % ("on" if index_info else "off"))
 
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
@@ -494,10 +548,14 @@ def main() -> int:
     n_chunks = sum(l.encoded.n_chunks for l in layers)
     chunk_bytes = sum(int(l.encoded.chunk_nbytes.astype(np.int64).sum()) for l in layers)
     n_tables = len({dt.tables.key for dt in dts})
-    # bitstreams + offsets and lengths + sign/mantissa + window tables + bf16 write
-    algo_bytes = chunk_bytes + 8 * n_chunks + n + (5 * 4096 + 256) * n_tables + 2 * n
+    # bitstreams + offsets and lengths + sign/mantissa + window tables + bf16
+    # write (+ the segment index entries and chunk bases read)
+    algo_plain = chunk_bytes + 8 * n_chunks + n + (5 * 4096 + 256) * n_tables + 2 * n
+    algo_bytes = algo_plain + (index_info["bytes_read_per_launch"] if index_info else 0)
     achieved = algo_bytes / kernel_s / 1e9
     value = 2 * n * args.steps / wall / 1e9
+    if index_info:
+        config_key += "/index"
     traffic = _traffic(config_key)
     rec = {
         "metric": METRIC,
@@ -522,6 +580,7 @@ def main() -> int:
             "packed_exponent_bytes": chunk_bytes,
             "bits_per_exponent": round(8 * chunk_bytes / n, 4),
             "bit_exact": ok,
+            "segment_index": index_info,
         },
         "roofline": {
             "bound": "hbm",
@@ -532,6 +591,13 @@ def main() -> int:
             "traffic": traffic,
             "algorithmic_bytes_per_launch": algo_bytes,
             "kernel_us": round(kernel_s * 1e6, 2),
+        },
+        "no_index": {
+            "kernel_us": round(no_index_s * 1e6, 2),
+            "decompressed_gbs": round(2 * n / no_index_s / 1e9, 1),
+            "achieved_gbs": round(algo_plain / no_index_s / 1e9, 1),
+            "frac": round(algo_plain / no_index_s / 1e9 / HBM_PEAK_GBS, 4),
+            "launches": min(args.steps, 100),
         },
         "cpu_baseline": None,
     }

@@ -87,6 +87,8 @@ typedef struct aimg_tensor {
     const uint8_t* sign_mantissa;  /* device: n_symbols bytes (bf16 only)       */
     void* out;                     /* device: uint16 bf16 bits, or uint8        */
     const void* table;             /* device: blob from aimg_build_table        */
+    void* index;                   /* device: segment index, or NULL (below)    */
+    int64_t index_nbytes;          /* bytes at `index`                          */
     int64_t packed_nbytes;         /* bytes readable at `packed`                */
     int64_t n_symbols;             /* elements to write (below 2^31)            */
     int32_t chunk_size;            /* symbols per chunk                         */
@@ -137,6 +139,44 @@ int aimg_decode_gemv_bf16(const aimg_tensor* t, int64_t rows, int64_t cols, cons
  */
 int aimg_recombine_bf16(const uint8_t* exponent, const uint8_t* sign_mantissa, void* out,
                         int64_t n, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Segment index (optional; no counterpart in the reference, whose decoder    */
+/* runs one chunk per lane and needs none).                                  */
+/* The decode kernels split each chunk into segments of a fixed number of     */
+/* bits, one per thread, and find where each segment's first codeword starts */
+/* by decoding ahead of it and checking agreement with the thread before.    */
+/* A segment index records, once per resident tensor, each segment's first   */
+/* codeword boundary and codeword count (2 bytes per segment of 168 bits for */
+/* bf16 exponent codes: about 2.3% of a compressed layer). A decode given    */
+/* the index skips the look-ahead, the agreement check and the compaction    */
+/* of its symbols, and writes each segment's symbols straight to their       */
+/* place. Decoding without an index (index == NULL) gives the same result.   */
+/* An index describes one tensor's packed bytes, chunk offsets and lengths   */
+/* and table: the decoders use it only with the table it was built with      */
+/* (checked by checksum) and otherwise ignore it; with other packed bytes or */
+/* offsets than it was built from the output is unspecified (memory stays    */
+/* in bounds).                                                               */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Bytes of the segment index for a tensor of packed_nbytes packed bytes in
+ * n_chunks chunks whose chunks lie back to back in `packed` (as the
+ * encoder writes them, huffman_chunked.py:204-205), for the table whose
+ * host blob (from aimg_build_table) is host_table.
+ */
+int aimg_index_nbytes(const void* host_table, int64_t packed_nbytes, int32_t n_chunks,
+                      size_t* nbytes);
+
+/*
+ * Build the segment index of each tensor into its `index` (device memory of
+ * index_nbytes >= aimg_index_nbytes bytes; tensors with a NULL index are
+ * skipped). Two launches on `stream`; the decoders that follow on the
+ * stream use the index. When the chunks' segments do not fit index_nbytes
+ * (chunks not back to back) the index is marked unusable and decoders
+ * ignore it. Other fields as for aimg_decode_u8.
+ */
+int aimg_build_index(const aimg_tensor* tensors, int n_tensors, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Host decode (CPU threads).                                                */

@@ -1,7 +1,14 @@
 // Runs the CPU build of the decode kernel on one case directory written by
-// tests/test_kernel_emulation.py: decode <dir> <u8|bf16>. Every device buffer
-// is a heap block of exactly its size, so AddressSanitizer reports any access
-// past it.
+// tests/test_kernel_emulation.py: decode <dir> <u8|bf16|gemv> [index mode].
+// Every device buffer is a heap block of exactly its size, so
+// AddressSanitizer reports any access past it.
+//
+// Index modes: "index" builds the segment index (aimg_build_index, exact
+// size) and decodes with it, after checking that the build marked it
+// usable; "index-small" gives the build room for the chunk bases only (the
+// index must come out marked unusable, and decoding ignores it);
+// "index-foreign" changes the table checksum the index records after the
+// build (decoding must ignore it).
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -53,6 +60,34 @@ int main(int argc, char** argv) {
     t.n_symbols = n_symbols;
     t.chunk_size = chunk_size;
     t.n_chunks = (int32_t)n_chunks;
+    const std::string ix_mode = argc > 3 ? argv[3] : "";
+    if (!ix_mode.empty()) {
+        size_t ixn = 0;
+        if (aimg_index_nbytes(table, t.packed_nbytes, t.n_chunks, &ixn)) {
+            fprintf(stderr, "index_nbytes: %s\n", aimg_last_error());
+            return 8;
+        }
+        // index-small: the header and chunk bases, and room for one entry.
+        if (ix_mode == "index-small") ixn = ((64 + 4 * (n_chunks + 1) + 15) & ~15ull) + 2;
+        std::vector<uint8_t> ixv(ixn, 0x5A);
+        t.index = exact<uint8_t>(ixv);
+        t.index_nbytes = (int64_t)ixn;
+        if (aimg_build_index(&t, 1, nullptr)) {
+            fprintf(stderr, "build_index: %s\n", aimg_last_error());
+            return 9;
+        }
+        uint32_t hdr[7];
+        memcpy(hdr, t.index, sizeof hdr);
+        const bool ok = hdr[4] == 1;
+        if (ok != (ix_mode != "index-small") && n_symbols > 0) {
+            fprintf(stderr, "index ok flag %u in mode %s\n", hdr[4], ix_mode.c_str());
+            return 10;
+        }
+        if (ix_mode == "index-foreign") {
+            hdr[3] ^= 1u;
+            memcpy(t.index, hdr, sizeof hdr);
+        }
+    }
     if (std::string(argv[2]) == "gemv") {
         // y += W x for the rows x cols bf16 weight W, checked against
         // expect_y.bin within rel 1e-2 / abs 1e-3 (the GPU tests' bar).
@@ -94,6 +129,7 @@ int main(int argc, char** argv) {
     if (expect.size() != outv.size()) { fprintf(stderr, "size mismatch\n"); return 7; }
     size_t bad = 0;
     for (size_t k = 0; k < outv.size(); ++k) bad += ((const uint8_t*)out)[k] != expect[k];
-    printf("%s %s: %s (%zu bad bytes of %zu)\n", d.c_str(), argv[2], bad ? "MISMATCH" : "ok", bad, outv.size());
+    printf("%s %s %s: %s (%zu bad bytes of %zu)\n", d.c_str(), argv[2], ix_mode.c_str(),
+           bad ? "MISMATCH" : "ok", bad, outv.size());
     return bad ? 1 : 0;
 }

@@ -1,0 +1,204 @@
+"""Segment index (aimg_build_index) on the GPU: its entries against a CPU walk
+of the codeword starts, and decodes with it against decodes without it and
+against the known weights / exponents.
+
+The index has no counterpart in the reference (its decoder runs one chunk per
+lane and needs none); these tests pin it to the reference's decode results,
+which the decodes without the index already equal (test_gpu_decode.py).
+"""
+import numpy as np
+import pytest
+import torch
+
+from afterimage_amd import workloads
+from afterimage_amd.runtime.compressed_store import compress_layer, compress_group
+from afterimage_amd.runtime.device import (
+    DeviceTensor,
+    TABLES,
+    decode_bf16,
+    decode_gemv,
+    decode_u8,
+    segment_bits,
+)
+from afterimage_amd.runtime.huffman_chunked import encode_chunked
+from tests.distributions import many_escape_windows
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _starts(enc, c):
+    """Bit offsets of the codewords that start inside chunk c, walking from
+    its first bit (bits past the chunk read as zero, and a window the LUT has
+    no codeword for takes the shortest code length), then the end of the
+    last of them."""
+    off, nb = int(enc.chunk_offsets[c]), int(enc.chunk_nbytes[c])
+    data = np.frombuffer(np.asarray(enc.packed, np.uint8)[off: off + nb].tobytes() + b"\0" * 4,
+                         np.uint8)
+    mb = int(enc.max_bits)
+    lens = np.asarray(enc.len_lut, np.int64)
+    min_len = int(lens[lens > 0].min())
+    out, p, end = [], 0, 8 * nb
+    while p < end:
+        b = p >> 3
+        w = (int(data[b]) << 16 | int(data[b + 1]) << 8 | int(data[b + 2])) >> (8 - (p & 7))
+        idx = (w >> (16 - mb)) & ((1 << mb) - 1)
+        ln = int(lens[idx]) or min_len
+        out.append(p)
+        p += ln
+    out.append(p)
+    return np.asarray(out, np.int64)
+
+
+def _expected_index(enc, seg):
+    """(bases, entries) of the index: per chunk, per segment of seg bits, the
+    first boundary's offset from the segment start | count << 4."""
+    bases, entries = [], []
+    n_jobs = -(-int(enc.n_symbols) // int(enc.chunk_size))
+    for c in range(len(enc.chunk_offsets)):
+        bases.append(len(entries))
+        if c >= n_jobs:
+            continue
+        bounds = _starts(enc, c)
+        st = bounds[:-1]
+        nseg = -(-8 * int(enc.chunk_nbytes[c]) // seg)
+        for k in range(nseg):
+            lo = k * seg
+            inside = st[(st >= lo) & (st < lo + seg)]
+            f = int(bounds[bounds >= lo][0]) - lo
+            entries.append(f | (len(inside) << 4))
+    bases.append(len(entries))
+    return np.asarray(bases, np.uint32), np.asarray(entries, np.uint16)
+
+
+def _index_arrays(t):
+    ix = t.index.cpu().numpy()
+    hdr = ix[:64].view(np.uint32)
+    n = t.n_chunks
+    bases = ix[64: 64 + 4 * (n + 1)].view(np.uint32)
+    at = (64 + 4 * (n + 1) + 15) & ~15
+    return hdr, bases, ix[at:]
+
+
+@pytest.mark.parametrize("kind,chunk", [("skewed", 64), ("skewed", 1024), ("bf16", 4096),
+                                        ("bf16", 65536), ("escapes", 4096)])
+def test_index_entries_equal_a_cpu_walk_of_the_codeword_starts(kind, chunk):
+    if kind == "skewed":
+        torch.manual_seed(0)
+        exps = torch.randint(100, 140, (9000,))
+    elif kind == "escapes":
+        exps = torch.as_tensor(many_escape_windows(seed=5, n=30000))
+    else:
+        W = workloads.bf16_normal((64, 4500), 3, 0.02, outlier_frac=1e-3)
+        exps = ((W.view(torch.int16).to(torch.int32) & 0xFFFF) >> 7 & 0xFF).reshape(-1)
+    enc = encode_chunked(exps, chunk_size=chunk)
+    t = DeviceTensor.from_encoded(enc, None, DEV).build_index()
+    seg = segment_bits(t.tables.host_blob)
+    hdr, bases, entries = _index_arrays(t)
+    want_b, want_e = _expected_index(enc, seg)
+    assert hdr[2] == seg and hdr[4] == 1, "header: seg_bits %d ok %d" % (hdr[2], hdr[4])
+    assert np.array_equal(bases, want_b)
+    got = entries.view(np.uint16)[: len(want_e)]
+    bad = np.nonzero(got != want_e)[0]
+    assert bad.size == 0, "entries differ at %s: %s vs %s" % (bad[:5], got[bad[:5]], want_e[bad[:5]])
+    assert np.array_equal(decode_u8([t])[0].cpu().numpy(), exps.numpy().astype(np.uint8))
+
+
+@pytest.mark.parametrize("chunk", [16, 64, 256, 1024, 4096, 16384, 65536])
+def test_u8_decode_with_index_equals_the_exponents(chunk):
+    torch.manual_seed(chunk)
+    exps = torch.randint(60, 130, (50000,))
+    enc = encode_chunked(exps, chunk_size=chunk)
+    t = DeviceTensor.from_encoded(enc, None, DEV)
+    plain = decode_u8([t])[0].cpu().numpy()
+    t.build_index()
+    got = decode_u8([t])[0].cpu().numpy()
+    assert np.array_equal(plain, exps.numpy().astype(np.uint8))
+    assert np.array_equal(got, plain)
+
+
+def test_full_alphabet_and_ragged_tail_with_index():
+    torch.manual_seed(1)
+    exps = torch.randint(0, 256, (7777,))
+    enc = encode_chunked(exps, chunk_size=333)
+    t = DeviceTensor.from_encoded(enc, None, DEV).build_index()
+    assert np.array_equal(decode_u8([t])[0].cpu().numpy(), exps.numpy().astype(np.uint8))
+
+
+def test_bf16_full_layer_with_index_is_bit_exact():
+    W = workloads.bf16_normal((5120, 17408), 2, 0.02, outlier_frac=1e-3)
+    layer = compress_layer(W, chunk_size=65536)
+    t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, DEV).build_index()
+    out = decode_bf16([t])[0]
+    assert torch.equal(out.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
+    # Index size: 2 bytes per 168-bit segment (2.6 bits per exponent), about
+    # 2.3% of the compressed layer.
+    comp = t.packed.numel() + t.sign_mantissa.numel()
+    assert t.index.numel() < 0.025 * comp
+
+
+def test_block_with_and_without_indexes_in_one_launch():
+    blk = workloads.block_14b(scale=0.01, chunk_size=65536)
+    ts = [DeviceTensor.from_encoded(l.encoded, l.sign_mantissa, DEV) for _, _, l in blk]
+    for k, t in enumerate(ts):
+        if k % 2 == 0:
+            t.build_index()
+    outs = decode_bf16(ts)
+    for (name, w, _), o in zip(blk, outs):
+        assert torch.equal(o.view(torch.int16).cpu(), w.reshape(-1).view(torch.int16)), name
+
+
+def test_index_of_another_codebook_is_ignored():
+    ws = [workloads.bf16_normal((300, 2000), s, 0.02 * (s + 1), outlier_frac=1e-3) for s in (1, 2)]
+    la, lb = (compress_layer(w, chunk_size=4096) for w in ws)
+    ta = DeviceTensor.from_encoded(la.encoded, la.sign_mantissa, DEV).build_index()
+    tb = DeviceTensor.from_encoded(lb.encoded, lb.sign_mantissa, DEV)
+    # tb's bytes decoded with ta's index: the index records ta's table, so
+    # the decoder must not use it (different checksum).
+    tb.index = ta.index
+    assert not np.array_equal(la.encoded.sym_lut, lb.encoded.sym_lut) or \
+        not np.array_equal(la.encoded.len_lut, lb.encoded.len_lut)
+    out = decode_bf16([tb])[0]
+    assert torch.equal(out.view(torch.int16).cpu(), ws[1].reshape(-1).view(torch.int16))
+
+
+def test_shared_codebook_tensors_each_with_an_index():
+    ws = [workloads.bf16_normal((256, 3000), s, 0.02, outlier_frac=1e-3) for s in (4, 5, 6)]
+    layers = compress_group(ws, chunk_size=2048)
+    ts = [DeviceTensor.from_encoded(l.encoded, l.sign_mantissa, DEV).build_index() for l in layers]
+    assert len({id(t.tables) for t in ts}) == 1
+    for w, o in zip(ws, decode_bf16(ts)):
+        assert torch.equal(o.view(torch.int16).cpu(), w.reshape(-1).view(torch.int16))
+
+
+def test_an_index_too_small_is_marked_unusable_and_ignored():
+    W = workloads.bf16_normal((200, 3000), 7, 0.02, outlier_frac=1e-3)
+    layer = compress_layer(W, chunk_size=4096)
+    t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, DEV)
+    t.index = torch.zeros(((64 + 4 * (t.n_chunks + 1) + 15) & ~15) + 16, dtype=torch.uint8,
+                          device=DEV)
+    from afterimage_amd import _native
+    from afterimage_amd.runtime.device import _descriptor, _stream_handle
+    d = (_native.AimgTensor * 1)()
+    d[0] = _descriptor(t, None, t.n_symbols)
+    _native.check(_native.lib().aimg_build_index(d, 1, _stream_handle(DEV)))
+    hdr = t.index[:64].cpu().numpy().view(np.uint32)
+    assert hdr[4] == 0
+    out = decode_bf16([t])[0]
+    assert torch.equal(out.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_gemv_with_index_matches_without(batch):
+    W = workloads.bf16_normal((1024, 4096), 8, 0.02, outlier_frac=1e-3)
+    layer = compress_layer(W, chunk_size=65536)
+    t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, DEV)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn((batch, 4096), generator=g).to(torch.bfloat16).to(DEV)
+    y0 = decode_gemv(t, x, 1024, 4096)
+    t.build_index()
+    y1 = decode_gemv(t, x, 1024, 4096)
+    want = (x.double().cpu() @ W.double().t()).float()
+    assert torch.allclose(y1.cpu(), want, rtol=1e-2, atol=1e-3)
+    assert torch.allclose(y1, y0, rtol=1e-4, atol=1e-4)

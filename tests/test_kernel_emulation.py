@@ -73,28 +73,29 @@ def _write(d, enc, expect, sm=None):
         f.write("%d %d %d %d\n" % (enc.max_bits, enc.chunk_size, enc.n_symbols, len(enc.chunk_offsets)))
 
 
-def _run(emu, name, mode):
+def _run(emu, name, mode, index=""):
     exe, d = emu
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0")
-    r = subprocess.run([exe, str(d / name), mode], capture_output=True, text=True, env=env, timeout=600)
+    args = [exe, str(d / name), mode] + ([index] if index else [])
+    r = subprocess.run(args, capture_output=True, text=True, env=env, timeout=600)
     assert r.returncode == 0 and ": ok" in r.stdout, (r.stdout + r.stderr)[-4000:]
 
 
-def _u8(emu, name, exps, chunk_size):
+def _u8(emu, name, exps, chunk_size, index=""):
     exps = np.asarray(exps)
     enc = encode_chunked(torch.as_tensor(exps), chunk_size=chunk_size)
     _write(emu[1] / name, enc, exps.astype(np.uint8))
-    _run(emu, name, "u8")
+    _run(emu, name, "u8", index)
 
 
-def _bf16(emu, name, W, chunk_size):
+def _bf16(emu, name, W, chunk_size, index=""):
     layer = compress_layer(W, chunk_size=chunk_size)
     _write(emu[1] / name, layer.encoded, W.reshape(-1).view(torch.int16).numpy(),
            layer.sign_mantissa.numpy())
-    _run(emu, name, "bf16")
+    _run(emu, name, "bf16", index)
 
 
-def _gemv(emu, name, rows, cols, chunk_size, batch, seed):
+def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index=""):
     W = workloads.bf16_normal((rows, cols), seed, 0.02, outlier_frac=1e-3)
     layer = compress_layer(W, chunk_size=chunk_size)
     g = np.random.default_rng(seed + 1)
@@ -106,7 +107,7 @@ def _gemv(emu, name, rows, cols, chunk_size, batch, seed):
     want.numpy().tofile(os.path.join(d, "expect_y.bin"))
     with open(os.path.join(d, "gemv.txt"), "w") as f:
         f.write("%d %d %d\n" % (rows, cols, batch))
-    _run(emu, name, "gemv")
+    _run(emu, name, "gemv", index)
 
 
 @pytest.mark.parametrize("batch", [1, 4])
@@ -174,3 +175,64 @@ def test_u8_segment_guesses_all_wrong(emu):
     rng = np.random.default_rng(8)
     _u8(emu, "guess4096", rng.integers(0, 8, 20000), 4096)
     _u8(emu, "guess65536", rng.integers(0, 8, 70000), 65536)
+
+
+# Decoding with the segment index (aimg_build_index): the index is built by
+# the same kernel's build mode, then each segment decodes from its recorded
+# start straight into place; the result must equal the weights / exponents.
+
+@pytest.mark.parametrize("chunk_size", [64, 1024, 4096])
+def test_u8_with_index(emu, chunk_size):
+    torch.manual_seed(11)
+    _u8(emu, "ix_u8_%d" % chunk_size, torch.randint(100, 140, (12000,)).numpy(), chunk_size,
+        index="index")
+
+
+def test_u8_full_alphabet_with_index(emu):
+    torch.manual_seed(1)
+    _u8(emu, "ix_uniform256", torch.randint(0, 256, (8000,)).numpy(), 256, index="index")
+
+
+def test_u8_escape_blocks_beyond_the_lds_share_with_index(emu):
+    _u8(emu, "ix_escapes", many_escape_windows(seed=5, n=30000), 4096, index="index")
+
+
+def test_u8_tiny_packed_buffer_with_index(emu):
+    _u8(emu, "ix_tiny", np.array([7, 7, 7], np.uint8), 64, index="index")
+
+
+def test_u8_index_built_where_every_guess_is_wrong(emu):
+    rng = np.random.default_rng(8)
+    _u8(emu, "ix_guess", rng.integers(0, 8, 70000), 65536, index="index")
+
+
+def test_bf16_vector_path_with_index(emu):
+    torch.manual_seed(2)
+    _bf16(emu, "ix_bf16_vec", (torch.randn(256, 1024) * 0.02).to(torch.bfloat16), 4096,
+          index="index")
+
+
+def test_bf16_scalar_path_ragged_with_index(emu):
+    torch.manual_seed(4)
+    _bf16(emu, "ix_bf16_ragged", (torch.randn(300, 333) * 0.02).to(torch.bfloat16), 1000,
+          index="index")
+
+
+def test_bf16_two_round_64k_chunks_with_index(emu):
+    W = workloads.bf16_normal((64, 17408), 2, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "ix_bf16_64k", W, 65536, index="index")
+
+
+@pytest.mark.parametrize("mode", ["index-small", "index-foreign"])
+def test_unusable_index_is_ignored(emu, mode):
+    W = workloads.bf16_normal((40, 5000), 6, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "ix_%s" % mode, W, 4096, index=mode)
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_gemv_with_index(emu, batch):
+    _gemv(emu, "ix_gemv512_b%d" % batch, 70, 1000, 32768, batch, 5, index="index")
+
+
+def test_gemv_16_thread_chunks_with_index(emu):
+    _gemv(emu, "ix_gemv16", 96, 40, 64, 2, 3, index="index")

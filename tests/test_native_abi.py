@@ -239,3 +239,60 @@ def test_escape_blocks_can_exceed_the_lds_share():
     assert hdr[6] > 64  # n_esc_blocks
     assert int(enc.len_lut.max()) > 12
 
+
+
+def _bf16_table():
+    W = (torch.randn(64, 512, generator=torch.Generator().manual_seed(3)) * 0.02).to(torch.bfloat16)
+    bits = W.view(torch.int16).to(torch.int32) & 0xFFFF
+    enc = encode_chunked(((bits >> 7) & 0xFF).reshape(-1), chunk_size=1024)
+    return enc, build_table_blob(enc.sym_lut, enc.len_lut, enc.max_bits)
+
+
+def test_table_blob_records_a_checksum_of_its_tables():
+    _, blob = _bf16_table()
+    h = 2166136261
+    for b in blob[64:].tobytes():
+        h = ((h ^ b) * 16777619) & 0xFFFFFFFF
+    assert int(blob[28:32].view(np.uint32)[0]) == h
+
+
+def test_index_size_is_two_bytes_per_segment_plus_chunk_bases():
+    lib = _native.lib()
+    enc, blob = _bf16_table()
+    min_len = int(blob[12:16].view(np.uint32)[0])
+    seg = min(84 * min_len, 168) & ~7
+    n = ctypes.c_size_t()
+    packed, chunks = 1_000_003, 77
+    assert lib.aimg_index_nbytes(blob.ctypes.data, packed, chunks, ctypes.byref(n)) == 0
+    entries_at = (64 + 4 * (chunks + 1) + 15) & ~15
+    assert n.value == entries_at + 2 * (-(-8 * packed // seg) + chunks)
+    bad = blob.copy()
+    bad[0] ^= 1
+    assert lib.aimg_index_nbytes(bad.ctypes.data, packed, chunks, ctypes.byref(n)) == \
+        _native.AIMG_ERR_BAD_TABLE
+    assert lib.aimg_index_nbytes(blob.ctypes.data, -1, chunks, ctypes.byref(n)) == \
+        _native.AIMG_ERR_INVALID_ARGUMENT
+    assert lib.aimg_index_nbytes(None, packed, chunks, ctypes.byref(n)) == \
+        _native.AIMG_ERR_INVALID_ARGUMENT
+
+
+def test_build_index_validates_before_launching():
+    lib = _native.lib()
+    arr = (_native.AimgTensor * 1)()
+    arr[0].chunk_size = 16
+    arr[0].n_chunks = 4
+    arr[0].n_symbols = 64
+    # No index: nothing to build, nothing launched.
+    assert lib.aimg_build_index(arr, 1, None) == _native.AIMG_OK
+    assert lib.aimg_build_index(arr, 33, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    arr[0].index = 4096
+    arr[0].index_nbytes = 64  # below the header and 5 chunk bases
+    assert lib.aimg_build_index(arr, 1, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    assert b"index_nbytes" in lib.aimg_last_error()
+    arr[0].index = 4100
+    arr[0].index_nbytes = 4096
+    assert lib.aimg_build_index(arr, 1, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    assert b"aligned" in lib.aimg_last_error()
+    arr[0].index = 4096  # the shared checks: null device pointers
+    assert lib.aimg_build_index(arr, 1, None) == _native.AIMG_ERR_INVALID_ARGUMENT
+    assert b"null" in lib.aimg_last_error()
