@@ -398,37 +398,14 @@ __device__ __forceinline__ void slot_put(uint8_t* q, uint32_t syms) {
     w[1] = static_cast<uint32_t>(v >> 32);
 }
 
-// Place the symbols of one lookup at q in a stage area that is zero where
-// nothing was placed, by OR into the word holding q and the word after it:
-// neighbouring segments share the words at their ends, so both are atomic.
-__device__ __forceinline__ void stage_or(uint8_t* q, uint32_t syms) {
-    const uint32_t b = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(q)) & 3u;
-    const uint64_t v = static_cast<uint64_t>(syms) << (8 * b);
-    uint32_t* w = reinterpret_cast<uint32_t*>(q - b);
-    __hip_atomic_fetch_or(w, static_cast<uint32_t>(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    __hip_atomic_fetch_or(w + 1, static_cast<uint32_t>(v >> 32), __ATOMIC_RELAXED,
-                          __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-template <bool kDirect>
-__device__ __forceinline__ void put(uint8_t* q, uint32_t syms) {
-    if (kDirect) {
-        stage_or(q, syms);
-    } else {
-        slot_put(q, syms);
-    }
-}
-
 // Parse codewords from true boundary p while they start before x, placing
-// their symbols from `slot` on. Returns the first boundary at or after x and
-// the number of codewords. Every codeword (or unused window) takes at least
-// min_len bits, so a segment of at most kSlotCap * min_len bits never holds
-// more than kSlotCap codewords, and every write stays within kSlotCap + 4
-// bytes of `slot`. The last lookup's symbols that start at or after x are
-// masked off before it is placed. kDirect: `slot` is the segment's place in
-// a zeroed stage area (stage_or); otherwise a private slot whose first word
-// is zero (slot_put).
-template <bool kGlobalEsc, bool kDirect>
+// their symbols in the slot (first word zero). Returns the first boundary at
+// or after x and the number of codewords. Every codeword (or unused window)
+// takes at least min_len bits, so a segment of at most kSlotCap * min_len
+// bits never holds more than kSlotCap codewords, and every write stays
+// inside the slot. The last lookup's symbols that start at or after x are
+// masked off before it is placed.
+template <bool kGlobalEsc>
 __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint32_t p,
                                           uint32_t x, uint8_t* slot) {
     if (p >= x) return {p, 0u};
@@ -442,7 +419,7 @@ __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint3
         // The next step's meta and pair go out before this step's symbols
         // are placed, its symbols after.
         Step t = lookup<false>(below, tb, pn, pn - s.m, s.next);
-        put<kDirect>(q, syms);
+        slot_put(q, syms);
         q += c;
         t.syms = tb.syms[t.idx];
         s = t;
@@ -451,8 +428,60 @@ __device__ __forceinline__ Adv decode_run(TileRef below, const Tables& tb, uint3
     }
     uint32_t kept;  // 1..4
     const uint32_t e = cut_window(tb, s.p, s.p + adv, syms, c, x, &kept);
-    put<kDirect>(q, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
+    slot_put(q, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
     return {e, static_cast<uint32_t>(q - slot) + kept};
+}
+
+__device__ __forceinline__ void lds_or(uint32_t* w, uint32_t v) {
+    __hip_atomic_fetch_or(w, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// OR one lookup's symbols (bytes of syms, zero above its count) into the
+// word holding q, together with `carry`, the bytes the previous lookup put
+// past its own word, which belong at the start of this word. Returns this
+// lookup's bytes past the word (zero unless it crosses into the next one),
+// the next call's carry.
+__device__ __forceinline__ uint32_t stage_or(uint8_t* q, uint32_t syms, uint32_t carry) {
+    const uint32_t b = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(q)) & 3u;
+    const uint64_t v = static_cast<uint64_t>(syms) << (8 * b);
+    lds_or(reinterpret_cast<uint32_t*>(q - b), static_cast<uint32_t>(v) | carry);
+    return static_cast<uint32_t>(v >> 32);
+}
+
+// Decode the segment from true boundary p while codewords start before x,
+// placing its symbols from q on in a stage area that is zero where nothing
+// is placed. Neighbouring segments share the words at their ends, so every
+// write is an atomic OR: one per lookup, a lookup's bytes that spill into
+// the next word going out with the next lookup's word, and the last spill
+// at the end. Dense placement puts the lanes of a wave at effectively
+// random LDS banks, so every write pays bank conflicts: on the 5120x17408
+// layer one write per lookup is 9% faster than two (the word and the word
+// after it), and as fast as the same writes to conflict-free addresses; a
+// byte-aligned 4-byte store per lookup with no atomics is 29% slower.
+template <bool kGlobalEsc>
+__device__ __forceinline__ void decode_placed(TileRef below, const Tables& tb, uint32_t p,
+                                              uint32_t x, uint8_t* q) {
+    if (p >= x) return;
+    const Reader rd = reader_at(below, p);
+    Step s = lookup<true>(below, tb, rd.p, rd.sh, rd.pair);
+    uint32_t syms, adv, c;
+    take<kGlobalEsc>(tb, s, &syms, &adv, &c);
+    uint32_t carry = 0;
+    uint32_t pn = s.p + adv;
+    while (pn < x) {
+        Step t = lookup<false>(below, tb, pn, pn - s.m, s.next);
+        carry = stage_or(q, syms, carry);
+        q += c;
+        t.syms = tb.syms[t.idx];
+        s = t;
+        take<kGlobalEsc>(tb, s, &syms, &adv, &c);
+        pn = s.p + adv;
+    }
+    uint32_t kept;
+    cut_window(tb, s.p, s.p + adv, syms, c, x, &kept);
+    const uint32_t spill = stage_or(q, syms & (0xFFFFFFFFu >> (32u - 8u * kept)), carry);
+    if (spill != 0u)
+        lds_or(reinterpret_cast<uint32_t*>((q - (reinterpret_cast<uintptr_t>(q) & 3u)) + 4), spill);
 }
 
 // Where to load the 4 bytes from packed-buffer byte A (A below the buffer
@@ -1326,9 +1355,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                     const uint32_t f = seg_lo + (ent & 15u);
                     uint8_t* dst = stage + lead + o;
                     if (global_esc) {
-                        decode_run<true, true>(below, tb, f, seg_hi, dst);
+                        decode_placed<true>(below, tb, f, seg_hi, dst);
                     } else {
-                        decode_run<false, true>(below, tb, f, seg_hi, dst);
+                        decode_placed<false>(below, tb, f, seg_hi, dst);
                     }
                 }
                 __syncthreads();  // the round is placed; the tile takes the next words
@@ -1398,10 +1427,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 Adv a;
                 if (global_esc) {
                     f = i == 0 ? p0 : advance<true>(below, tb, seg_lo - kOverlapBits, seg_lo);
-                    a = decode_run<true, false>(below, tb, f, seg_hi, slot);
+                    a = decode_run<true>(below, tb, f, seg_hi, slot);
                 } else {
                     f = i == 0 ? p0 : advance<false>(below, tb, seg_lo - kOverlapBits, seg_lo);
-                    a = decode_run<false, false>(below, tb, f, seg_hi, slot);
+                    a = decode_run<false>(below, tb, f, seg_hi, slot);
                 }
                 e = a.p;
                 cnt = a.n;
@@ -1430,8 +1459,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 if (bad) {
                     f = ep;
                     start_slot(slot);
-                    const Adv a = global_esc ? decode_run<true, false>(below, tb, f, seg_hi, slot)
-                                             : decode_run<false, false>(below, tb, f, seg_hi, slot);
+                    const Adv a = global_esc ? decode_run<true>(below, tb, f, seg_hi, slot)
+                                             : decode_run<false>(below, tb, f, seg_hi, slot);
                     e = a.p;
                     cnt = a.n;
                 }

@@ -231,6 +231,8 @@ def _bench_gemv(args) -> int:
     g = np.random.default_rng(23)
     x = torch.from_numpy(g.standard_normal((b, cols), dtype=np.float32)).to(torch.bfloat16).to(dev)
     t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, dev)
+    if not args.no_index:
+        t.build_index()  # the resident layer's segment index, built once
     y = torch.zeros((b, rows), dtype=torch.float32, device=dev)
 
     def step():
@@ -286,8 +288,10 @@ def _bench_gemv(args) -> int:
     enc = layer.encoded
     n = enc.n_symbols
     chunk_bytes = int(enc.chunk_nbytes.astype(np.int64).sum())
-    # bitstreams + offsets/lengths + sign/mantissa + table + x read + y read/write
-    algo_bytes = chunk_bytes + 8 * enc.n_chunks + n + (5 * 4096 + 256) + 2 * b * cols + 8 * b * rows
+    # bitstreams + offsets/lengths + sign/mantissa + table + x read + y
+    # read/write (+ the segment index read)
+    algo_bytes = (chunk_bytes + 8 * enc.n_chunks + n + (5 * 4096 + 256) + 2 * b * cols
+                  + 8 * b * rows + t.index_bytes_read)
     rec = {
         "metric": "fused decode->GEMV weight GB/s (bf16 bytes consumed per second)",
         "value": round(2 * n * args.steps / wall / 1e9, 2),
@@ -305,7 +309,8 @@ def _bench_gemv(args) -> int:
                                "outliers, %d-symbol chunks) x bf16 activation [%d, 17408] N(0,1) "
                                "(seed 23), fp32 accumulate -> bf16" % (enc.chunk_size, b),
                    "batch": b, "within_tolerance": ok, "tolerance": "rel 1e-2, abs 1e-3",
-                   "flops_per_step": 2 * n * b, "chunk_size": enc.chunk_size},
+                   "flops_per_step": 2 * n * b, "chunk_size": enc.chunk_size,
+                   "segment_index": t.index is not None},
         # The GEMV moves 2.5x fewer bytes than the decode but runs its decode
         # loop: its bound is the decode's symbol rate, measured here on the
         # same tensor with exponent-byte output (the decode's smallest output).
@@ -398,6 +403,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-index", action="store_true",
                     help="layer/block: time the decode without segment indexes only")
+    ap.add_argument("--index-only", action="store_true",
+                    help="layer/block: skip the launches without the index (for profiling)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="CPU-baseline threads (0: OpenMP's count, i.e. every CPU given)")
     ap.add_argument("--chunk-size", type=int, default=65536,
@@ -411,6 +418,9 @@ def main() -> int:
         print("bench.py measures one GPU only: this build has no multi-GPU decode path "
               "(chunks would shard by range with no exchange step). Run with --gpus 1.",
               file=sys.stderr)
+        return 2
+    if args.no_index and args.index_only:
+        print("--no-index and --index-only exclude each other", file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
@@ -489,12 +499,14 @@ def main() -> int:
     # Without segment indexes first (the path any caller gets), then, unless
     # --no-index, build each tensor's index once (a resident layer's load
     # step) and time the decode that uses it.
-    plain = descriptors()
-    launches(plain, max(1, args.warmup))
-    if not bit_exact():
-        print("decoded output (no index) differs from the original weights", file=sys.stderr)
-        return 1
-    no_index_s = launches(plain, min(args.steps, 100))
+    no_index_s = None
+    if not args.index_only:
+        plain = descriptors()
+        launches(plain, max(1, args.warmup))
+        if not bit_exact():
+            print("decoded output (no index) differs from the original weights", file=sys.stderr)
+            return 1
+        no_index_s = launches(plain, min(args.steps, 100))
     index_info = None
     if not args.no_index:
         for o in outs:
@@ -592,7 +604,7 @@ def main() -> int:
             "algorithmic_bytes_per_launch": algo_bytes,
             "kernel_us": round(kernel_s * 1e6, 2),
         },
-        "no_index": {
+        "no_index": None if no_index_s is None else {
             "kernel_us": round(no_index_s * 1e6, 2),
             "decompressed_gbs": round(2 * n / no_index_s / 1e9, 1),
             "achieved_gbs": round(algo_plain / no_index_s / 1e9, 1),
