@@ -37,6 +37,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -112,7 +113,6 @@ struct DevTensor {
     uint32_t packed_n32;  // packed_nbytes, capped at 2^32 - 1 (buffer loads)
     uint8_t* index;       // segment index, or null
     uint32_t index_n32;   // index bytes, capped at 2^32 - 1
-    uint32_t ix_entries;  // byte offset of the index entries
     int32_t n_chunks;
 };
 
@@ -527,11 +527,14 @@ struct Job {
     uint32_t lim;  // output symbols of the chunk
     uint32_t nr;   // rounds
     uint32_t ib;   // index entry of the chunk's first segment, or kNoIndex
+    uint32_t rend; // with the index: the chunk's real end in bits
 };
 
-// Whether tensor T's segment index is complete and was built for its
-// table: same segment length and table checksum (kModeIndex, which writes
-// the index, needs only the plan of the index built before it).
+// Index build: whether the plan step gave tensor T's index its chunk bases
+// and found room for every entry (entries are written only then). Decode:
+// whether the index is usable with T's table (built for it: segment length,
+// checksum; complete; laid out for this tensor). The same for every
+// sub-group of an item.
 template <int kMode>
 __device__ __forceinline__ bool index_usable(const DevTensor& T, uint32_t S) {
     const uint8_t* ix = uniform(T.index);
@@ -541,13 +544,15 @@ __device__ __forceinline__ bool index_usable(const DevTensor& T, uint32_t S) {
     if (kMode == kModeIndex) return true;
     return h->version == static_cast<uint32_t>(kAbiVersion) && h->seg_bits == S &&
            h->table_checksum == header_of(uniform(T.table))->checksum &&
-           h->n_chunks == static_cast<uint32_t>(T.n_chunks);
+           h->n_chunks == static_cast<uint32_t>(T.n_chunks) &&
+           h->n_jobs == static_cast<uint32_t>(T.n_jobs) &&
+           index_entries_at(T.n_chunks) <= T.index_n32;
 }
 
 // kLg > 0: every tensor of the launch has 1 << kLg threads per chunk.
 template <int kMode, uint32_t kLg>
 __device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, uint32_t tid) {
-    Job J{-1, 0u, kMaxSegBits, 0, 0u, 0u, 0u, 0u, kNoIndex};
+    Job J{-1, 0u, kMaxSegBits, 0, 0u, 0u, 0u, 0u, kNoIndex, 0u};
     if (item >= args.total_items) return J;
     int d = 0;
     while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
@@ -558,32 +563,35 @@ __device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, ui
     J.c = (item - T.item_begin) * n_groups + (tid >> J.lg);
     // Segment length: at most kSlotCap codewords of the shortest length.
     J.S = segment_bits(header_of(uniform(T.table))->min_len);
-    // The same for every sub-group of the item (a workgroup-wide choice).
     const bool use_ix = index_usable<kMode>(T, J.S);
+    const uint8_t* const ixp = use_ix ? uniform(T.index) : nullptr;
     const __attribute__((address_space(4))) uint32_t* ix_base =
-        use_ix ? (const __attribute__((address_space(4))) uint32_t*)(uniform(T.index) +
-                                                                       sizeof(IndexHeader))
-               : nullptr;
+        (const __attribute__((address_space(4))) uint32_t*)(ixp + sizeof(IndexHeader));
+    const __attribute__((address_space(4))) uint32_t* ix_rend =
+        (const __attribute__((address_space(4))) uint32_t*)(ixp + index_rend_at(T.n_chunks));
     // A wave holds 64 >> lg sub-groups (one when lg >= 6), on consecutive
     // chunks. Their offsets and lengths come through scalar loads, so no wait
     // for them waits for the vector stores in flight; each lane keeps its own.
     const int64_t c_wave = (item - T.item_begin) * n_groups + (uniform(tid & ~63u) >> J.lg);
     const uint32_t per_wave = J.lg >= 6 ? 1u : 64u >> J.lg;
     int64_t off = 0, nb = 0;
-    uint32_t ib = 0;
+    uint32_t ib = 0, re = 0;
 #pragma unroll
     for (uint32_t k = 0; k < 64 / kMinTpc; ++k) {
         if (k < per_wave && c_wave + k < T.n_jobs) {
             const int64_t o = load_uniform(T.offsets + c_wave + k);
             const int64_t n = load_uniform(T.nbytes + c_wave + k);
             const uint32_t b = use_ix ? ix_base[c_wave + k] : 0u;
+            const uint32_t e = use_ix && kMode != kModeIndex ? ix_rend[c_wave + k] : 0u;
             if (J.c == c_wave + k) {
                 off = o;
                 nb = n;
                 ib = b;
+                re = e;
             }
         }
     }
+    J.rend = re;
     // kNoIndex marks "no index" for the whole item, so no entry may equal it.
     J.ib = use_ix ? (ib < kNoIndex ? ib : kNoIndex - 1u) : kNoIndex;
     if (J.c < T.n_jobs) {
@@ -609,19 +617,20 @@ __device__ __forceinline__ uint32_t round_len(const Job& J, uint32_t r) {
 }
 
 // A thread's stream words of one round, in flight in registers until they
-// are written to the LDS tile: words k * tpc + i of the round; and, for a
-// chunk decoded with its segment index, the index entry of the thread's
-// segment of that round.
+// are written to the LDS tile: words k * tpc + i of the round.
 struct Fetch {
     uint32_t raw[kTileBatch];
-    uint32_t ent;
+    uint32_t ent;  // with the index: the entry of the thread's segment
 };
 
-// The index entries of tensor T as a buffer (reads past its end return 0,
-// writes past it are dropped).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t index_entries(const DevTensor& T) {
-    const uint32_t at = T.ix_entries < T.index_n32 ? T.ix_entries : T.index_n32;
-    return buffer_of(T.index + at, T.index_n32 - at);
+// The part of tensor T's index at [at, at + n) as a buffer (reads past it
+// return 0, writes past it are dropped).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t index_part(const DevTensor& T, uint64_t at,
+                                                             uint64_t n) {
+    const uint64_t lim = T.index_n32;
+    const uint64_t a = at < lim ? at : lim;
+    const uint64_t m = n < lim - a ? n : lim - a;
+    return buffer_of(T.index + a, static_cast<uint32_t>(m));
 }
 
 // Word 0 of sub-group g's tile (the tile is filled downwards, see Reader).
@@ -644,9 +653,11 @@ __device__ __forceinline__ void fetch_issue(Fetch& F, const LaunchArgs& args, co
     if (round_len(J, r) == 0) return;
     const DevTensor& T = args.t[J.d];
     const uint32_t tpc = 1u << J.lg;
-    if (kMode != kModeIndex && !kTiny && J.ib != kNoIndex)
-        F.ent = __builtin_amdgcn_raw_buffer_load_b16(
-            index_entries(T), 2u * (J.ib + r * tpc + (tid & (tpc - 1))), 0, 0);
+    if (kMode != kModeIndex && !kTiny && J.ib != kNoIndex) {
+        const uint64_t at = index_entries_at(T.n_chunks);
+        F.ent = __builtin_amdgcn_raw_buffer_load_b16(index_part(T, at, T.index_n32 - at),
+                                                     2u * (J.ib + r * tpc + (tid & (tpc - 1))), 0, 0);
+    }
     const uint32_t b0 = ((r * J.S) << J.lg) / 8 + 4 * (tid & (tpc - 1));
     // All words are requested before any is used; words past the chunk read
     // an in-buffer word and are zeroed when written.
@@ -778,10 +789,12 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
     return __uint_as_float(bits16 << 16);
 }
 
-// Output element el from its exponent e.
+// Output element el from its exponent e (elements past the tensor are
+// dropped).
 template <int kMode>
 __device__ __forceinline__ void store_one(const DevTensor& T, const GemvArgs& G, int64_t el,
                                           uint32_t e) {
+    if (el < 0 || el >= T.n_symbols) return;
     if (kMode == kModeU8) {
         static_cast<uint8_t*>(T.out)[el] = static_cast<uint8_t>(e);
     } else if (kMode == kModeBf16) {
@@ -932,7 +945,7 @@ __device__ __forceinline__ void step_rc(uint32_t& row, uint32_t& col, const Gemv
 template <int kMode, int kGroup, int kB>
 __device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch], const GemvArgs& G,
                                                  int nb, const uint8_t* stage, uint32_t a0,
-                                                 uint32_t nfull, uint32_t i) {
+                                                 uint32_t nfull, uint32_t i, uint32_t v_lo) {
     static_assert(kThreads * kGroup == 4096, "step_rows / step_cols are for 4096 elements");
     constexpr uint32_t kXAhead = kB == 1 ? 3 : 0;
     constexpr uint32_t kSpan = 64 * kGroup;  // elements a wave holds at one step
@@ -969,7 +982,7 @@ __device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch],
         if (k * kThreads + wave_first >= nfull) break;  // this wave's groups are done
         const uint4(&xc)[kB] = xq[k % (kXAhead + 1)];
         const uint32_t v = k * kThreads + i;
-        const uint32_t m = v < nfull ? 0xFFFFFFFFu : 0u;  // live group
+        const uint32_t m = v < nfull && v >= v_lo ? 0xFFFFFFFFu : 0u;  // live group
         const uint2 e = *reinterpret_cast<const uint2*>(stage + v * kGroup);
         uint4 w;
         w.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, e.x) & m;
@@ -1034,16 +1047,23 @@ __device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch],
 // thread i of a sub-group of tpc takes groups i, i + tpc, ... kWhole: the
 // sub-group is the whole workgroup, whose stage area is readable for every
 // group a store batch can name, so the staged reads need no clamping.
+// skip: group 0's first `skip` elements are another piece of work's (a
+// segment run that starts inside a vector group); group 0's other elements
+// are stored one by one, and the vector paths start at group 1.
 template <int kMode, int kGroup, bool kWhole>
 __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTensor& T,
                                             const GemvArgs& G, const uint8_t* stage, int64_t a0,
-                                            uint32_t nfull, uint32_t i, uint32_t tpc) {
+                                            uint32_t nfull, uint32_t i, uint32_t tpc,
+                                            uint32_t skip = 0) {
     if (kGroup == 1) {
         for (uint32_t v = i; v < nfull; v += tpc) store_one<kMode>(T, G, a0 + v, stage[v]);
         return;
     }
+    if (skip != 0 && nfull != 0 && i >= skip && i < static_cast<uint32_t>(kGroup))
+        store_one<kMode>(T, G, a0 + i, stage[i]);
+    const uint32_t v_lo = skip != 0 ? 1u : 0u;
     if (kMode == kModeU8) {
-        for (uint32_t v = i; v < nfull; v += tpc)
+        for (uint32_t v = i < v_lo ? i + tpc : i; v < nfull; v += tpc)
             // Non-temporal, like the bf16 stores (2.8% faster on the layer).
             __builtin_nontemporal_store(
                 *reinterpret_cast<const v4u32*>(stage + v * kGroup),
@@ -1095,7 +1115,7 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
 #pragma unroll
         for (uint32_t k = 0; k < kStoreBatch; ++k) {
             const uint32_t v = k * tpc + i;
-            if (v >= nfull) continue;
+            if (v >= nfull || v < v_lo) continue;
             v4u32 o4;
             o4[0] = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, ev[k].x);
             o4[1] = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, ev[k].x);
@@ -1108,7 +1128,7 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
     if constexpr (kWhole && (kMode == kModeGemv || kMode == kModeGemv1)) {
         constexpr int kB = kMode == kModeGemv1 ? 1 : kGemvMaxBatch;
         gemv_round_whole<kMode, kGroup, kB>(sm, G, kMode == kModeGemv1 ? 1 : G.batch, stage,
-                                            static_cast<uint32_t>(a0), nfull, i);
+                                            static_cast<uint32_t>(a0), nfull, i, v_lo);
         return;
     }
     // Fused GEMV: each group's 8 weights (one matrix row, as cols % 8 == 0)
@@ -1157,7 +1177,7 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
         }
         const uint4(&xc)[kB] = xq[k % (kXAhead + 1)];
         const uint32_t v = k * tpc + i;
-        const bool live = v < nfull;
+        const bool live = v < nfull && v >= v_lo;
         const uint64_t lm = __ballot(live);
         if (lm == 0) continue;
         // Staged exponents read here rather than all at once: registers.
@@ -1311,10 +1331,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         if (use_idx) {
             // Each segment's first boundary and codeword count come from the
             // index, so the round's placement is known before it decodes:
-            // each thread decodes from its true start and ORs its symbols
-            // straight into their place in the stage area, which is zero
-            // wherever nothing is placed. No look-ahead, agreement check or
-            // compaction.
+            // each thread decodes from its true start up to its segment's
+            // end or the chunk's real end, and ORs its symbols straight into
+            // their place in the stage area, which is zero wherever nothing
+            // is placed. No look-ahead, agreement check or compaction.
             for (uint32_t j = tid; j < kStageBytes / 16; j += kThreads)
                 reinterpret_cast<uint4*>(s_stage)[j] = make_uint4(0u, 0u, 0u, 0u);
             for (uint32_t r = 0; r < NR; ++r) {
@@ -1330,9 +1350,12 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 sm_issue<kMode, kGroup>(smb, T, chunk_base + ob - lead, i, tpc);
                 const uint32_t RB = round_len(cur, r);
                 const bool g_active = RB != 0;
+                // The round's bits up to the chunk's real end.
+                const uint32_t r_at = (r * S) << lg;
+                const uint32_t R_end = cur.rend > r_at ? (cur.rend - r_at < RB ? cur.rend - r_at : RB) : 0u;
                 const uint32_t seg_lo = i * S;
-                const bool active = seg_lo < RB;
-                const uint32_t seg_hi = active ? (seg_lo + S < RB ? seg_lo + S : RB) : 0u;
+                const bool active = seg_lo < R_end;
+                const uint32_t seg_hi = active ? (seg_lo + S < R_end ? seg_lo + S : R_end) : 0u;
                 // Counts above kSlotCap only come from a foreign index; the
                 // clamp keeps every placement inside the stage area.
                 const uint32_t ecnt = ent >> 4;
@@ -1346,7 +1369,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 const uint32_t gtot = s_gpre[g + 1] - s_gpre[g];
                 const int64_t still = lim - ob;
                 const uint32_t want =
-                    g_active ? (gtot < still ? gtot : static_cast<uint32_t>(still)) : 0u;
+                    g_active ? (gtot < still ? gtot : static_cast<uint32_t>(still > 0 ? still : 0)) : 0u;
                 const uint32_t avail = lead + want;
                 const uint32_t nfull = avail / kGroup;
                 const int64_t a0 = chunk_base + ob - lead;
@@ -1375,9 +1398,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                     k0 = src[0];
                     k1 = src[1];
                     const uint64_t a = static_cast<uint64_t>(k0.x) | static_cast<uint64_t>(k0.y) << 32;
-                    const uint64_t b = static_cast<uint64_t>(k1.x) | static_cast<uint64_t>(k1.y) << 32;
+                    const uint64_t bb = static_cast<uint64_t>(k1.x) | static_cast<uint64_t>(k1.y) << 32;
                     const uint64_t am = rem >= 8 ? a : a & ((uint64_t{1} << (8 * rem)) - 1);
-                    const uint64_t bm = rem <= 8 ? 0 : b & ((uint64_t{1} << (8 * (rem - 8))) - 1);
+                    const uint64_t bm = rem <= 8 ? 0 : bb & ((uint64_t{1} << (8 * (rem - 8))) - 1);
                     k0 = make_uint2(static_cast<uint32_t>(am), static_cast<uint32_t>(am >> 32));
                     k1 = make_uint2(static_cast<uint32_t>(bm), static_cast<uint32_t>(bm >> 32));
                 }
@@ -1470,10 +1493,12 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             if constexpr (kMode == kModeIndex) {
                 // Index build: each segment's first boundary (0..15 bits
                 // past its start) and codeword count; no output.
-                if (active && cur.ib != kNoIndex)
+                if (active && cur.ib != kNoIndex) {
+                    const IndexLayout L = index_layout(T.packed_nbytes, T.n_chunks, S);
                     __builtin_amdgcn_raw_buffer_store_b16(
-                        static_cast<uint16_t>((cnt << 4) | (f - seg_lo)), index_entries(T),
-                        2u * (cur.ib + r * tpc + i), 0, 0);
+                        static_cast<uint16_t>((cnt << 4) | (f - seg_lo)),
+                        index_part(T, L.entries, 2 * L.capacity), 2u * (cur.ib + r * tpc + i), 0, 0);
+                }
                 fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
                 __syncthreads();
                 if (g_active) p0 = s_glast[g] - RB;
@@ -1562,6 +1587,599 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     }
 }
 
+// ---------------------------------------------------------------------------
+// Segment index build (aimg_build_index): plan, entries, finish.
+// ---------------------------------------------------------------------------
+
+typedef const __attribute__((address_space(4))) uint32_t* ConstU32;
+
+// A chunk's byte range, clamped to the packed buffer as the decoders clamp it.
+__device__ __forceinline__ void chunk_range(const DevTensor& T, int64_t c, int64_t* off, int64_t* nb) {
+    int64_t o = T.offsets[c], n = T.nbytes[c];
+    o = o < 0 ? 0 : (o > T.packed_nbytes ? T.packed_nbytes : o);
+    n = n < 0 ? 0 : (n > T.packed_nbytes - o ? T.packed_nbytes - o : n);
+    *off = o;
+    *nb = n;
+}
+
+__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* s_wsum) {
+    const uint32_t x = wave_scan_incl(v);
+    if ((threadIdx.x & 63) == 63) s_wsum[threadIdx.x >> 6] = x;
+    __syncthreads();
+    uint32_t t = 0;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) t += s_wsum[k];
+    __syncthreads();
+    return t;
+}
+
+// Plan, one workgroup per tensor: chunk c (c < n_jobs) gets segments
+// base[c] .. base[c] + ceil(8 * nbytes / S) - 1, bchunk the chunk of every
+// 512th segment, and the header the segment length, the table's checksum,
+// and ok = 1 when the chunks lie back to back and the layout fits the index
+// (the entries step writes only then; the finish step may clear ok).
+__global__ __launch_bounds__(kThreads) void index_plan_kernel(const LaunchArgs args) {
+    __shared__ uint32_t s_wsum[kWaves];
+    __shared__ uint32_t s_bad;
+    const DevTensor& T = args.t[blockIdx.x];
+    uint8_t* const ix = T.index;
+    if (ix == nullptr) return;
+    const auto* th = header_of(T.table);
+    const uint32_t S = segment_bits(th->min_len);
+    const IndexLayout L = index_layout(T.packed_nbytes, T.n_chunks, S);
+    const bool fits = L.total <= T.index_n32 && L.capacity < kNoIndex;
+    if (threadIdx.x == 0) s_bad = fits ? 0u : 1u;
+    __syncthreads();
+    uint32_t* const base = reinterpret_cast<uint32_t*>(ix + L.base);
+    uint32_t* const bchunk = reinterpret_cast<uint32_t*>(ix + L.bchunk);
+    uint64_t run = 0;
+    for (int64_t c0 = 0; c0 < T.n_chunks; c0 += kThreads) {
+        const int64_t c = c0 + threadIdx.x;
+        uint32_t nseg = 0;
+        if (c < T.n_jobs) {
+            int64_t off, nb;
+            chunk_range(T, c, &off, &nb);
+            nseg = static_cast<uint32_t>((nb * 8 + S - 1) / S);
+            // Back to back: the next chunk starts where this one ends.
+            if (c + 1 < T.n_jobs && T.offsets[c + 1] != off + nb) s_bad = 1u;
+        }
+        const uint32_t excl = block_scan_excl(nseg, s_wsum);
+        uint32_t tot = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) tot += s_wsum[w];
+        const uint64_t at = run + excl;
+        if (fits && c < T.n_chunks) {
+            base[c] = static_cast<uint32_t>(at < kNoIndex ? at : kNoIndex - 1u);
+            // bchunk[m] = c for the 512-segment blocks that start in this chunk.
+            if (nseg != 0)
+                for (uint64_t m = (at + kIndexBlock - 1) / kIndexBlock;
+                     m * kIndexBlock < at + nseg && m < L.n_bchunk; ++m)
+                    bchunk[m] = static_cast<uint32_t>(c);
+        }
+        run += tot;
+        __syncthreads();  // s_wsum is written again by the next block's scan
+    }
+    if (threadIdx.x == 0) {
+        if (fits) base[T.n_chunks] = static_cast<uint32_t>(run < kNoIndex ? run : kNoIndex - 1u);
+        IndexHeader h{};
+        h.magic = kIndexMagic;
+        h.version = static_cast<uint32_t>(kAbiVersion);
+        h.seg_bits = S;
+        h.table_checksum = th->checksum;
+        h.ok = s_bad == 0u && run <= L.capacity ? 1u : 0u;
+        h.n_chunks = static_cast<uint32_t>(T.n_chunks);
+        h.n_segments = static_cast<uint32_t>(run < kNoIndex ? run : kNoIndex - 1u);
+        h.n_jobs = static_cast<uint32_t>(T.n_jobs);
+        *reinterpret_cast<IndexHeader*>(ix) = h;
+    }
+}
+
+// The first codeword at bit p of a chunk's bytes (zero past nb): its length.
+// The table blob is read from global memory (the finish step runs once).
+__device__ __forceinline__ uint32_t codeword_len_at(const uint8_t* table, const uint8_t* bytes,
+                                                    uint32_t nb, uint32_t p) {
+    uint32_t w = 0;
+    const uint32_t b0 = p >> 3;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) w = (w << 8) | (b0 + k < nb ? bytes[b0 + k] : 0u);
+    w <<= (p & 7u);  // bits p.. at the top
+    const auto* hdr = header_of(table);
+    const uint32_t idx = w >> (32 - kWinBits);
+    const uint8_t meta = table[kMetaOffset + idx];
+    const uint32_t ent = reinterpret_cast<const uint32_t*>(table + kSymsOffset)[idx];
+    const uint32_t min_len = hdr->min_len >= 1 ? hdr->min_len : 1u;
+    if (meta != 0) return table[kLenOffset + (ent & 0xFFu)];
+    const uint32_t blk = ent & 0xFFFFu;
+    if (blk == kUnusedBlock || blk >= hdr->n_esc_blocks) return min_len;
+    const uint16_t v = reinterpret_cast<const uint16_t*>(table + kEscOffset)[
+        blk * kEscBlockEntries + ((w >> (28 - kWinBits)) & 15u)];
+    return (v >> 8) ? (v >> 8) : min_len;
+}
+
+// Finish, one workgroup per chunk (c < n_jobs): the chunk's lim-th codeword
+// is found from the entries' counts; its end is the chunk's real end rend,
+// that segment keeps only the codewords up to it and later segments none.
+// A chunk with fewer than lim codewords, or whose lim-th codeword runs past
+// its bytes, makes the index unusable.
+__global__ __launch_bounds__(256) void index_finish_kernel(const LaunchArgs args, int64_t total) {
+    __shared__ uint32_t s_wsum[kWaves];
+    __shared__ uint32_t s_found;
+    for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+        int d = 0;
+        while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
+        const DevTensor& T = args.t[d];
+        const int64_t c = item - T.item_begin;
+        uint8_t* const ix = T.index;
+        const auto* h = reinterpret_cast<const IndexHeader*>(ix);
+        if (h->magic != kIndexMagic || h->ok != 1u) continue;
+        const uint32_t S = h->seg_bits;
+        const IndexLayout L = index_layout(T.packed_nbytes, T.n_chunks, S);
+        const uint32_t* base = reinterpret_cast<const uint32_t*>(ix + L.base);
+        uint32_t* rend = reinterpret_cast<uint32_t*>(ix + L.rend);
+        uint16_t* ent = reinterpret_cast<uint16_t*>(ix + L.entries);
+        const uint32_t b0 = base[c], b1 = base[c + 1];
+        int64_t off, nb;
+        chunk_range(T, c, &off, &nb);
+        int64_t lim = T.n_symbols - c * T.chunk_size;
+        lim = lim > T.chunk_size ? T.chunk_size : lim;
+        if (threadIdx.x == 0) s_found = 0;
+        uint32_t pre = 0;  // codewords of the chunk before this block of segments
+        for (uint32_t g0 = b0; g0 < b1; g0 += 256) {
+            const uint32_t g = g0 + threadIdx.x;
+            const uint32_t e = g < b1 ? ent[g] : 0u;
+            const uint32_t cnt = e >> 4;
+            // Block scan (256 threads: waves 0..3).
+            const uint32_t x = wave_scan_incl(cnt);
+            __syncthreads();
+            if ((threadIdx.x & 63) == 63) s_wsum[threadIdx.x >> 6] = x;
+            __syncthreads();
+            uint32_t before = 0, tot = 0;
+            for (uint32_t k = 0; k < 4; ++k) {
+                before += k < (threadIdx.x >> 6) ? s_wsum[k] : 0u;
+                tot += s_wsum[k];
+            }
+            const uint32_t excl = pre + before + x - cnt;  // codewords before segment g
+            if (g < b1) {
+                if (excl < static_cast<uint64_t>(lim) && excl + cnt >= static_cast<uint64_t>(lim)) {
+                    // The lim-th codeword is in this segment: walk to its end.
+                    const uint32_t keep = static_cast<uint32_t>(lim - excl);
+                    const uint32_t lo = (g - b0) * S;
+                    uint32_t p = lo + (e & 15u);
+                    for (uint32_t k = 0; k < keep; ++k)
+                        p += codeword_len_at(T.table, T.packed + off, static_cast<uint32_t>(nb), p);
+                    rend[c] = p;
+                    ent[g] = static_cast<uint16_t>((e & 15u) | (keep << 4));
+                    s_found = p <= 8 * nb ? 1u : 2u;
+                } else if (excl >= static_cast<uint64_t>(lim)) {
+                    ent[g] = static_cast<uint16_t>(e & 15u);  // past the real end
+                }
+            }
+            pre += tot;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0 && s_found != 1u) reinterpret_cast<IndexHeader*>(ix)->ok = 0u;
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Segment runs: decode of tensors that carry a usable segment index.
+//
+// The index makes every segment's start and output place known, and its
+// counts run on from chunk to chunk, so a tensor's segments form one
+// sequence that any workgroup can take a slice of: the launch's segments
+// (of every tensor it decodes this way) are split evenly over the grid,
+// whatever the chunk size, and a round is any 512 consecutive segments,
+// chunk boundaries included. Each thread decodes its segment from its true
+// start up to the segment's end or its chunk's real end, whichever comes
+// first, and ORs the symbols straight into place in the stage area.
+// ---------------------------------------------------------------------------
+
+// Chunks of at least this many symbols decode in segment runs when they have
+// a usable index: such chunks have at least 13 segments, so a round of 512
+// segments meets at most kRunChunks chunks.
+constexpr int32_t kRunMinChunk = 1024;
+constexpr uint32_t kRunChunks = 64;
+constexpr uint32_t kRunTileWords = kThreads * kMaxSegBits / 32 + kTileSlackWords;
+// The symbols of a round (at most kSlotCap per segment) after a carried
+// partial group, and every group a store batch names.
+constexpr uint32_t kRunStageBytes =
+    (kLeadBytes + kThreads * kSlotCap + 4 + 15) / 16 * 16 > kStoreBatch * kThreads * 8
+        ? (kLeadBytes + kThreads * kSlotCap + 4 + 15) / 16 * 16
+        : kStoreBatch * kThreads * 8;
+
+struct __attribute__((aligned(16))) RunLds {
+    uint8_t wmeta[kWinEntries];
+    uint8_t len[256];
+    uint16_t esc[kLdsEscBlocks * kEscBlockEntries];
+    uint32_t wsyms[kWinEntries];
+    uint32_t wsum[kWaves];
+    uint32_t wmax[kWaves];
+    // Chunks c0 .. c0 + kRunChunks - 1 of a round (c0: the chunk of its
+    // first segment): first segment, byte offset, real end in bits. Two
+    // sets, the current round's and the next one's.
+    uint32_t cbase[2][kRunChunks];
+    uint32_t coff[2][kRunChunks];
+    uint32_t crend[2][kRunChunks];
+    // mark[i] = j when segment g0 + i is chunk c0 + j's first (j >= 1).
+    uint8_t mark[2][kThreads];
+    uint32_t segs[AIMG_MAX_TENSORS];  // run_segments of each tensor of the launch
+    uint32_t tile[kRunTileWords];
+    __attribute__((aligned(16))) uint8_t stage[kRunStageBytes];
+};
+
+// Tensor T's segment count when its index is usable with its table: built
+// for this table (segment length, checksum), complete, and laid out for
+// this tensor. 0 otherwise. (Read by one thread per tensor.)
+__device__ __forceinline__ uint32_t run_segments(const DevTensor& T) {
+    const uint8_t* ix = T.index;
+    if (ix == nullptr) return 0u;
+    const auto* h = reinterpret_cast<const IndexHeader*>(ix);
+    const auto* th = reinterpret_cast<const TableHeader*>(T.table);
+    const uint32_t S = segment_bits(th->min_len);
+    if (h->magic != kIndexMagic || h->version != static_cast<uint32_t>(kAbiVersion) ||
+        h->ok != 1u || h->seg_bits != S || h->table_checksum != th->checksum ||
+        h->n_chunks != static_cast<uint32_t>(T.n_chunks) ||
+        h->n_jobs != static_cast<uint32_t>(T.n_jobs))
+        return 0u;
+    if (index_layout(T.packed_nbytes, T.n_chunks, S).total > T.index_n32) return 0u;
+    return h->n_segments;
+}
+
+// In flight for the next round: its stream words, each thread's index
+// entry, and (threads below kRunChunks) one chunk of its chunk table.
+struct RunFetch {
+    uint32_t raw[kTileBatch];
+    uint32_t ent;
+    uint32_t cb, co, cr;
+};
+
+struct RunPos {
+    uint32_t c0;   // chunk of the round's first segment
+    uint32_t g0;   // the round's first segment
+    uint32_t A0;   // byte of the packed buffer where its bits start
+};
+
+__device__ __forceinline__ void run_fetch_issue(RunFetch& F, const DevTensor& T,
+                                                const IndexLayout& L, const RunPos& P,
+                                                uint32_t s_hi, uint32_t tid) {
+    const __amdgpu_buffer_rsrc_t rs = buffer_of(T.packed, T.packed_n32);
+    const uint32_t last = last_word(T);
+#pragma unroll
+    for (uint32_t k = 0; k < kTileBatch; ++k) {
+        const uint32_t A = P.A0 + 4 * (k * kThreads + tid);
+        F.raw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, word_at(A, last), 0, 0);
+    }
+    const uint32_t g = P.g0 + tid;
+    F.ent = g < s_hi ? __builtin_amdgcn_raw_buffer_load_b16(
+                           index_part(T, L.entries, 2 * L.capacity), 2 * g, 0, 0)
+                     : 0u;
+    // Every wave loads the table (each lane one chunk, the same addresses in
+    // every wave), so each wave has the same loads in flight and the waits
+    // for them stay exact; the entries past the last chunk are replaced at
+    // the commit. Buffer loads throughout: a flat load would also count
+    // against the LDS wait counter, and the decode loop's first LDS wait
+    // would wait for it.
+    const uint32_t c = P.c0 + (tid & (kRunChunks - 1));
+    F.cb = __builtin_amdgcn_raw_buffer_load_b32(index_part(T, L.base, 4 * (T.n_chunks + 1)),
+                                                4 * c, 0, 0);
+    F.cr = __builtin_amdgcn_raw_buffer_load_b32(index_part(T, L.rend, 4 * T.n_chunks), 4 * c, 0, 0);
+    F.co = __builtin_amdgcn_raw_buffer_load_b32(
+        buffer_of(T.offsets, static_cast<uint32_t>(4 * T.n_chunks)), 4 * c, 0, 0);
+}
+
+// The fetched words into the tile (big-endian, bytes past the packed
+// buffer zero), and the chunk table and chunk-start marks of the round into
+// set `b`.
+__device__ __forceinline__ void run_fetch_commit(const RunFetch& F, const DevTensor& T,
+                                                 const RunPos& P, uint32_t tid, RunLds& lds,
+                                                 uint32_t b) {
+#pragma unroll
+    for (uint32_t k = 0; k < kTileBatch; ++k) consume(F.raw[k]);
+    consume(F.ent);
+    consume(F.cb);
+    consume(F.co);
+    consume(F.cr);
+    const uint32_t last = last_word(T);
+    uint32_t* const top = lds.tile + kRunTileWords - 1;
+#pragma unroll
+    for (uint32_t k = 0; k < kTileBatch; ++k) {
+        const uint32_t j = k * kThreads + tid;
+        if (j >= kRunTileWords) continue;
+        const uint32_t A = P.A0 + 4 * j;
+        uint32_t v = F.raw[k];
+        v >>= 8 * ((A - word_at(A, last)) & 3u);
+        *(top - j) = A < T.packed_n32 ? be_word(v, T.packed_n32 - A, 0) : 0u;
+    }
+    if (tid < kRunChunks) {
+        const bool real = P.c0 + tid < static_cast<uint32_t>(T.n_jobs);
+        const uint32_t cb = real ? F.cb : kNoIndex;
+        lds.cbase[b][tid] = cb;
+        lds.coff[b][tid] = F.co;
+        lds.crend[b][tid] = F.cr;
+        // Chunk c0 + tid starts inside the round: mark its first segment.
+        if (tid >= 1 && cb >= P.g0 && cb < P.g0 + kThreads)
+            lds.mark[b][cb - P.g0] = static_cast<uint8_t>(tid);
+    }
+}
+
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// Inclusive max over the workgroup of v (every thread), and the exclusive
+// sum of u, with one barrier.
+__device__ __forceinline__ void block_scan_sum_max(uint32_t u, uint32_t v, uint32_t* s_wsum,
+                                                   uint32_t* s_wmax, uint32_t* excl,
+                                                   uint32_t* vmax, uint32_t* sum_all) {
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const uint32_t x = wave_scan_incl(u);
+    uint32_t m = v;
+    m = umax(m, dpp<0x111>(m));
+    m = umax(m, dpp<0x112>(m));
+    m = umax(m, dpp<0x114>(m));
+    m = umax(m, dpp<0x118>(m));
+    m = umax(m, dpp<0x142, 0xA>(m));
+    m = umax(m, dpp<0x143, 0xC>(m));
+    if (lane == 63) {
+        s_wsum[w] = x;
+        s_wmax[w] = m;
+    }
+    __syncthreads();
+    uint32_t pre = 0, pm = 0, tot = 0;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) {
+        pre += k < w ? s_wsum[k] : 0u;
+        pm = k < w ? umax(pm, s_wmax[k]) : pm;
+        tot += s_wsum[k];
+    }
+    *excl = pre + x - u;
+    *vmax = umax(pm, m);
+    *sum_all = tot;
+}
+
+// Segments [s_lo, s_hi) of tensor T (usable index, table in LDS).
+template <int kMode, int kGroup>
+__device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const LaunchArgs& args,
+                          const DevTensor& T, uint32_t s_lo, uint32_t s_hi) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t S = segment_bits(tb.min_len);
+    const IndexLayout L = index_layout(T.packed_nbytes, T.n_chunks, S);
+    const uint8_t* const ix = uniform(T.index);
+    const ConstU32 base = (ConstU32)(ix + L.base);
+    const ConstU32 bchunk = (ConstU32)(ix + L.bchunk);
+    const uint32_t n_jobs = static_cast<uint32_t>(T.n_jobs);
+    // The chunk of segment s_lo.
+    uint32_t c0 = bchunk[s_lo / kIndexBlock];
+    c0 = c0 < n_jobs ? c0 : n_jobs - 1;
+    while (c0 + 1 < n_jobs && base[c0 + 1] <= s_lo) ++c0;
+    // Output element of the piece's first symbol: its chunk's first element
+    // plus the codewords of the chunk's segments before s_lo.
+    const uint32_t cb0 = base[c0];
+    uint32_t pre = 0;
+    {
+        const __amdgpu_buffer_rsrc_t re = index_part(T, L.entries, 2 * L.capacity);
+        for (uint32_t g = cb0 + tid; g < s_lo; g += kThreads)
+            pre += __builtin_amdgcn_raw_buffer_load_b16(re, 2 * g, 0, 0) >> 4;
+    }
+    pre = block_sum(pre, lds.wsum);
+    int64_t ob = static_cast<int64_t>(c0) * T.chunk_size + pre;  // next symbol's element
+    // The stage is zero wherever nothing is placed.
+    for (uint32_t j = tid; j < kRunStageBytes / 16; j += kThreads)
+        reinterpret_cast<uint4*>(lds.stage)[j] = make_uint4(0u, 0u, 0u, 0u);
+    for (uint32_t j = tid; j < 2 * kThreads; j += kThreads) (&lds.mark[0][0])[j] = 0;
+    __syncthreads();
+
+    RunPos P;
+    P.c0 = c0;
+    P.g0 = s_lo;
+    P.A0 = static_cast<uint32_t>(T.offsets[c0]) + (s_lo - cb0) * (S / 8);
+    RunFetch F;
+    run_fetch_issue(F, T, L, P, s_hi, tid);
+    run_fetch_commit(F, T, P, tid, lds, 0);
+    __syncthreads();
+
+    TileRef below = (TileRef)(lds.tile + kRunTileWords - 2);
+    asm volatile("" : "+v"(below));
+    uint8_t* const stage = lds.stage;
+    uint32_t lead = static_cast<uint32_t>(ob & (kGroup - 1));  // symbols staged before the round's
+    uint32_t skip = lead;  // of those, the ones another piece writes
+    uint32_t r = 0;
+    for (uint32_t g0 = s_lo; g0 < s_hi; g0 += kThreads, ++r) {
+        const uint32_t b = r & 1u;
+        const uint32_t ent = F.ent;
+        const uint32_t m = lds.mark[b][tid];
+        // The next round's first segment gn: its chunk is the last of the
+        // table's chunks that start at or before it (every wave counts them,
+        // one table entry a lane), so its words are requested before the
+        // round's scan, like the next round's of a chunk.
+        static_assert(kRunChunks == 64, "one table entry per lane of a wave");
+        const uint32_t lane = tid & 63u;
+        const uint32_t gn = g0 + kThreads;
+        const uint32_t jn = static_cast<uint32_t>(
+            __builtin_popcountll(__ballot(lane >= 1 && lds.cbase[b][lane] <= gn)));
+        RunPos N;
+        N.c0 = P.c0 + jn;
+        N.g0 = gn;
+        N.A0 = uniform(lds.coff[b][jn] + (gn - lds.cbase[b][jn]) * (S / 8));
+        __builtin_amdgcn_s_setprio(3);
+        if (gn < s_hi) run_fetch_issue(F, T, L, N, s_hi, tid);
+        const int64_t a0 = ob - lead;
+        SmBatch<kMode> smb;
+        sm_issue<kMode, kGroup>(smb, T, a0, tid, kThreads);
+        lds.mark[b][tid] = 0;
+        const uint32_t g = g0 + tid;
+        const bool active = g < s_hi;
+        const uint32_t ecnt = ent >> 4;
+        const uint32_t cnt = active ? (ecnt < kSlotCap ? ecnt : kSlotCap) : 0u;
+        __builtin_amdgcn_s_setprio(1);
+        uint32_t excl, jj, gtot;
+        block_scan_sum_max(cnt, m, lds.wsum, lds.wmax, &excl, &jj, &gtot);
+        jj = jj < kRunChunks ? jj : kRunChunks - 1;
+        const uint32_t avail = lead + gtot;
+        // Whole groups, never past the tensor's end (only an index that does
+        // not describe the tensor could place symbols there).
+        const int64_t room = (T.n_symbols - a0) / kGroup;
+        const uint32_t nfull = room < static_cast<int64_t>(avail / kGroup)
+                                   ? static_cast<uint32_t>(room > 0 ? room : 0)
+                                   : avail / kGroup;
+        // This thread's segment: chunk c0 + jj, segment g - base of it.
+        const uint32_t cbase = lds.cbase[b][jj];
+        const uint32_t coff = lds.coff[b][jj];
+        const uint32_t crend = lds.crend[b][jj];
+        const uint32_t B0 = 8 * P.A0;
+        const uint32_t at = 8 * coff + (g - cbase) * S;  // bit of the packed buffer
+        const uint32_t cend = 8 * coff + crend;
+        const uint32_t lo = at - B0;
+        const uint32_t hi = (at + S < cend ? at + S : cend) - B0;
+        __builtin_amdgcn_s_setprio(0);
+        if (active && at < cend) {
+            uint8_t* dst = stage + lead + excl;
+            if (global_esc) {
+                decode_placed<true>(below, tb, lo + (ent & 15u), hi, dst);
+            } else {
+                decode_placed<false>(below, tb, lo + (ent & 15u), hi, dst);
+            }
+        }
+        __syncthreads();  // the round is placed; the tile takes the next words
+        if (gn < s_hi) run_fetch_commit(F, T, N, tid, lds, b ^ 1u);
+        __builtin_amdgcn_s_setprio(2);
+        store_round<kMode, kGroup, true>(smb, T, args.gemv, stage, a0, nfull, tid, kThreads, skip);
+        if (nfull != 0) skip = 0;
+        ob += gtot;
+        // The partial vector group (rem < 16 bytes at a multiple of kGroup)
+        // moves to the front; all else placed is cleared.
+        const uint32_t rem0 = avail - nfull * kGroup;
+        const uint32_t rem = rem0 < static_cast<uint32_t>(kGroup) ? rem0 : kGroup - 1u;
+        uint2 k0 = make_uint2(0u, 0u), k1 = make_uint2(0u, 0u);
+        if (tid == 0 && rem != 0) {
+            const uint2* src = reinterpret_cast<const uint2*>(stage + nfull * kGroup);
+            k0 = src[0];
+            k1 = src[1];
+            const uint64_t a = static_cast<uint64_t>(k0.x) | static_cast<uint64_t>(k0.y) << 32;
+            const uint64_t bb = static_cast<uint64_t>(k1.x) | static_cast<uint64_t>(k1.y) << 32;
+            const uint64_t am = rem >= 8 ? a : a & ((uint64_t{1} << (8 * rem)) - 1);
+            const uint64_t bm = rem <= 8 ? 0 : bb & ((uint64_t{1} << (8 * (rem - 8))) - 1);
+            k0 = make_uint2(static_cast<uint32_t>(am), static_cast<uint32_t>(am >> 32));
+            k1 = make_uint2(static_cast<uint32_t>(bm), static_cast<uint32_t>(bm >> 32));
+        }
+        const uint32_t placed = (lead + gtot + 4 + 15) & ~15u;
+        const uint32_t zend = placed < kRunStageBytes ? placed : kRunStageBytes;
+        __syncthreads();
+        for (uint32_t z = 16 + 16 * tid; z < zend; z += 16 * kThreads)
+            *reinterpret_cast<uint4*>(stage + z) = make_uint4(0u, 0u, 0u, 0u);
+        if (tid == 0) {
+            reinterpret_cast<uint2*>(stage)[0] = k0;
+            reinterpret_cast<uint2*>(stage)[1] = k1;
+        }
+        lead = rem;
+        P = N;
+    }
+    // The symbols still staged (those of the piece's first group that
+    // another piece writes excepted).
+    __syncthreads();
+    if (tid >= skip && tid < lead) store_one<kMode>(T, args.gemv, ob - lead + tid, stage[tid]);
+    __syncthreads();
+}
+
+// Chunks [c_lo, c_hi) of tensor T whose index is not usable: one thread per
+// chunk decodes it whole, codeword by codeword, as the reference does (table
+// in LDS). Correct for any input, slow; decoders take this path only when a
+// caller passes an index that does not match the tensor's table.
+template <int kMode>
+__device__ void run_fallback(const Tables& tb, const LaunchArgs& args, const DevTensor& T,
+                             int64_t c_lo, int64_t c_hi) {
+    for (int64_t c = c_lo + threadIdx.x; c < c_hi; c += kThreads) {
+        int64_t off, nb;
+        chunk_range(T, c, &off, &nb);
+        const uint8_t* bytes = T.packed + off;
+        int64_t lim = T.n_symbols - c * T.chunk_size;
+        lim = lim > T.chunk_size ? T.chunk_size : lim;
+        uint64_t p = 0;
+        for (int64_t k = 0; k < lim; ++k) {
+            uint32_t w = 0;
+            const uint64_t b0 = p >> 3;
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j)
+                w = (w << 8) | (b0 + j < static_cast<uint64_t>(nb) ? bytes[b0 + j] : 0u);
+            w <<= (p & 7u);
+            const uint32_t idx = w >> (32 - kWinBits);
+            uint32_t sym, len;
+            if (tb.meta[idx] != 0) {
+                sym = tb.syms[idx] & 0xFFu;
+                len = tb.len[sym];
+            } else {
+                sym = escape<true>(tb, tb.syms[idx], w, &len);
+            }
+            store_one<kMode>(T, args.gemv, c * T.chunk_size + k, sym);
+            p += len;
+        }
+    }
+}
+
+template <int kMode, int kGroup>
+__global__ __launch_bounds__(kThreads, kWavesPerSimd) void run_kernel(const LaunchArgs args) {
+    __shared__ RunLds lds;
+    const uint32_t tid = threadIdx.x;
+    Tables tb;
+    tb.syms = lds.wsyms;
+    tb.meta = lds.wmeta;
+    tb.len = lds.len;
+    tb.esc = lds.esc;
+    const uint8_t* loaded = nullptr;
+    // The launch's work in rounds (512 consecutive segments of one tensor),
+    // whole rounds to each workgroup: the first `extra` workgroups take one
+    // more. (Workgroups b and b + 256 share a CU, so no CU takes two extra
+    // rounds while another takes none; an even split of segments instead
+    // gives every workgroup a last, mostly empty round.)
+    if (tid < static_cast<uint32_t>(args.n_tensors)) lds.segs[tid] = run_segments(args.t[tid]);
+    __syncthreads();
+    uint64_t units = 0;
+    for (int d = 0; d < args.n_tensors; ++d)
+        units += (static_cast<uint64_t>(lds.segs[d]) + kThreads - 1) / kThreads;
+    const uint64_t per = units / gridDim.x, extra = units % gridDim.x;
+    const uint64_t lo = blockIdx.x * per + (blockIdx.x < extra ? blockIdx.x : extra);
+    const uint64_t hi = lo + per + (blockIdx.x < extra ? 1 : 0);
+    uint64_t at = 0;  // rounds of the tensors before d
+    for (int d = 0; d < args.n_tensors; ++d) {
+        const DevTensor& T = args.t[d];
+        const uint32_t G = uniform(lds.segs[d]);
+        const uint64_t U = (static_cast<uint64_t>(G) + kThreads - 1) / kThreads;
+        const uint64_t ua = lo > at ? lo : at;
+        const uint64_t ub = hi < at + U ? hi : at + U;
+        // Segments of this tensor's rounds [ua - at, ub - at).
+        const uint64_t a = (ua - at) * kThreads;
+        const uint64_t b0 = (ub - at) * kThreads;
+        const uint64_t b = ua < ub ? (b0 < G ? b0 : G) : a;
+        // Tensors without a usable index: an even share of their chunks.
+        const int64_t c_lo = G != 0 ? 0 : T.n_jobs * static_cast<int64_t>(blockIdx.x) / gridDim.x;
+        const int64_t c_hi = G != 0 ? 0 : T.n_jobs * static_cast<int64_t>(blockIdx.x + 1) / gridDim.x;
+        const bool work = G != 0 ? a < b : c_lo < c_hi;
+        if (!work) {
+            at += U;
+            continue;
+        }
+        const uint8_t* const table = uniform(T.table);
+        const auto* hdr = header_of(table);
+        tb.sym0 = hdr->sym0;
+        tb.min_len = hdr->min_len >= 1 ? hdr->min_len : 1u;
+        tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(table + kEscOffset);
+        const bool global_esc = hdr->n_esc_blocks > static_cast<uint32_t>(kLdsEscBlocks);
+        if (table != loaded) {
+            __syncthreads();  // every thread is done with the previous table
+            loaded = table;
+            load_table(table, tid, lds.wsyms, lds.wmeta, lds.len, lds.esc);
+            __syncthreads();
+        }
+        if (G != 0 && a < b) {
+            run_piece<kMode, kGroup>(lds, tb, global_esc, args, T, static_cast<uint32_t>(a),
+                                     static_cast<uint32_t>(b));
+        } else if (G == 0 && c_lo < c_hi) {
+            run_fallback<kMode>(tb, args, T, c_lo, c_hi);
+        }
+        at += U;
+    }
+}
+
 int cu_count() {
     static std::once_flag once;
     static int n = 0;
@@ -1627,8 +2245,35 @@ int launch_batch(Batch& B, hipStream_t s, bool tiny) {
 }
 
 // Validate tensor i and add it to the normal or the tiny-buffer batch.
+// The segment-run kernel over the batch's tensors: a full grid, whose
+// workgroups split the tensors' segments evenly among themselves.
 template <int kMode>
-int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny) {
+int launch_run(Batch& B, hipStream_t s) {
+    if (B.m == 0) return AIMG_OK;
+    B.args.n_tensors = B.m;
+    B.args.total_items = 0;
+    int64_t bits = 0;
+    for (int d = 0; d < B.m; ++d) bits += 8 * B.args.t[d].packed_nbytes;
+    // About 4 rounds of 512 segments per workgroup at least; a full grid for
+    // anything larger.
+    const int64_t slots = static_cast<int64_t>(cu_count()) * kBlocksPerCu;
+    const int64_t want = bits / (4 * static_cast<int64_t>(kThreads) * kMaxSegBits) + 1;
+    const dim3 gdim(static_cast<uint32_t>(want < slots ? want : slots)), bdim(kThreads);
+    constexpr int kVecGroup = kMode == kModeU8 ? 16 : 8;
+    hipLaunchKernelGGL((run_kernel<kMode, kVecGroup>), gdim, bdim, 0, s, B.args);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+        return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    return AIMG_OK;
+}
+
+// Tensors with a segment index (chunks of kRunMinChunk symbols or more, the
+// vector path's alignment) go to `run`, the segment-run kernel, when their
+// chunks take fewer than kThreads threads or `big_runs` says so; the others
+// decode chunk by chunk (with their index, when it is usable).
+template <int kMode>
+int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny, Batch* run = nullptr,
+               bool big_runs = false) {
     const std::string who = "tensor " + std::to_string(i) + ": ";
     if (t.chunk_size < 1) return fail(AIMG_ERR_INVALID_ARGUMENT, who + "chunk_size must be >= 1");
     if (t.n_chunks < 0 || t.n_symbols < 0 || t.packed_nbytes < 0)
@@ -1646,11 +2291,18 @@ int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny) {
         return fail(AIMG_ERR_INVALID_ARGUMENT, who + "null device pointer");
     if (reinterpret_cast<uintptr_t>(t.table) % 16 != 0)
         return fail(AIMG_ERR_INVALID_ARGUMENT, who + "table must be 16-byte aligned");
-    Batch& B = t.packed_nbytes < 4 ? tiny : normal;
     const int group = kMode == kModeU8 ? 16 : 8;
-    if ((need_out && reinterpret_cast<uintptr_t>(t.out) % 16 != 0) || t.chunk_size % group != 0 ||
-        (need_sm && reinterpret_cast<uintptr_t>(t.sign_mantissa) % 8 != 0))
-        B.vec = false;
+    const bool vec_layout = !((need_out && reinterpret_cast<uintptr_t>(t.out) % 16 != 0) ||
+                              t.chunk_size % group != 0 ||
+                              (need_sm && reinterpret_cast<uintptr_t>(t.sign_mantissa) % 8 != 0));
+    // An index smaller than its header, or misaligned, is not one.
+    const bool has_index = t.index != nullptr && t.index_nbytes >= static_cast<int64_t>(sizeof(IndexHeader)) &&
+                           reinterpret_cast<uintptr_t>(t.index) % 16 == 0;
+    const bool to_run = run != nullptr && has_index && t.chunk_size >= kRunMinChunk &&
+                        t.packed_nbytes >= 4 && vec_layout &&
+                        (threads_per_chunk(t.chunk_size) < static_cast<uint32_t>(kThreads) || big_runs);
+    Batch& B = to_run ? *run : (t.packed_nbytes < 4 ? tiny : normal);
+    if (!vec_layout) B.vec = false;
     DevTensor& dt = B.args.t[B.m++];
     dt.packed = t.packed;
     dt.offsets = t.chunk_offsets;
@@ -1664,17 +2316,10 @@ int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny) {
     dt.n_symbols = t.n_symbols;
     dt.chunk_size = t.chunk_size;
     dt.n_chunks = t.n_chunks;
-    // An index too small for its header and chunk bases, or misaligned, is
-    // not one (the decoders ignore it; aimg_build_index refuses it).
-    const size_t ix_at = index_entries_offset(t.n_chunks);
-    const bool ix_ok = t.index != nullptr && t.index_nbytes >= static_cast<int64_t>(ix_at) &&
-                       reinterpret_cast<uintptr_t>(t.index) % 16 == 0;
-    dt.index = ix_ok ? static_cast<uint8_t*>(t.index) : nullptr;
-    dt.index_n32 = !ix_ok ? 0u
+    dt.index = has_index ? static_cast<uint8_t*>(t.index) : nullptr;
+    dt.index_n32 = !has_index ? 0u
                    : t.index_nbytes > static_cast<int64_t>(UINT32_MAX) ? UINT32_MAX
                    : static_cast<uint32_t>(t.index_nbytes);
-    dt.ix_entries = ix_ok && ix_at < UINT32_MAX ? static_cast<uint32_t>(ix_at) : 0u;
-    if (ix_ok && ix_at >= UINT32_MAX) dt.index = nullptr;
     dt.tpc = static_cast<int32_t>(threads_per_chunk(t.chunk_size));
     if (dt.tpc != kThreads) B.full = false;
     // Chunks past the last output element hold nothing to write.
@@ -1692,65 +2337,43 @@ int launch(const aimg_tensor* ts, int n, const GemvArgs& gemv, bool vec_ok, void
     if (n < 0 || n > AIMG_MAX_TENSORS)
         return fail(AIMG_ERR_INVALID_ARGUMENT,
                     "n_tensors must be in 0.." + std::to_string(AIMG_MAX_TENSORS));
-    Batch normal, tiny;
+    Batch normal, tiny, run;
     normal.args.gemv = gemv;
     tiny.args.gemv = gemv;
+    run.args.gemv = gemv;
     normal.vec = vec_ok;
+    // Chunks of a whole workgroup (kThreads threads) decode chunk by chunk,
+    // with their index, unless there are too few of them to spread evenly
+    // over the grid: with fewer than 4 per workgroup slot, some CUs get one
+    // chunk more than others (1360 chunks on 512 slots: 6 on some CUs, 5 on
+    // the rest), and segment runs, which split the work in rounds, are
+    // faster despite their dearer rounds (measured: 3.7% on a 1360-chunk
+    // layer; 7.5% slower on a 5042-chunk block).
+    // AIMG_SEGMENT_RUNS=1 sends every tensor with an index (that can) to the
+    // segment runs, =0 none; otherwise the choice above (tests and
+    // benchmarks use it to time and check each path).
+    const char* force = std::getenv("AIMG_SEGMENT_RUNS");
+    const int runs_mode = force == nullptr ? -1 : force[0] == '1' ? 1 : force[0] == '0' ? 0 : -1;
+    int64_t big_chunks = 0;
     for (int i = 0; i < n; ++i) {
-        const int rc = add_tensor<kMode>(ts[i], i, normal, tiny);
+        const aimg_tensor& t = ts[i];
+        if (t.index != nullptr && t.chunk_size > 0 && t.n_symbols > 0 &&
+            threads_per_chunk(t.chunk_size) == static_cast<uint32_t>(kThreads))
+            big_chunks += (t.n_symbols + t.chunk_size - 1) / t.chunk_size;
+    }
+    const bool big_runs = runs_mode == 1 ||
+                          big_chunks < 4 * static_cast<int64_t>(cu_count()) * kBlocksPerCu;
+    Batch* const to_run = vec_ok && runs_mode != 0 ? &run : nullptr;
+    for (int i = 0; i < n; ++i) {
+        const int rc = add_tensor<kMode>(ts[i], i, normal, tiny, to_run, big_runs);
         if (rc != AIMG_OK) return rc;
     }
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const int rc = launch_batch<kMode>(normal, s, false);
+    int rc = launch_run<kMode>(run, s);
+    if (rc != AIMG_OK) return rc;
+    rc = launch_batch<kMode>(normal, s, false);
     if (rc != AIMG_OK) return rc;
     return launch_batch<kMode>(tiny, s, true);
-}
-
-// First step of an index build, one workgroup per tensor: chunk c's
-// segments (ceil(8 * nbytes / S), for the chunk's bytes clamped to the
-// packed buffer as the decode kernels clamp them) get entries base[c] ..
-// base[c + 1] - 1, and the header records the segment length, the table's
-// checksum and whether every entry fits the index.
-__global__ __launch_bounds__(kThreads) void index_plan_kernel(const LaunchArgs args) {
-    __shared__ uint32_t s_wsum[kWaves];
-    const DevTensor& T = args.t[blockIdx.x];
-    uint8_t* const ix = T.index;
-    if (ix == nullptr) return;
-    const auto* th = header_of(T.table);
-    const uint32_t S = segment_bits(th->min_len);
-    uint32_t* const base = reinterpret_cast<uint32_t*>(ix + sizeof(IndexHeader));
-    const uint64_t cap = T.ix_entries < T.index_n32 ? (T.index_n32 - T.ix_entries) / 2 : 0;
-    uint64_t run = 0;
-    for (int64_t c0 = 0; c0 < T.n_chunks; c0 += kThreads) {
-        const int64_t c = c0 + threadIdx.x;
-        uint32_t nseg = 0;
-        if (c < T.n_jobs) {
-            int64_t off = T.offsets[c], nb = T.nbytes[c];
-            off = off < 0 ? 0 : (off > T.packed_nbytes ? T.packed_nbytes : off);
-            nb = nb < 0 ? 0 : (nb > T.packed_nbytes - off ? T.packed_nbytes - off : nb);
-            nseg = static_cast<uint32_t>((nb * 8 + S - 1) / S);
-        }
-        const uint32_t excl = block_scan_excl(nseg, s_wsum);
-        uint32_t tot = 0;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) tot += s_wsum[w];
-        const uint64_t at = run + excl;
-        if (c < T.n_chunks) base[c] = at < kNoIndex ? static_cast<uint32_t>(at) : kNoIndex - 1u;
-        run += tot;
-        __syncthreads();  // s_wsum is written again by the next block's scan
-    }
-    if (threadIdx.x == 0) {
-        base[T.n_chunks] = run < kNoIndex ? static_cast<uint32_t>(run) : kNoIndex - 1u;
-        IndexHeader h{};
-        h.magic = kIndexMagic;
-        h.version = static_cast<uint32_t>(kAbiVersion);
-        h.seg_bits = S;
-        h.table_checksum = th->checksum;
-        h.ok = run <= cap ? 1u : 0u;
-        h.n_chunks = static_cast<uint32_t>(T.n_chunks);
-        h.capacity = static_cast<uint32_t>(cap < kNoIndex ? cap : kNoIndex - 1u);
-        *reinterpret_cast<IndexHeader*>(ix) = h;
-    }
 }
 
 // Recombine of already-decoded exponents: out[i] = bf16 bits of (sm[i], e[i]).
@@ -1819,16 +2442,16 @@ extern "C" int aimg_build_index(const aimg_tensor* tensors, int n_tensors, void*
     if (n_tensors < 0 || n_tensors > AIMG_MAX_TENSORS)
         return fail(AIMG_ERR_INVALID_ARGUMENT,
                     "n_tensors must be in 0.." + std::to_string(AIMG_MAX_TENSORS));
-    // Tensors that have an index; each must be able to hold its header and
-    // chunk bases. Tensors with no symbols have nothing to index.
+    // Tensors that have an index; each must hold at least its header.
+    // Tensors with no symbols have nothing to index.
     aimg::Batch normal, tiny;
     aimg::LaunchArgs plan{};
     int n_plan = 0;
+    int64_t chunks = 0;
     for (int i = 0; i < n_tensors; ++i) {
         const aimg_tensor& t = tensors[i];
         if (t.index == nullptr) continue;
-        if (t.n_chunks < 0 ||
-            t.index_nbytes < static_cast<int64_t>(aimg::index_entries_offset(t.n_chunks)))
+        if (t.index_nbytes < static_cast<int64_t>(sizeof(aimg::IndexHeader)))
             return fail(AIMG_ERR_INVALID_ARGUMENT, "tensor " + std::to_string(i) +
                                                        ": index_nbytes is below aimg_index_nbytes");
         if (reinterpret_cast<uintptr_t>(t.index) % 16 != 0)
@@ -1837,21 +2460,34 @@ extern "C" int aimg_build_index(const aimg_tensor* tensors, int n_tensors, void*
         const int n0 = normal.m, t0 = tiny.m;
         const int rc = aimg::add_tensor<aimg::kModeIndex>(t, i, normal, tiny);
         if (rc != AIMG_OK) return rc;
-        if (normal.m > n0) plan.t[n_plan++] = normal.args.t[normal.m - 1];
-        if (tiny.m > t0) plan.t[n_plan++] = tiny.args.t[tiny.m - 1];
+        aimg::DevTensor* dt = normal.m > n0 ? &normal.args.t[normal.m - 1]
+                              : tiny.m > t0 ? &tiny.args.t[tiny.m - 1] : nullptr;
+        if (dt == nullptr) continue;
+        plan.t[n_plan] = *dt;
+        plan.t[n_plan].item_begin = chunks;  // the finish step's chunk numbering
+        chunks += dt->n_jobs;
+        ++n_plan;
     }
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (n_plan > 0) {
-        plan.n_tensors = n_plan;
-        hipLaunchKernelGGL(aimg::index_plan_kernel, dim3(static_cast<uint32_t>(n_plan)),
-                           dim3(aimg::kThreads), 0, s, plan);
-        const hipError_t err = hipGetLastError();
-        if (err != hipSuccess)
-            return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
-    }
-    const int rc = aimg::launch_batch<aimg::kModeIndex>(normal, s, false);
+    if (n_plan == 0) return AIMG_OK;
+    plan.n_tensors = n_plan;
+    hipLaunchKernelGGL(aimg::index_plan_kernel, dim3(static_cast<uint32_t>(n_plan)),
+                       dim3(aimg::kThreads), 0, s, plan);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+        return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    int rc = aimg::launch_batch<aimg::kModeIndex>(normal, s, false);
     if (rc != AIMG_OK) return rc;
-    return aimg::launch_batch<aimg::kModeIndex>(tiny, s, true);
+    rc = aimg::launch_batch<aimg::kModeIndex>(tiny, s, true);
+    if (rc != AIMG_OK) return rc;
+    const int64_t slots = static_cast<int64_t>(aimg::cu_count()) * 8;
+    hipLaunchKernelGGL(aimg::index_finish_kernel,
+                       dim3(static_cast<uint32_t>(chunks < slots ? chunks : slots)), dim3(256), 0, s,
+                       plan, chunks);
+    err = hipGetLastError();
+    if (err != hipSuccess)
+        return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    return AIMG_OK;
 }
 
 extern "C" int aimg_decode_bf16(const aimg_tensor* tensors, int n_tensors, void* stream) {

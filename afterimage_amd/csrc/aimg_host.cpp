@@ -181,13 +181,11 @@ extern "C" int aimg_index_nbytes(const void* host_table, int64_t packed_nbytes, 
     if (hdr.magic != aimg::kTableMagic || hdr.version != static_cast<uint32_t>(aimg::kAbiVersion))
         return fail(AIMG_ERR_BAD_TABLE, "table blob has a wrong magic or version "
                                         "(build it with aimg_build_table)");
-    // Chunks laid out back to back have ceil(8 * nbytes / S) segments each,
-    // at most 8 * packed_nbytes / S + 1 together per chunk.
-    const int64_t seg = aimg::segment_bits(hdr.min_len);
-    const int64_t entries = (packed_nbytes * 8 + seg - 1) / seg + n_chunks;
-    if (entries > static_cast<int64_t>(UINT32_MAX))
-        return fail(AIMG_ERR_UNSUPPORTED, "index of more than 2^32 - 1 segments");
-    *nbytes = aimg::index_entries_offset(n_chunks) + 2 * static_cast<size_t>(entries);
+    const aimg::IndexLayout l =
+        aimg::index_layout(packed_nbytes, n_chunks, aimg::segment_bits(hdr.min_len));
+    if (l.capacity >= UINT32_MAX)
+        return fail(AIMG_ERR_UNSUPPORTED, "index of 2^32 - 1 or more segments");
+    *nbytes = static_cast<size_t>(l.total);
     return AIMG_OK;
 }
 

@@ -58,17 +58,26 @@ inline size_t table_nbytes() {
     return kEscOffset + sizeof(uint16_t) * kEscBlockEntries * kMaxEscBlocks;
 }
 
-// Segment index of one tensor (aimg_build_index): for every segment of
-// seg_bits bits of every chunk (segment k of chunk c covers chunk bits
-// [k * seg_bits, (k + 1) * seg_bits)), the first codeword boundary at or
-// after the segment start, as an offset 0..15 from it, and the number of
-// codewords that start inside the segment, in one uint16:
-//   offset | count << 4.
-// Layout: the header, uint32 base[n_chunks + 1] (entry of segment 0 of
-// chunk c; base[n_chunks] = entries used), then uint16 entries[capacity].
-// seg_bits and the table checksum tie the index to the table it was built
-// with; ok is 1 when every chunk's entries fit the capacity.
-constexpr uint32_t kIndexMagic = 0x58444941u;  // "AIDX"
+// Segment index of one tensor (aimg_build_index). Segment k of chunk c
+// covers chunk bits [k * seg_bits, (k + 1) * seg_bits); the chunk's
+// segments are numbered base[c] .. base[c + 1] - 1 in one sequence over the
+// tensor (its chunks that hold output elements, n_jobs of them). For each,
+// one uint16 entry:
+//   offset | count << 4
+// offset: the first codeword boundary at or after the segment start, 0..15
+// bits past it; count: the codewords that start inside the segment and
+// before the chunk's real end rend[c], the end of its lim-th codeword (lim:
+// the chunk's output elements). Codewords past rend[c] (the zero bits that
+// pad a chunk to whole bytes) are not counted, so a chunk's counts add up
+// to lim and the tensor's symbols run on from chunk to chunk.
+// Layout (index_layout): the header, uint32 base[n_chunks + 1] (entries
+// past n_jobs repeat the total), uint32 rend[n_chunks], uint16
+// entries[capacity], and uint32 bchunk[n_bchunk]: the chunk of segment
+// 512 * m. The index is usable (ok == 1) only when the chunks lie back to
+// back in the packed buffer, every chunk holds its lim codewords within its
+// bytes, and everything fits; seg_bits and the table checksum tie it to
+// the table it was built with.
+constexpr uint32_t kIndexMagic = 0x32444941u;  // "AID2"
 
 struct IndexHeader {
     uint32_t magic;
@@ -77,15 +86,47 @@ struct IndexHeader {
     uint32_t table_checksum;
     uint32_t ok;
     uint32_t n_chunks;
-    uint32_t capacity;  // entries
-    uint32_t reserved[9];
+    uint32_t n_segments;  // base[n_jobs]: the tensor's segments
+    uint32_t n_jobs;
+    uint32_t reserved[8];
 };
 static_assert(sizeof(IndexHeader) == 64, "index header is 64 bytes");
 
-// Offset of the entries of an index over n_chunks chunks (16-byte aligned).
-constexpr size_t index_entries_offset(int64_t n_chunks) {
-    return (sizeof(IndexHeader) + sizeof(uint32_t) * static_cast<size_t>(n_chunks + 1) + 15) &
-           ~static_cast<size_t>(15);
+struct IndexLayout {
+    uint64_t base, rend, entries, bchunk, total;
+    uint64_t capacity, n_bchunk;
+};
+
+// Segments one bchunk entry spans (one round of a whole workgroup).
+constexpr uint32_t kIndexBlock = 512;
+
+// Byte offsets of the real ends and the entries of an index over n_chunks
+// chunks (they do not depend on the segment count).
+constexpr uint64_t index_rend_at(int64_t n_chunks) {
+    return sizeof(IndexHeader) + 4 * static_cast<uint64_t>(n_chunks > 0 ? n_chunks + 1 : 1);
+}
+constexpr uint64_t index_entries_at(int64_t n_chunks) {
+    return (index_rend_at(n_chunks) + 4 * static_cast<uint64_t>(n_chunks > 0 ? n_chunks : 0) + 15) &
+           ~uint64_t{15};
+}
+
+// Byte offsets of an index's arrays for a tensor of packed_nbytes packed
+// bytes in n_chunks chunks and segments of seg_bits: room for the segments
+// of chunks that lie back to back, ceil(8 * packed_nbytes / seg_bits) plus
+// one partial segment per chunk.
+constexpr IndexLayout index_layout(int64_t packed_nbytes, int64_t n_chunks, uint32_t seg_bits) {
+    IndexLayout l{};
+    const uint64_t pb = packed_nbytes > 0 ? static_cast<uint64_t>(packed_nbytes) : 0u;
+    const uint64_t nc = n_chunks > 0 ? static_cast<uint64_t>(n_chunks) : 0u;
+    const uint64_t s = seg_bits > 0 ? seg_bits : 1u;
+    l.capacity = (8 * pb + s - 1) / s + nc;
+    l.n_bchunk = l.capacity / kIndexBlock + 2;
+    l.base = sizeof(IndexHeader);
+    l.rend = index_rend_at(n_chunks);
+    l.entries = index_entries_at(n_chunks);
+    l.bchunk = (l.entries + 2 * l.capacity + 15) & ~uint64_t{15};
+    l.total = l.bchunk + 4 * l.n_bchunk;
+    return l;
 }
 
 // Segment length for a code whose shortest codeword has min_len bits: at

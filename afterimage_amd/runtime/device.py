@@ -262,13 +262,13 @@ class DeviceTensor:
 
     @property
     def index_bytes_read(self) -> int:
-        """Index bytes a decode reads: the chunk bases and the entries of the
-        chunks' segments (0 without an index)."""
+        """Index bytes a decode reads: the entries of the chunks' segments and
+        each chunk's first segment and real end (0 without an index)."""
         if self.index is None:
             return 0
         seg = segment_bits(self.tables.host_blob)
         nb = self.chunk_nbytes.to(torch.int64)
-        return int(4 * self.n_chunks + 2 * ((nb * 8 + seg - 1) // seg).sum().item())
+        return int(8 * self.n_chunks + 2 * ((nb * 8 + seg - 1) // seg).sum().item())
 
     @property
     def algorithmic_bytes(self) -> int:
@@ -279,9 +279,12 @@ class DeviceTensor:
                 + self.n_symbols + (5 * 4096 + 256) + self.index_bytes_read
                 + 2 * self.n_symbols)
 
-    def build_index(self) -> "DeviceTensor":
+    def build_index(self, keep_unusable: bool = False) -> "DeviceTensor":
         """Build this tensor's segment index on the current stream (one pass
-        over its bitstreams); later decodes use it. Returns self."""
+        over its bitstreams, then a check of the result, which waits for
+        it); later decodes use it. An index the build marks unusable (chunks
+        not back to back in the packed buffer, or a chunk that does not hold
+        its symbols) is dropped unless keep_unusable. Returns self."""
         dev = self.packed.device
         if dev.type != "cuda":
             raise RuntimeError("the segment index is built on the GPU; tensor is on %s" % dev)
@@ -292,8 +295,14 @@ class DeviceTensor:
         d[0].index_nbytes = int(ix.numel())
         with torch.cuda.device(dev):
             _native.check(_native.lib().aimg_build_index(d, 1, _stream_handle(dev)))
-        self.index = ix
+        usable = int(ix[16:20].cpu().numpy().view(np.uint32)[0]) == 1
+        self.index = ix if usable or keep_unusable else None
         return self
+
+    @property
+    def index_usable(self) -> bool:
+        return self.index is not None and \
+            int(self.index[16:20].cpu().numpy().view(np.uint32)[0]) == 1
 
     def drop_index(self) -> None:
         self.index = None

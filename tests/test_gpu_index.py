@@ -52,33 +52,49 @@ def _starts(enc, c):
 
 
 def _expected_index(enc, seg):
-    """(bases, entries) of the index: per chunk, per segment of seg bits, the
-    first boundary's offset from the segment start | count << 4."""
-    bases, entries = [], []
+    """(bases, rends, entries) of the index: per chunk, per segment of seg
+    bits, the first boundary's offset from the segment start | count << 4,
+    where count takes only the codewords before the chunk's real end (the
+    end of its lim-th codeword, lim its output elements)."""
+    bases, rends, entries = [], [], []
     n_jobs = -(-int(enc.n_symbols) // int(enc.chunk_size))
     for c in range(len(enc.chunk_offsets)):
         bases.append(len(entries))
         if c >= n_jobs:
+            rends.append(None)
             continue
+        lim = min(int(enc.chunk_size), int(enc.n_symbols) - c * int(enc.chunk_size))
         bounds = _starts(enc, c)
         st = bounds[:-1]
+        rend = int(bounds[lim])  # end of the lim-th codeword
+        rends.append(rend)
         nseg = -(-8 * int(enc.chunk_nbytes[c]) // seg)
         for k in range(nseg):
             lo = k * seg
-            inside = st[(st >= lo) & (st < lo + seg)]
+            inside = st[(st >= lo) & (st < lo + seg) & (st < rend)]
             f = int(bounds[bounds >= lo][0]) - lo
             entries.append(f | (len(inside) << 4))
     bases.append(len(entries))
-    return np.asarray(bases, np.uint32), np.asarray(entries, np.uint16)
+    return np.asarray(bases, np.uint32), rends, np.asarray(entries, np.uint16)
 
 
-def _index_arrays(t):
+def _layout(t, seg):
+    """Byte offsets of the index arrays (header, bases, real ends, entries)."""
+    n = t.n_chunks
+    cap = -(-8 * int(t.packed.numel()) // seg) + n
+    base = 64
+    rend = base + 4 * (n + 1)
+    entries = (rend + 4 * n + 15) & ~15
+    return base, rend, entries, cap
+
+
+def _index_arrays(t, seg):
     ix = t.index.cpu().numpy()
     hdr = ix[:64].view(np.uint32)
     n = t.n_chunks
-    bases = ix[64: 64 + 4 * (n + 1)].view(np.uint32)
-    at = (64 + 4 * (n + 1) + 15) & ~15
-    return hdr, bases, ix[at:]
+    base, rend, entries, cap = _layout(t, seg)
+    return (hdr, ix[base: base + 4 * (n + 1)].view(np.uint32), ix[rend: rend + 4 * n].view(np.uint32),
+            ix[entries: entries + 2 * cap].view(np.uint16))
 
 
 @pytest.mark.parametrize("kind,chunk", [("skewed", 64), ("skewed", 1024), ("bf16", 4096),
@@ -95,11 +111,14 @@ def test_index_entries_equal_a_cpu_walk_of_the_codeword_starts(kind, chunk):
     enc = encode_chunked(exps, chunk_size=chunk)
     t = DeviceTensor.from_encoded(enc, None, DEV).build_index()
     seg = segment_bits(t.tables.host_blob)
-    hdr, bases, entries = _index_arrays(t)
-    want_b, want_e = _expected_index(enc, seg)
+    hdr, bases, rends, entries = _index_arrays(t, seg)
+    want_b, want_r, want_e = _expected_index(enc, seg)
     assert hdr[2] == seg and hdr[4] == 1, "header: seg_bits %d ok %d" % (hdr[2], hdr[4])
+    assert hdr[6] == len(want_e), "segments %d, want %d" % (hdr[6], len(want_e))
     assert np.array_equal(bases, want_b)
-    got = entries.view(np.uint16)[: len(want_e)]
+    assert [int(r) for r, w in zip(rends, want_r) if w is not None] == \
+        [w for w in want_r if w is not None]
+    got = entries[: len(want_e)]
     bad = np.nonzero(got != want_e)[0]
     assert bad.size == 0, "entries differ at %s: %s vs %s" % (bad[:5], got[bad[:5]], want_e[bad[:5]])
     assert np.array_equal(decode_u8([t])[0].cpu().numpy(), exps.numpy().astype(np.uint8))
@@ -176,8 +195,7 @@ def test_an_index_too_small_is_marked_unusable_and_ignored():
     W = workloads.bf16_normal((200, 3000), 7, 0.02, outlier_frac=1e-3)
     layer = compress_layer(W, chunk_size=4096)
     t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, DEV)
-    t.index = torch.zeros(((64 + 4 * (t.n_chunks + 1) + 15) & ~15) + 16, dtype=torch.uint8,
-                          device=DEV)
+    t.index = torch.zeros(t.index_nbytes - 16, dtype=torch.uint8, device=DEV)
     from afterimage_amd import _native
     from afterimage_amd.runtime.device import _descriptor, _stream_handle
     d = (_native.AimgTensor * 1)()
@@ -202,3 +220,35 @@ def test_gemv_with_index_matches_without(batch):
     want = (x.double().cpu() @ W.double().t()).float()
     assert torch.allclose(y1.cpu(), want, rtol=1e-2, atol=1e-3)
     assert torch.allclose(y1, y0, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("chunk", [1024, 2048, 65536])
+def test_segment_runs_split_chunks_over_the_grid(chunk):
+    # Large enough for a full grid: every workgroup's slice of the segments
+    # starts and ends inside chunks.
+    W = workloads.bf16_normal((2048, 8192), 16, 0.02, outlier_frac=1e-3)
+    layer = compress_layer(W, chunk_size=chunk)
+    t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, DEV).build_index()
+    out = decode_bf16([t])[0]
+    assert torch.equal(out.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
+
+
+def test_chunks_not_back_to_back_make_the_index_unusable():
+    # Same bytes, chunk 1 moved to the end of the buffer: still a valid
+    # compressed tensor, but its chunks do not follow one another.
+    W = workloads.bf16_normal((64, 4096), 17, 0.02, outlier_frac=1e-3)
+    layer = compress_layer(W, chunk_size=4096)
+    enc = layer.encoded
+    packed = np.asarray(enc.packed, np.uint8)
+    offs = np.asarray(enc.chunk_offsets, np.int32).copy()
+    nbs = np.asarray(enc.chunk_nbytes, np.int32)
+    moved = packed[offs[1]: offs[1] + nbs[1]].copy()
+    packed2 = np.concatenate([packed, moved])
+    offs[1] = len(packed)
+    t = DeviceTensor.from_encoded(enc, layer.sign_mantissa, DEV)
+    t.packed = torch.from_numpy(packed2).to(DEV)
+    t.chunk_offsets = torch.from_numpy(offs).to(DEV)
+    t.build_index(keep_unusable=True)
+    assert not t.index_usable
+    out = decode_bf16([t])[0]
+    assert torch.equal(out.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))

@@ -73,9 +73,12 @@ def _write(d, enc, expect, sm=None):
         f.write("%d %d %d %d\n" % (enc.max_bits, enc.chunk_size, enc.n_symbols, len(enc.chunk_offsets)))
 
 
-def _run(emu, name, mode, index=""):
+def _run(emu, name, mode, index="", runs=None):
     exe, d = emu
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0")
+    env.pop("AIMG_SEGMENT_RUNS", None)
+    if runs is not None:
+        env["AIMG_SEGMENT_RUNS"] = runs
     args = [exe, str(d / name), mode] + ([index] if index else [])
     r = subprocess.run(args, capture_output=True, text=True, env=env, timeout=600)
     assert r.returncode == 0 and ": ok" in r.stdout, (r.stdout + r.stderr)[-4000:]
@@ -88,14 +91,14 @@ def _u8(emu, name, exps, chunk_size, index=""):
     _run(emu, name, "u8", index)
 
 
-def _bf16(emu, name, W, chunk_size, index=""):
+def _bf16(emu, name, W, chunk_size, index="", runs=None):
     layer = compress_layer(W, chunk_size=chunk_size)
     _write(emu[1] / name, layer.encoded, W.reshape(-1).view(torch.int16).numpy(),
            layer.sign_mantissa.numpy())
-    _run(emu, name, "bf16", index)
+    _run(emu, name, "bf16", index, runs)
 
 
-def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index=""):
+def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None):
     W = workloads.bf16_normal((rows, cols), seed, 0.02, outlier_frac=1e-3)
     layer = compress_layer(W, chunk_size=chunk_size)
     g = np.random.default_rng(seed + 1)
@@ -107,7 +110,7 @@ def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index=""):
     want.numpy().tofile(os.path.join(d, "expect_y.bin"))
     with open(os.path.join(d, "gemv.txt"), "w") as f:
         f.write("%d %d %d\n" % (rows, cols, batch))
-    _run(emu, name, "gemv", index)
+    _run(emu, name, "gemv", index, runs)
 
 
 @pytest.mark.parametrize("batch", [1, 4])
@@ -236,3 +239,52 @@ def test_gemv_with_index(emu, batch):
 
 def test_gemv_16_thread_chunks_with_index(emu):
     _gemv(emu, "ix_gemv16", 96, 40, 64, 2, 3, index="index")
+
+
+def test_bf16_segment_runs_cross_chunk_and_workgroup_boundaries(emu):
+    # 1024-symbol chunks over 768K weights: about 20 segments of 168 bits a
+    # chunk, and the launch's segments split over several workgroups, so
+    # rounds and workgroup slices start and end inside chunks and inside
+    # vector groups.
+    W = workloads.bf16_normal((96, 8192), 12, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "ix_runs1024", W, 1024, index="index")
+
+
+def test_u8_segment_runs_of_a_ragged_tensor(emu):
+    # The last chunk holds 700 of its 2048 symbols.
+    rng = np.random.default_rng(13)
+    _u8(emu, "ix_runs_ragged", rng.integers(90, 135, 2048 * 150 + 700), 2048, index="index")
+
+
+def test_gemv_segment_runs_at_chunk_1024(emu):
+    _gemv(emu, "ix_gemv1024", 128, 2048, 1024, 2, 14, index="index")
+
+
+def test_unusable_index_fallback_over_several_workgroups(emu):
+    W = workloads.bf16_normal((96, 8192), 15, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "ix_fallback_many", W, 1024, index="index-foreign")
+
+
+# The same indexes decoded chunk by chunk (AIMG_SEGMENT_RUNS=0 forces it; on
+# its own the library takes that path for launches of many whole-workgroup
+# chunks) and in segment runs (=1).
+
+@pytest.mark.parametrize("runs", ["0", "1"])
+def test_bf16_two_round_64k_chunks_with_index_both_paths(emu, runs):
+    W = workloads.bf16_normal((64, 17408), 2, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "ix_64k_paths%s" % runs, W, 65536, index="index", runs=runs)
+
+
+@pytest.mark.parametrize("runs", ["0", "1"])
+def test_bf16_1024_chunks_with_index_both_paths(emu, runs):
+    W = workloads.bf16_normal((48, 8192), 18, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "ix_1024_paths%s" % runs, W, 1024, index="index", runs=runs)
+
+
+def test_gemv_with_index_chunk_by_chunk(emu):
+    _gemv(emu, "ix_gemv512_items", 70, 1000, 32768, 4, 5, index="index", runs="0")
+
+
+def test_foreign_index_chunk_by_chunk(emu):
+    W = workloads.bf16_normal((40, 5000), 6, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "ix_foreign_items", W, 4096, index="index-foreign", runs="0")

@@ -256,7 +256,7 @@ def test_table_blob_records_a_checksum_of_its_tables():
     assert int(blob[28:32].view(np.uint32)[0]) == h
 
 
-def test_index_size_is_two_bytes_per_segment_plus_chunk_bases():
+def test_index_size_is_two_bytes_per_segment_plus_chunk_tables():
     lib = _native.lib()
     enc, blob = _bf16_table()
     min_len = int(blob[12:16].view(np.uint32)[0])
@@ -264,8 +264,14 @@ def test_index_size_is_two_bytes_per_segment_plus_chunk_bases():
     n = ctypes.c_size_t()
     packed, chunks = 1_000_003, 77
     assert lib.aimg_index_nbytes(blob.ctypes.data, packed, chunks, ctypes.byref(n)) == 0
-    entries_at = (64 + 4 * (chunks + 1) + 15) & ~15
-    assert n.value == entries_at + 2 * (-(-8 * packed // seg) + chunks)
+    # 64-byte header, first segment (chunks + 1) and real end (chunks) of
+    # each chunk, 2 bytes per segment of the packed bytes (one partial
+    # segment per chunk), and the chunk of every 512th segment.
+    cap = -(-8 * packed // seg) + chunks
+    entries_at = (64 + 4 * (chunks + 1) + 4 * chunks + 15) & ~15
+    bchunk_at = (entries_at + 2 * cap + 15) & ~15
+    assert n.value == bchunk_at + 4 * (cap // 512 + 2)
+    assert n.value < 2.05 * cap + 12 * chunks + 128
     bad = blob.copy()
     bad[0] ^= 1
     assert lib.aimg_index_nbytes(bad.ctypes.data, packed, chunks, ctypes.byref(n)) == \
@@ -286,7 +292,7 @@ def test_build_index_validates_before_launching():
     assert lib.aimg_build_index(arr, 1, None) == _native.AIMG_OK
     assert lib.aimg_build_index(arr, 33, None) == _native.AIMG_ERR_INVALID_ARGUMENT
     arr[0].index = 4096
-    arr[0].index_nbytes = 64  # below the header and 5 chunk bases
+    arr[0].index_nbytes = 32  # below the 64-byte header
     assert lib.aimg_build_index(arr, 1, None) == _native.AIMG_ERR_INVALID_ARGUMENT
     assert b"index_nbytes" in lib.aimg_last_error()
     arr[0].index = 4100
