@@ -1079,7 +1079,7 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
     uint2 sm[kStoreBatch];
 #pragma unroll
     for (uint32_t k = 0; k < kSmAhead; ++k) sm[k] = B.v[k];
-    if (__builtin_amdgcn_ballot_w64(kSmAhead * tpc + i < nfull) != 0) {
+    if (__ballot(kSmAhead * tpc + i < nfull) != 0) {
         const __amdgpu_buffer_rsrc_t rs = buffer_of(T.sm, static_cast<uint32_t>(T.n_symbols));
         const uint32_t v0 = static_cast<uint32_t>(a0) + i * kGroup;
 #pragma unroll

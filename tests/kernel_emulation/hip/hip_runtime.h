@@ -137,6 +137,10 @@ inline unsigned long long __ballot(int p) {
     return m;
 }
 
+// The raw builtin is used by the kernel only inside divergent code (the
+// escape branch of the decode loop), where lanes that have left the loop do
+// not meet at a wave barrier: each lane sees its own bit, so a lane without
+// an escape skips the branch in which it would do nothing.
 inline uint64_t __builtin_amdgcn_ballot_w64(bool p) { return p ? (1ull << emu::lane()) : 0ull; }
 // Same signatures as the compiler builtins (int in, int out). readfirstlane
 // is applied to wave-uniform values only, so the lane's own value is it.
