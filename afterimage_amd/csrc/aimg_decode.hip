@@ -129,9 +129,10 @@ constexpr bool needs_sm(int mode) { return mode != kModeU8 && mode != kModeIndex
 // Job::ib of a chunk decoded without the index.
 constexpr uint32_t kNoIndex = 0xFFFFFFFFu;
 constexpr int kGemvMaxBatch = 4;
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+// Steps ahead of use that x is requested with up to kGemvMaxBatch x vectors
+// (with one, 3). Measured on the 5120x17408 layer at batch 4: 2 steps
+// ahead 7% slower than 1, 3 steps 39% slower.
+constexpr uint32_t kGemvXAhead = 1;
 
 struct GemvArgs {
     const uint16_t* x;  // bf16 [batch][cols]
@@ -831,44 +832,33 @@ __device__ __forceinline__ void sm_issue(SmBatch<kMode>& B, const DevTensor& T, 
     }
 }
 
-// The diagonal of a 16x16 MFMA result summed over the wave, in lane 63.
-// Lane l holds result rows 4 (l / 16) + r, r < 4, of column l % 16, so its
-// diagonal element (if any) is r = l % 16 - 4 (l / 16).
-__device__ __forceinline__ float mfma_diag_sum(const f32x4& d) {
-    const int lane = threadIdx.x & 63;
-    const int r = (lane & 15) - 4 * (lane >> 4);
-    uint32_t v = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v |= __float_as_uint(d[j]) & (r == j ? 0xFFFFFFFFu : 0u);
-    return __uint_as_float(wave_scan_incl_f32(v));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// c + the products of 8 bf16 weights and 8 bf16 x values, in fp32
+// (v_dot2c_f32_bf16: two products per instruction).
+__device__ __forceinline__ float dot8_acc(const uint4& w, const uint4& x, float c) {
+    c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.x),
+                                        __builtin_bit_cast(bf16x2, x.x), c, false);
+    c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.y),
+                                        __builtin_bit_cast(bf16x2, x.y), c, false);
+    c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.z),
+                                        __builtin_bit_cast(bf16x2, x.z), c, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.w),
+                                           __builtin_bit_cast(bf16x2, x.w), c, false);
 }
 
-// Add the wave's accumulated products for y[b][row], b < nb, to y (one
-// atomic per batch row, from lane 63) and clear the accumulators.
+// Add the wave's per-lane sums s[b] (b < nb) to y[b][row]: one wave sum and
+// one atomic (from lane 63) per batch row.
 template <int kB>
-__device__ __forceinline__ void gemv_flush(const GemvArgs& G, int nb, f32x4 (&acc)[kB],
-                                           uint32_t row) {
+__device__ __forceinline__ void gemv_flush_lanes(const GemvArgs& G, int nb, const float (&s)[kB],
+                                                 uint32_t row) {
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
         if (b >= nb) break;
-        const float s = mfma_diag_sum(acc[b]);
-        if ((threadIdx.x & 63) == 63 && s != 0.0f)
-            atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + row, s);
-        acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const float t = __uint_as_float(wave_scan_incl_f32(__float_as_uint(s[b])));
+        if ((threadIdx.x & 63) == 63 && t != 0.0f)
+            atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + row, t);
     }
-}
-
-// Sum of the products of 8 bf16 weights and 8 bf16 x values, in fp32.
-__device__ __forceinline__ float dot8_bf16(const uint4& w, const uint4& x) {
-    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-    const uint32_t xv[4] = {x.x, x.y, x.z, x.w};
-    float s = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        s += __uint_as_float(wv[q] << 16) * __uint_as_float(xv[q] << 16);
-        s += __uint_as_float(wv[q] & 0xFFFF0000u) * __uint_as_float(xv[q] & 0xFFFF0000u);
-    }
-    return s;
 }
 
 // Adds each live lane's products p[b] (b < nb) to y[b][row of the lane] with
@@ -898,17 +888,25 @@ __device__ __forceinline__ void advance_col(uint32_t& col, uint32_t step, uint32
     while (col >= cols) col -= cols;
 }
 
-// The 8 x values at column col of each batch row b < nb (col < cols, and
-// col % 8 == 0 with a 16-byte-aligned x, so the reads are in bounds and
-// aligned). Rows b >= nb are left zero.
+// The 8 x values at column col of each batch row b < kB (col < cols, and
+// col % 8 == 0 with a 16-byte-aligned x, so the reads are aligned). The
+// buffer ends after the nb rows of x, so rows b >= nb read as zero. Every
+// load is issued on every path: the compiler then counts them exactly, and
+// a wait for one x vector's words does not become a wait for every load in
+// flight.
 template <int kB>
 __device__ __forceinline__ void gemv_load_x(uint4 (&dst)[kB], const GemvArgs& G, int nb,
                                             uint32_t col) {
+    if constexpr (kB == 1) {  // one x vector: a plain load (measured 1% faster)
+        dst[0] = *reinterpret_cast<const uint4*>(G.x + col);
+        return;
+    }
+    const uint32_t row_bytes = 2u * G.cols;
+    const __amdgpu_buffer_rsrc_t rs = buffer_of(G.x, static_cast<uint32_t>(nb) * row_bytes);
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
-        dst[b] = make_uint4(0u, 0u, 0u, 0u);
-        if (b < nb)
-            dst[b] = *reinterpret_cast<const uint4*>(G.x + static_cast<int64_t>(b) * G.cols + col);
+        const auto d = __builtin_amdgcn_raw_buffer_load_b128(rs, 2u * col, b * row_bytes, 0);
+        dst[b] = make_uint4(d[0], d[1], d[2], d[3]);
     }
 }
 
@@ -922,32 +920,27 @@ __device__ __forceinline__ void step_rc(uint32_t& row, uint32_t& col, const Gemv
     row += wrap ? 1u : 0u;
 }
 
-// Fused GEMV over one staged round when the workgroup is one chunk. Thread i
-// holds group i + 512 k, so at each step k wave w's 64 groups are the 512
-// consecutive elements from a0 + 8 (64 w + 512 k). Their first row and
-// column are tracked for the whole wave as scalars, each lane's own as
-// registers, both by step_rc (no division past the first step). When the
-// 512 lie in one row (all but about 512 / cols of the steps for
-// cols >= 512), one MFMA per x vector takes the wave's products: lane l
-// supplies its 8 weights as A row l % 16 and its 8 x values as B column
-// l % 16 over the same k, so the diagonal of the 16x16 result holds the sums
-// of each lane's own products (dead lanes supply zeros). The accumulator is
-// reduced over the wave and added to y when the row changes. A step that
-// crosses a row boundary (about 512 / cols of them) takes two masked MFMAs,
-// the lanes of the first row and then those of the second, with the first
-// row's sum added in between: two atomics per x vector instead of one per
-// lane (per-lane atomics at one step in 34 on 17408-column rows made up
-// most of the fused GEMV's time). Only rows shorter than 512 elements take
-// per-lane atomics. Liveness is applied as masks, so the step is straight
-// code. With one x vector its words are requested kXAhead steps ahead of
-// use; every x read is in bounds, since a column is always below cols. G's x
-// and y are those of the nb <= kB x vectors of this pass.
+// Fused GEMV over one staged round when the workgroup is one chunk (or a
+// segment run). Thread i holds group i + 512 k, so at each step k wave w's
+// 64 groups are the 512 consecutive elements from a0 + 8 (64 w + 512 k).
+// Their first row and column are tracked for the whole wave as scalars,
+// each lane's own as registers, both by step_rc (no division past the first
+// step). Each lane keeps one fp32 sum per x vector and adds its 8 products
+// with four v_dot2c_f32_bf16; the sums are reduced over the wave (DPP) and
+// added to y with one atomic per x vector when the row changes. A step that
+// crosses a row boundary (about 512 / cols of them) flushes the lanes of the
+// first row and starts the next row's sums with the others. Only rows
+// shorter than 512 elements take per-lane atomics. Dead lanes' products are
+// dropped (not multiplied by zero), so an infinite x cannot make a NaN. x is
+// requested kXAhead steps ahead of use for every x vector, and every
+// vector's loads and products are unconditional (see gemv_load_x); G's x and
+// y are those of the nb <= kB x vectors of this pass.
 template <int kMode, int kGroup, int kB>
 __device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch], const GemvArgs& G,
                                                  int nb, const uint8_t* stage, uint32_t a0,
                                                  uint32_t nfull, uint32_t i, uint32_t v_lo) {
     static_assert(kThreads * kGroup == 4096, "step_rows / step_cols are for 4096 elements");
-    constexpr uint32_t kXAhead = kB == 1 ? 3 : 0;
+    constexpr uint32_t kXAhead = kB == 1 ? 3 : kGemvXAhead;
     constexpr uint32_t kSpan = 64 * kGroup;  // elements a wave holds at one step
     const uint32_t cols = G.cols;
     const uint32_t lane = i & 63;
@@ -965,9 +958,9 @@ __device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch],
         if (k > 0) step_rc(lr_ld, lc_ld, G);
         gemv_load_x<kB>(xq[k], G, nb, lc_ld);
     }
-    f32x4 acc[kB];
+    float acc[kB];
 #pragma unroll
-    for (int b = 0; b < kB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < kB; ++b) acc[b] = 0.0f;
     uint32_t acc_row = 0xFFFFFFFFu;
 #pragma unroll
     for (uint32_t k = 0; k < kStoreBatch; ++k) {
@@ -982,65 +975,60 @@ __device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch],
         if (k * kThreads + wave_first >= nfull) break;  // this wave's groups are done
         const uint4(&xc)[kB] = xq[k % (kXAhead + 1)];
         const uint32_t v = k * kThreads + i;
-        const uint32_t m = v < nfull && v >= v_lo ? 0xFFFFFFFFu : 0u;  // live group
+        const bool live = v < nfull && v >= v_lo;
         const uint2 e = *reinterpret_cast<const uint2*>(stage + v * kGroup);
         uint4 w;
-        w.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, e.x) & m;
-        w.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, e.x) & m;
-        w.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, e.y) & m;
-        w.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, e.y) & m;
+        w.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, e.x);
+        w.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, e.x);
+        w.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, e.y);
+        w.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, e.y);
         if (ec + kSpan <= cols) {
             if (er != acc_row) {
-                if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);
+                if (acc_row != 0xFFFFFFFFu) {
+                    gemv_flush_lanes<kB>(G, nb, acc, acc_row);
+#pragma unroll
+                    for (int b = 0; b < kB; ++b) acc[b] = 0.0f;
+                }
                 acc_row = er;
             }
 #pragma unroll
             for (int b = 0; b < kB; ++b) {
-                if (b >= nb) break;
-                const uint4 xz = make_uint4(xc[b].x & m, xc[b].y & m, xc[b].z & m, xc[b].w & m);
-                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    __builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, xz), acc[b], 0, 0, 0);
+                const float t = dot8_acc(w, xc[b], acc[b]);
+                acc[b] = live ? t : acc[b];
             }
         } else if (cols >= kSpan) {
             // Two rows: lanes below the boundary finish row er, the rest
             // start row er + 1.
             if (er != acc_row) {
-                if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);
+                if (acc_row != 0xFFFFFFFFu) {
+                    gemv_flush_lanes<kB>(G, nb, acc, acc_row);
+#pragma unroll
+                    for (int b = 0; b < kB; ++b) acc[b] = 0.0f;
+                }
                 acc_row = er;
             }
-            const uint32_t lo = lr == er ? 0xFFFFFFFFu : 0u;
-            const uint4 w_lo = make_uint4(w.x & lo, w.y & lo, w.z & lo, w.w & lo);
-            const uint4 w_hi = make_uint4(w.x & ~lo, w.y & ~lo, w.z & ~lo, w.w & ~lo);
+            const bool lo = lr == er;
+            float p[kB];
 #pragma unroll
             for (int b = 0; b < kB; ++b) {
-                if (b >= nb) break;
-                const uint32_t ml = m & lo;
-                const uint4 xz = make_uint4(xc[b].x & ml, xc[b].y & ml, xc[b].z & ml, xc[b].w & ml);
-                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    __builtin_bit_cast(bf16x8, w_lo), __builtin_bit_cast(bf16x8, xz), acc[b], 0, 0, 0);
+                const float t = dot8_acc(w, xc[b], 0.0f);
+                p[b] = live ? t : 0.0f;
+                acc[b] += lo ? p[b] : 0.0f;
             }
-            gemv_flush<kB>(G, nb, acc, er);
+            gemv_flush_lanes<kB>(G, nb, acc, er);
+#pragma unroll
+            for (int b = 0; b < kB; ++b) acc[b] = lo ? 0.0f : p[b];
             acc_row = er + 1;
+        } else if (live) {
+            // Rows shorter than a wave's 512 elements: per-lane atomics.
 #pragma unroll
             for (int b = 0; b < kB; ++b) {
                 if (b >= nb) break;
-                const uint32_t mh = m & ~lo;
-                const uint4 xz = make_uint4(xc[b].x & mh, xc[b].y & mh, xc[b].z & mh, xc[b].w & mh);
-                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    __builtin_bit_cast(bf16x8, w_hi), __builtin_bit_cast(bf16x8, xz), acc[b], 0, 0, 0);
-            }
-        } else if (m != 0u) {
-            // Rows shorter than a wave's 512 elements: per-lane atomics (a
-            // wave sum per row here, as in the small-chunk path, costs this
-            // kernel's other steps registers it does not have).
-#pragma unroll
-            for (int b = 0; b < kB; ++b) {
-                if (b >= nb) break;
-                atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + lr, dot8_bf16(w, xc[b]));
+                atomicAdd(G.y + static_cast<int64_t>(b) * G.rows + lr, dot8_acc(w, xc[b], 0.0f));
             }
         }
     }
-    if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);
+    if (acc_row != 0xFFFFFFFFu) gemv_flush_lanes<kB>(G, nb, acc, acc_row);
 }
 
 // Vector groups [0, nfull) of the staged round to output elements a0...;
@@ -1133,18 +1121,15 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
     }
     // Fused GEMV: each group's 8 weights (one matrix row, as cols % 8 == 0)
     // meet the 8 x values of their columns. When a wave's live groups at one
-    // k lie in one row (the usual case), one MFMA per x vector takes the
-    // wave's products: lane l supplies its weights as A row l % 16 and its x
-    // as B column l % 16 over the same 8 k, so the diagonal of the 16x16
-    // result holds the sums of each lane's own products (dead lanes supply
-    // zeros). The accumulator is reduced over the wave and added to y when
-    // the row changes. A step whose live groups span several rows takes the
-    // products on the VALU and adds one wave sum per distinct row.
-    // With one x vector its words are requested kXAhead groups ahead of use
-    // (a group's column is always below cols, so every read is in bounds,
-    // live group or not); with up to four there are no registers for that.
+    // k lie in one row (the usual case), each lane adds its products to its
+    // own fp32 sum per x vector (v_dot2c_f32_bf16), and the sums are reduced
+    // over the wave and added to y when the row changes. A step whose live
+    // groups span several rows adds one wave sum per distinct row. x is
+    // requested kXAhead groups ahead of use (a group's column is always below
+    // cols, so every read is in bounds, live group or not); loads and
+    // products are unconditional for every x vector (see gemv_load_x).
     constexpr int kB = kMode == kModeGemv1 ? 1 : kGemvMaxBatch;
-    constexpr uint32_t kXAhead = kMode == kModeGemv1 ? 3 : 0;
+    constexpr uint32_t kXAhead = kMode == kModeGemv1 ? 3 : kGemvXAhead;
     const int nb = kMode == kModeGemv1 ? 1 : G.batch;
     const uint32_t cols = G.cols;
     const uint32_t el = static_cast<uint32_t>(a0) + i * kGroup;  // element of group k = 0
@@ -1158,9 +1143,9 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
         if (k > 0) advance_col(col_ld, step, cols);
         gemv_load_x<kB>(xq[k], G, nb, col_ld);
     }
-    f32x4 acc[kB];
+    float acc[kB];
 #pragma unroll
-    for (int b = 0; b < kB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < kB; ++b) acc[b] = 0.0f;
     uint32_t acc_row = 0xFFFFFFFFu;
 #pragma unroll
     for (uint32_t k = 0; k < kStoreBatch; ++k) {
@@ -1183,22 +1168,24 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
         // Staged exponents read here rather than all at once: registers.
         const uint2 e = *reinterpret_cast<const uint2*>(stage + (kWhole || live ? v : 0u) * kGroup);
         uint4 w;
-        w.x = live ? bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, e.x) : 0u;
-        w.y = live ? bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, e.x) : 0u;
-        w.z = live ? bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, e.y) : 0u;
-        w.w = live ? bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, e.y) : 0u;
+        w.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, e.x);
+        w.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, e.x);
+        w.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, e.y);
+        w.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, e.y);
         const uint32_t r0 = __builtin_amdgcn_readlane(row, __builtin_ctzll(lm));
         if (__ballot(live && row != r0) == 0) {
             if (r0 != acc_row) {
-                if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);
+                if (acc_row != 0xFFFFFFFFu) {
+                    gemv_flush_lanes<kB>(G, nb, acc, acc_row);
+#pragma unroll
+                    for (int b = 0; b < kB; ++b) acc[b] = 0.0f;
+                }
                 acc_row = r0;
             }
 #pragma unroll
             for (int b = 0; b < kB; ++b) {
-                if (b >= nb) break;
-                const uint4 xz = live ? xc[b] : make_uint4(0u, 0u, 0u, 0u);
-                acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    __builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, xz), acc[b], 0, 0, 0);
+                const float t = dot8_acc(w, xc[b], acc[b]);
+                acc[b] = live ? t : acc[b];
             }
         } else {
             // Several rows: one wave sum and one atomic per distinct row
@@ -1206,11 +1193,14 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
             // chunks, and often several rows, in one wave step).
             float p[kB];
 #pragma unroll
-            for (int b = 0; b < kB; ++b) p[b] = live ? dot8_bf16(w, xc[b]) : 0.0f;
+            for (int b = 0; b < kB; ++b) {
+                const float t = dot8_acc(w, xc[b], 0.0f);
+                p[b] = live ? t : 0.0f;
+            }
             gemv_rows_add<kB>(G, nb, p, live, row);
         }
     }
-    if (acc_row != 0xFFFFFFFFu) gemv_flush<kB>(G, nb, acc, acc_row);
+    if (acc_row != 0xFFFFFFFFu) gemv_flush_lanes<kB>(G, nb, acc, acc_row);
 }
 
 // Window table and the first kLdsEscBlocks escape blocks of a table blob to LDS.

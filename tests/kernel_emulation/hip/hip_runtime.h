@@ -5,12 +5,13 @@
 //
 // Model: a block runs as one std::thread per work-item; blocks run one after
 // another; __shared__ data are function statics (one block at a time).
-// __syncthreads is a block barrier. Wave shuffles, readlane, HIP's __ballot
-// and the MFMA exchange values through a per-wave buffer between per-wave
+// __syncthreads is a block barrier. Wave shuffles, DPP, readlane and HIP's
+// __ballot exchange values through a per-wave buffer between per-wave
 // barriers, so they must be reached by all 64 lanes (the kernel calls them in
 // uniform control flow only). The compiler builtin ballot returns the calling
-// lane's own bit: the kernel uses it, inside divergent loops too, as "does any
-// lane need this?", for which the per-lane answer gives the same results.
+// lane's own bit: the kernel uses it only inside divergent loops, as "does
+// any lane need this?", for which the per-lane answer gives the same
+// results.
 #pragma once
 #include <barrier>
 #include <cstdint>
@@ -78,16 +79,6 @@ inline T wave_xchg(T v, unsigned src) {
     T out;
     std::memcpy(&out, &r, sizeof(T));
     return out;
-}
-// Every lane's v, gathered by every lane of the wave (out[k] from lane k).
-inline void wave_all(uint64_t v, uint64_t* out) {
-    Block& B = *g_block;
-    const unsigned w = threadIdx.x >> 6;
-    B.wave[w]->arrive_and_wait();
-    B.xbuf[threadIdx.x] = v;
-    B.wave[w]->arrive_and_wait();
-    for (unsigned k = 0; k < 64; ++k) out[k] = B.xbuf[w * 64 + k];
-    B.wave[w]->arrive_and_wait();
 }
 }  // namespace emu
 
@@ -203,6 +194,13 @@ inline emu_u32x2 __builtin_amdgcn_raw_buffer_load_b64(__amdgpu_buffer_rsrc_t r, 
     return v;
 }
 typedef uint32_t emu_u32x4 __attribute__((ext_vector_type(4)));
+inline emu_u32x4 __builtin_amdgcn_raw_buffer_load_b128(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so,
+                                                       int) {
+    const uint64_t off = (uint64_t)vo + so;
+    emu_u32x4 v;
+    for (int k = 0; k < 4; ++k) v[k] = emu_dword(r, off + 4 * k);
+    return v;
+}
 // Stores: each dword past num_records is dropped.
 inline void __builtin_amdgcn_raw_buffer_store_b128(emu_u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t vo,
                                                    uint32_t so, int) {
@@ -248,38 +246,16 @@ inline float atomicAdd(float* p, float v) {
 }
 inline int __ffs(int x) { return __builtin_ffs(x); }
 inline void __builtin_amdgcn_s_setprio(int) {}  // wave issue priority: no effect here
-// v_mfma_f32_16x16x32_bf16, D = A B + C with A 16x32, B 32x16, fp32 sums.
-// Lane l supplies A[l % 16][8 (l / 16) + j] and B[8 (l / 16) + j][l % 16]
-// (j < 8, its 8 bf16 operands) and receives D[4 (l / 16) + r][l % 16], r < 4.
-typedef __bf16 emu_bf16x8 __attribute__((ext_vector_type(8)));
-typedef float emu_f32x4 __attribute__((ext_vector_type(4)));
-inline float emu_bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
-inline emu_f32x4 __builtin_amdgcn_mfma_f32_16x16x32_bf16(emu_bf16x8 a, emu_bf16x8 b, emu_f32x4 c, int, int,
-                                                         int) {
-    uint16_t ab[16];
-    std::memcpy(ab, &a, 16);
-    std::memcpy(ab + 8, &b, 16);
-    uint64_t mine[4];
-    std::memcpy(mine, ab, 32);
-    uint16_t all[64][16];
-    for (int q = 0; q < 4; ++q) {
-        uint64_t got[64];
-        emu::wave_all(mine[q], got);
-        for (unsigned src = 0; src < 64; ++src) std::memcpy(&all[src][4 * q], &got[src], 8);
-    }
-    const unsigned l = emu::lane(), col = l & 15u;
-    emu_f32x4 d;
-    for (int r = 0; r < 4; ++r) {
-        const unsigned row = 4 * (l >> 4) + r;
-        float sum = c[r];
-        for (unsigned k = 0; k < 32; ++k)
-            sum += emu_bf16_to_f32(all[row + 16 * (k >> 3)][k & 7]) *
-                   emu_bf16_to_f32(all[col + 16 * (k >> 3)][8 + (k & 7)]);
-        d[r] = sum;
-    }
-    return d;
+// v_dot2c_f32_bf16: c + a.lo b.lo + a.hi b.hi in fp32 (bf16 products are exact
+// in fp32).
+typedef __bf16 emu_bf16x2 __attribute__((ext_vector_type(2)));
+inline float __builtin_amdgcn_fdot2_f32_bf16(emu_bf16x2 a, emu_bf16x2 b, float c, bool) {
+    uint16_t x[2], y[2];
+    std::memcpy(x, &a, 4);
+    std::memcpy(y, &b, 4);
+    return c + (__uint_as_float((uint32_t)x[0] << 16) * __uint_as_float((uint32_t)y[0] << 16) +
+                __uint_as_float((uint32_t)x[1] << 16) * __uint_as_float((uint32_t)y[1] << 16));
 }
-
 template <typename K, typename... A>
 inline void emu_launch(K kernel, dim3 g, dim3 b, A... args) {
     gridDim = {g.x, 1, 1};

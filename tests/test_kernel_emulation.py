@@ -9,7 +9,7 @@ is a heap block of exactly its size, so an access past any of them, or past
 the kernel's LDS block, fails the run with the offending source line. The
 outputs are compared with the known weights / exponents as well; the fused
 GEMV's y within the GPU tests' tolerance of a float64 product (the stand-in
-models the MFMA from its lane layout, and true wave ballots).
+gives true wave ballots, readlane and DPP).
 """
 import os
 import re
