@@ -1592,20 +1592,9 @@ __device__ __forceinline__ void chunk_range(const DevTensor& T, int64_t c, int64
     *nb = n;
 }
 
-__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* s_wsum) {
-    const uint32_t x = wave_scan_incl(v);
-    if ((threadIdx.x & 63) == 63) s_wsum[threadIdx.x >> 6] = x;
-    __syncthreads();
-    uint32_t t = 0;
-#pragma unroll
-    for (int k = 0; k < kWaves; ++k) t += s_wsum[k];
-    __syncthreads();
-    return t;
-}
-
 // Plan, one workgroup per tensor: chunk c (c < n_jobs) gets segments
-// base[c] .. base[c] + ceil(8 * nbytes / S) - 1, bchunk the chunk of every
-// 512th segment, and the header the segment length, the table's checksum,
+// base[c] .. base[c] + ceil(8 * nbytes / S) - 1, and the header the segment
+// length, the table's checksum,
 // and ok = 1 when the chunks lie back to back and the layout fits the index
 // (the entries step writes only then; the finish step may clear ok).
 __global__ __launch_bounds__(kThreads) void index_plan_kernel(const LaunchArgs args) {
@@ -1621,7 +1610,6 @@ __global__ __launch_bounds__(kThreads) void index_plan_kernel(const LaunchArgs a
     if (threadIdx.x == 0) s_bad = fits ? 0u : 1u;
     __syncthreads();
     uint32_t* const base = reinterpret_cast<uint32_t*>(ix + L.base);
-    uint32_t* const bchunk = reinterpret_cast<uint32_t*>(ix + L.bchunk);
     uint64_t run = 0;
     for (int64_t c0 = 0; c0 < T.n_chunks; c0 += kThreads) {
         const int64_t c = c0 + threadIdx.x;
@@ -1638,14 +1626,7 @@ __global__ __launch_bounds__(kThreads) void index_plan_kernel(const LaunchArgs a
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) tot += s_wsum[w];
         const uint64_t at = run + excl;
-        if (fits && c < T.n_chunks) {
-            base[c] = static_cast<uint32_t>(at < kNoIndex ? at : kNoIndex - 1u);
-            // bchunk[m] = c for the 512-segment blocks that start in this chunk.
-            if (nseg != 0)
-                for (uint64_t m = (at + kIndexBlock - 1) / kIndexBlock;
-                     m * kIndexBlock < at + nseg && m < L.n_bchunk; ++m)
-                    bchunk[m] = static_cast<uint32_t>(c);
-        }
+        if (fits && c < T.n_chunks) base[c] = static_cast<uint32_t>(at < kNoIndex ? at : kNoIndex - 1u);
         run += tot;
         __syncthreads();  // s_wsum is written again by the next block's scan
     }
@@ -1690,7 +1671,9 @@ __device__ __forceinline__ uint32_t codeword_len_at(const uint8_t* table, const 
 // is found from the entries' counts; its end is the chunk's real end rend,
 // that segment keeps only the codewords up to it and later segments none.
 // A chunk with fewer than lim codewords, or whose lim-th codeword runs past
-// its bytes, makes the index unusable.
+// its bytes, makes the index unusable. The round starts (segments 512 m)
+// that fall in the chunk are written too: with the counts so fixed, the
+// codewords before segment g of the chunk are min(raw count before g, lim).
 __global__ __launch_bounds__(256) void index_finish_kernel(const LaunchArgs args, int64_t total) {
     __shared__ uint32_t s_wsum[kWaves];
     __shared__ uint32_t s_found;
@@ -1707,6 +1690,7 @@ __global__ __launch_bounds__(256) void index_finish_kernel(const LaunchArgs args
         const uint32_t* base = reinterpret_cast<const uint32_t*>(ix + L.base);
         uint32_t* rend = reinterpret_cast<uint32_t*>(ix + L.rend);
         uint16_t* ent = reinterpret_cast<uint16_t*>(ix + L.entries);
+        RoundStart* rounds = reinterpret_cast<RoundStart*>(ix + L.rounds);
         const uint32_t b0 = base[c], b1 = base[c + 1];
         int64_t off, nb;
         chunk_range(T, c, &off, &nb);
@@ -1729,6 +1713,15 @@ __global__ __launch_bounds__(256) void index_finish_kernel(const LaunchArgs args
                 tot += s_wsum[k];
             }
             const uint32_t excl = pre + before + x - cnt;  // codewords before segment g
+            if (g < b1 && g % kIndexBlock == 0 && g / kIndexBlock < L.n_rounds) {
+                RoundStart rs;
+                rs.chunk = static_cast<uint32_t>(c);
+                rs.element = static_cast<uint32_t>(c * T.chunk_size +
+                                                   (excl < static_cast<uint64_t>(lim) ? excl : lim));
+                rs.byte = static_cast<uint32_t>(off + (g - b0) * (S / 8));
+                rs.chunk_base = b0;
+                rounds[g / kIndexBlock] = rs;
+            }
             if (g < b1) {
                 if (excl < static_cast<uint64_t>(lim) && excl + cnt >= static_cast<uint64_t>(lim)) {
                     // The lim-th codeword is in this segment: walk to its end.
@@ -1930,41 +1923,36 @@ __device__ __forceinline__ void block_scan_sum_max(uint32_t u, uint32_t v, uint3
 // Segments [s_lo, s_hi) of tensor T (usable index, table in LDS).
 template <int kMode, int kGroup>
 __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const LaunchArgs& args,
-                          const DevTensor& T, uint32_t s_lo, uint32_t s_hi) {
+                          const DevTensor& T, uint32_t s_lo, uint32_t s_hi, const uint8_t* table) {
     const uint32_t tid = threadIdx.x;
     const uint32_t S = segment_bits(tb.min_len);
     const IndexLayout L = index_layout(T.packed_nbytes, T.n_chunks, S);
     const uint8_t* const ix = uniform(T.index);
-    const ConstU32 base = (ConstU32)(ix + L.base);
-    const ConstU32 bchunk = (ConstU32)(ix + L.bchunk);
     const uint32_t n_jobs = static_cast<uint32_t>(T.n_jobs);
-    // The chunk of segment s_lo.
-    uint32_t c0 = bchunk[s_lo / kIndexBlock];
-    c0 = c0 < n_jobs ? c0 : n_jobs - 1;
-    while (c0 + 1 < n_jobs && base[c0 + 1] <= s_lo) ++c0;
-    // Output element of the piece's first symbol: its chunk's first element
-    // plus the codewords of the chunk's segments before s_lo.
-    const uint32_t cb0 = base[c0];
-    uint32_t pre = 0;
-    {
-        const __amdgpu_buffer_rsrc_t re = index_part(T, L.entries, 2 * L.capacity);
-        for (uint32_t g = cb0 + tid; g < s_lo; g += kThreads)
-            pre += __builtin_amdgcn_raw_buffer_load_b16(re, 2 * g, 0, 0) >> 4;
+    // Where the piece starts (s_lo is a round start, a multiple of 512): its
+    // chunk, the output element of its first symbol and its packed byte.
+    static_assert(sizeof(RoundStart) == sizeof(v4u32), "a round start is one 16-byte load");
+    const v4u32 rs = load_uniform(reinterpret_cast<const v4u32*>(ix + L.rounds) + s_lo / kIndexBlock);
+    const uint32_t rs_chunk = rs[0], rs_element = rs[1], rs_byte = rs[2];  // RoundStart fields
+    RunPos P;
+    P.c0 = rs_chunk < n_jobs ? rs_chunk : n_jobs - 1;
+    P.g0 = s_lo;
+    P.A0 = rs_byte;
+    int64_t ob = rs_element;  // next symbol's element
+    // The first round's words are requested first; the table (when this
+    // piece's differs from the one in LDS) and the cleared stage are
+    // written while they arrive.
+    RunFetch F;
+    run_fetch_issue(F, T, L, P, s_hi, tid);
+    if (table != nullptr) {
+        __syncthreads();  // every thread is done with the previous table
+        load_table(table, tid, lds.wsyms, lds.wmeta, lds.len, lds.esc);
     }
-    pre = block_sum(pre, lds.wsum);
-    int64_t ob = static_cast<int64_t>(c0) * T.chunk_size + pre;  // next symbol's element
     // The stage is zero wherever nothing is placed.
     for (uint32_t j = tid; j < kRunStageBytes / 16; j += kThreads)
         reinterpret_cast<uint4*>(lds.stage)[j] = make_uint4(0u, 0u, 0u, 0u);
     for (uint32_t j = tid; j < 2 * kThreads; j += kThreads) (&lds.mark[0][0])[j] = 0;
     __syncthreads();
-
-    RunPos P;
-    P.c0 = c0;
-    P.g0 = s_lo;
-    P.A0 = static_cast<uint32_t>(T.offsets[c0]) + (s_lo - cb0) * (S / 8);
-    RunFetch F;
-    run_fetch_issue(F, T, L, P, s_hi, tid);
     run_fetch_commit(F, T, P, tid, lds, 0);
     __syncthreads();
 
@@ -2154,16 +2142,19 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void run_kernel(const Laun
         tb.min_len = hdr->min_len >= 1 ? hdr->min_len : 1u;
         tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(table + kEscOffset);
         const bool global_esc = hdr->n_esc_blocks > static_cast<uint32_t>(kLdsEscBlocks);
-        if (table != loaded) {
-            __syncthreads();  // every thread is done with the previous table
-            loaded = table;
-            load_table(table, tid, lds.wsyms, lds.wmeta, lds.len, lds.esc);
-            __syncthreads();
-        }
         if (G != 0 && a < b) {
+            // The piece loads the table itself, once its first words are
+            // requested.
             run_piece<kMode, kGroup>(lds, tb, global_esc, args, T, static_cast<uint32_t>(a),
-                                     static_cast<uint32_t>(b));
+                                     static_cast<uint32_t>(b), table != loaded ? table : nullptr);
+            loaded = table;
         } else if (G == 0 && c_lo < c_hi) {
+            if (table != loaded) {
+                __syncthreads();  // every thread is done with the previous table
+                loaded = table;
+                load_table(table, tid, lds.wsyms, lds.wmeta, lds.len, lds.esc);
+                __syncthreads();
+            }
             run_fallback<kMode>(tb, args, T, c_lo, c_hi);
         }
         at += U;

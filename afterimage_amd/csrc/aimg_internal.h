@@ -8,7 +8,7 @@
 
 namespace aimg {
 
-constexpr int kAbiVersion = 9;
+constexpr int kAbiVersion = 10;
 constexpr uint32_t kTableMagic = 0x474D4941u;  // "AIMG"
 
 // Window table: for each 12-bit window, the codewords that lie wholly inside
@@ -72,11 +72,12 @@ inline size_t table_nbytes() {
 // to lim and the tensor's symbols run on from chunk to chunk.
 // Layout (index_layout): the header, uint32 base[n_chunks + 1] (entries
 // past n_jobs repeat the total), uint32 rend[n_chunks], uint16
-// entries[capacity], and uint32 bchunk[n_bchunk]: the chunk of segment
-// 512 * m. The index is usable (ok == 1) only when the chunks lie back to
-// back in the packed buffer, every chunk holds its lim codewords within its
-// bytes, and everything fits; seg_bits and the table checksum tie it to
-// the table it was built with.
+// entries[capacity], and RoundStart rounds[n_rounds]: where segment 512 * m
+// starts (a segment run begins at such a segment). The index is usable
+// (ok == 1) only when the chunks lie back to back in the packed buffer,
+// every chunk holds its lim codewords within its bytes, and everything
+// fits; seg_bits and the table checksum tie it to the table it was built
+// with.
 constexpr uint32_t kIndexMagic = 0x32444941u;  // "AID2"
 
 struct IndexHeader {
@@ -93,11 +94,22 @@ struct IndexHeader {
 static_assert(sizeof(IndexHeader) == 64, "index header is 64 bytes");
 
 struct IndexLayout {
-    uint64_t base, rend, entries, bchunk, total;
-    uint64_t capacity, n_bchunk;
+    uint64_t base, rend, entries, rounds, total;
+    uint64_t capacity, n_rounds;
 };
 
-// Segments one bchunk entry spans (one round of a whole workgroup).
+// Segment 512 * m of a tensor (m < n_segments / 512): its chunk, the output
+// element of its first codeword, the packed byte where its bits start, and
+// the chunk's first segment.
+struct RoundStart {
+    uint32_t chunk;
+    uint32_t element;
+    uint32_t byte;
+    uint32_t chunk_base;
+};
+static_assert(sizeof(RoundStart) == 16, "round start is 16 bytes");
+
+// Segments between two round starts (one round of a whole workgroup).
 constexpr uint32_t kIndexBlock = 512;
 
 // Byte offsets of the real ends and the entries of an index over n_chunks
@@ -120,12 +132,12 @@ constexpr IndexLayout index_layout(int64_t packed_nbytes, int64_t n_chunks, uint
     const uint64_t nc = n_chunks > 0 ? static_cast<uint64_t>(n_chunks) : 0u;
     const uint64_t s = seg_bits > 0 ? seg_bits : 1u;
     l.capacity = (8 * pb + s - 1) / s + nc;
-    l.n_bchunk = l.capacity / kIndexBlock + 2;
+    l.n_rounds = l.capacity / kIndexBlock + 2;
     l.base = sizeof(IndexHeader);
     l.rend = index_rend_at(n_chunks);
     l.entries = index_entries_at(n_chunks);
-    l.bchunk = (l.entries + 2 * l.capacity + 15) & ~uint64_t{15};
-    l.total = l.bchunk + 4 * l.n_bchunk;
+    l.rounds = (l.entries + 2 * l.capacity + 15) & ~uint64_t{15};
+    l.total = l.rounds + sizeof(RoundStart) * l.n_rounds;
     return l;
 }
 

@@ -79,22 +79,39 @@ def _expected_index(enc, seg):
 
 
 def _layout(t, seg):
-    """Byte offsets of the index arrays (header, bases, real ends, entries)."""
+    """Byte offsets of the index arrays (header, bases, real ends, entries,
+    round starts)."""
     n = t.n_chunks
     cap = -(-8 * int(t.packed.numel()) // seg) + n
     base = 64
     rend = base + 4 * (n + 1)
     entries = (rend + 4 * n + 15) & ~15
-    return base, rend, entries, cap
+    rounds = (entries + 2 * cap + 15) & ~15
+    return base, rend, entries, cap, rounds
 
 
 def _index_arrays(t, seg):
     ix = t.index.cpu().numpy()
     hdr = ix[:64].view(np.uint32)
     n = t.n_chunks
-    base, rend, entries, cap = _layout(t, seg)
+    base, rend, entries, cap, rounds = _layout(t, seg)
     return (hdr, ix[base: base + 4 * (n + 1)].view(np.uint32), ix[rend: rend + 4 * n].view(np.uint32),
-            ix[entries: entries + 2 * cap].view(np.uint16))
+            ix[entries: entries + 2 * cap].view(np.uint16),
+            ix[rounds: rounds + 16 * (cap // 512 + 2)].view(np.uint32).reshape(-1, 4))
+
+
+def _expected_rounds(enc, seg, bases, entries):
+    """Round starts: for segment g = 512 m, its chunk c, the output element
+    of its first codeword (c * chunk_size + the counts of the chunk's
+    segments before g), its packed byte and the chunk's first segment."""
+    out = []
+    counts = entries.astype(np.int64) >> 4
+    for g in range(0, len(entries), 512):
+        c = int(np.searchsorted(bases, g, side="right")) - 1
+        el = c * int(enc.chunk_size) + int(counts[bases[c]: g].sum())
+        byte = int(enc.chunk_offsets[c]) + (g - int(bases[c])) * (seg // 8)
+        out.append((c, el, byte, int(bases[c])))
+    return np.asarray(out, np.int64).reshape(-1, 4)
 
 
 @pytest.mark.parametrize("kind,chunk", [("skewed", 64), ("skewed", 1024), ("bf16", 4096),
@@ -111,7 +128,7 @@ def test_index_entries_equal_a_cpu_walk_of_the_codeword_starts(kind, chunk):
     enc = encode_chunked(exps, chunk_size=chunk)
     t = DeviceTensor.from_encoded(enc, None, DEV).build_index()
     seg = segment_bits(t.tables.host_blob)
-    hdr, bases, rends, entries = _index_arrays(t, seg)
+    hdr, bases, rends, entries, rounds = _index_arrays(t, seg)
     want_b, want_r, want_e = _expected_index(enc, seg)
     assert hdr[2] == seg and hdr[4] == 1, "header: seg_bits %d ok %d" % (hdr[2], hdr[4])
     assert hdr[6] == len(want_e), "segments %d, want %d" % (hdr[6], len(want_e))
@@ -121,6 +138,8 @@ def test_index_entries_equal_a_cpu_walk_of_the_codeword_starts(kind, chunk):
     got = entries[: len(want_e)]
     bad = np.nonzero(got != want_e)[0]
     assert bad.size == 0, "entries differ at %s: %s vs %s" % (bad[:5], got[bad[:5]], want_e[bad[:5]])
+    want_rs = _expected_rounds(enc, seg, want_b, want_e)
+    assert np.array_equal(rounds[: len(want_rs)].astype(np.int64), want_rs)
     assert np.array_equal(decode_u8([t])[0].cpu().numpy(), exps.numpy().astype(np.uint8))
 
 

@@ -266,11 +266,12 @@ def test_index_size_is_two_bytes_per_segment_plus_chunk_tables():
     assert lib.aimg_index_nbytes(blob.ctypes.data, packed, chunks, ctypes.byref(n)) == 0
     # 64-byte header, first segment (chunks + 1) and real end (chunks) of
     # each chunk, 2 bytes per segment of the packed bytes (one partial
-    # segment per chunk), and the chunk of every 512th segment.
+    # segment per chunk), and 16 bytes for every 512th segment (where a
+    # segment run may start: chunk, element, byte, chunk's first segment).
     cap = -(-8 * packed // seg) + chunks
     entries_at = (64 + 4 * (chunks + 1) + 4 * chunks + 15) & ~15
-    bchunk_at = (entries_at + 2 * cap + 15) & ~15
-    assert n.value == bchunk_at + 4 * (cap // 512 + 2)
+    rounds_at = (entries_at + 2 * cap + 15) & ~15
+    assert n.value == rounds_at + 16 * (cap // 512 + 2)
     assert n.value < 2.05 * cap + 12 * chunks + 128
     bad = blob.copy()
     bad[0] ^= 1
