@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before the library; see module doc)
 
 LIB_PATH = Path(__file__).resolve().parent / "libafterimage_decode.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 MAX_TENSORS = 32
 
 AIMG_OK = 0

@@ -527,33 +527,23 @@ struct Job {
     uint32_t nb;   // chunk bytes
     uint32_t lim;  // output symbols of the chunk
     uint32_t nr;   // rounds
-    uint32_t ib;   // index entry of the chunk's first segment, or kNoIndex
-    uint32_t rend; // with the index: the chunk's real end in bits
+    uint32_t ib;   // index build: the chunk's first segment, or kNoIndex
 };
 
 // Index build: whether the plan step gave tensor T's index its chunk bases
-// and found room for every entry (entries are written only then). Decode:
-// whether the index is usable with T's table (built for it: segment length,
-// checksum; complete; laid out for this tensor). The same for every
-// sub-group of an item.
-template <int kMode>
-__device__ __forceinline__ bool index_usable(const DevTensor& T, uint32_t S) {
+// and found room for every entry (entries are written only then). The same
+// for every sub-group of an item.
+__device__ __forceinline__ bool index_build_ready(const DevTensor& T) {
     const uint8_t* ix = uniform(T.index);
     if (ix == nullptr) return false;
     const auto* h = (const __attribute__((address_space(4))) IndexHeader*)(ix);
-    if (h->magic != kIndexMagic || h->ok != 1u) return false;
-    if (kMode == kModeIndex) return true;
-    return h->version == static_cast<uint32_t>(kAbiVersion) && h->seg_bits == S &&
-           h->table_checksum == header_of(uniform(T.table))->checksum &&
-           h->n_chunks == static_cast<uint32_t>(T.n_chunks) &&
-           h->n_jobs == static_cast<uint32_t>(T.n_jobs) &&
-           index_entries_at(T.n_chunks) <= T.index_n32;
+    return h->magic == kIndexMagic && h->ok == 1u;
 }
 
 // kLg > 0: every tensor of the launch has 1 << kLg threads per chunk.
 template <int kMode, uint32_t kLg>
 __device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, uint32_t tid) {
-    Job J{-1, 0u, kMaxSegBits, 0, 0u, 0u, 0u, 0u, kNoIndex, 0u};
+    Job J{-1, 0u, kMaxSegBits, 0, 0u, 0u, 0u, 0u, kNoIndex};
     if (item >= args.total_items) return J;
     int d = 0;
     while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
@@ -564,35 +554,31 @@ __device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, ui
     J.c = (item - T.item_begin) * n_groups + (tid >> J.lg);
     // Segment length: at most kSlotCap codewords of the shortest length.
     J.S = segment_bits(header_of(uniform(T.table))->min_len);
-    const bool use_ix = index_usable<kMode>(T, J.S);
+    // Decodes never use the index here (segment runs do).
+    const bool use_ix = kMode == kModeIndex && index_build_ready(T);
     const uint8_t* const ixp = use_ix ? uniform(T.index) : nullptr;
     const __attribute__((address_space(4))) uint32_t* ix_base =
         (const __attribute__((address_space(4))) uint32_t*)(ixp + sizeof(IndexHeader));
-    const __attribute__((address_space(4))) uint32_t* ix_rend =
-        (const __attribute__((address_space(4))) uint32_t*)(ixp + index_rend_at(T.n_chunks));
     // A wave holds 64 >> lg sub-groups (one when lg >= 6), on consecutive
     // chunks. Their offsets and lengths come through scalar loads, so no wait
     // for them waits for the vector stores in flight; each lane keeps its own.
     const int64_t c_wave = (item - T.item_begin) * n_groups + (uniform(tid & ~63u) >> J.lg);
     const uint32_t per_wave = J.lg >= 6 ? 1u : 64u >> J.lg;
     int64_t off = 0, nb = 0;
-    uint32_t ib = 0, re = 0;
+    uint32_t ib = 0;
 #pragma unroll
     for (uint32_t k = 0; k < 64 / kMinTpc; ++k) {
         if (k < per_wave && c_wave + k < T.n_jobs) {
             const int64_t o = load_uniform(T.offsets + c_wave + k);
             const int64_t n = load_uniform(T.nbytes + c_wave + k);
             const uint32_t b = use_ix ? ix_base[c_wave + k] : 0u;
-            const uint32_t e = use_ix && kMode != kModeIndex ? ix_rend[c_wave + k] : 0u;
             if (J.c == c_wave + k) {
                 off = o;
                 nb = n;
                 ib = b;
-                re = e;
             }
         }
     }
-    J.rend = re;
     // kNoIndex marks "no index" for the whole item, so no entry may equal it.
     J.ib = use_ix ? (ib < kNoIndex ? ib : kNoIndex - 1u) : kNoIndex;
     if (J.c < T.n_jobs) {
@@ -621,7 +607,6 @@ __device__ __forceinline__ uint32_t round_len(const Job& J, uint32_t r) {
 // are written to the LDS tile: words k * tpc + i of the round.
 struct Fetch {
     uint32_t raw[kTileBatch];
-    uint32_t ent;  // with the index: the entry of the thread's segment
 };
 
 // The part of tensor T's index at [at, at + n) as a buffer (reads past it
@@ -654,11 +639,6 @@ __device__ __forceinline__ void fetch_issue(Fetch& F, const LaunchArgs& args, co
     if (round_len(J, r) == 0) return;
     const DevTensor& T = args.t[J.d];
     const uint32_t tpc = 1u << J.lg;
-    if (kMode != kModeIndex && !kTiny && J.ib != kNoIndex) {
-        const uint64_t at = index_entries_at(T.n_chunks);
-        F.ent = __builtin_amdgcn_raw_buffer_load_b16(index_part(T, at, T.index_n32 - at),
-                                                     2u * (J.ib + r * tpc + (tid & (tpc - 1))), 0, 0);
-    }
     const uint32_t b0 = ((r * J.S) << J.lg) / 8 + 4 * (tid & (tpc - 1));
     // All words are requested before any is used; words past the chunk read
     // an in-buffer word and are zeroed when written.
@@ -687,7 +667,6 @@ __device__ __forceinline__ void fetch_commit(const Fetch& F, const LaunchArgs& a
                                              uint32_t r, uint32_t tid, uint32_t* s_tile) {
 #pragma unroll
     for (uint32_t k = 0; k < kTileBatch; ++k) consume(F.raw[k]);
-    consume(F.ent);
     const uint32_t RB = round_len(J, r);
     if (RB == 0) return;
     const DevTensor& T = args.t[J.d];
@@ -1316,96 +1295,6 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
 
         int64_t ob = 0;     // chunk-local symbols placed so far
         uint32_t lead = 0;  // placed symbols still staged at the front of the region
-        // Chunks with a usable segment index (the same for the whole item).
-        const bool use_idx = kMode != kModeIndex && !kTiny && uniform(cur.ib) != kNoIndex;
-        if (use_idx) {
-            // Each segment's first boundary and codeword count come from the
-            // index, so the round's placement is known before it decodes:
-            // each thread decodes from its true start up to its segment's
-            // end or the chunk's real end, and ORs its symbols straight into
-            // their place in the stage area, which is zero wherever nothing
-            // is placed. No look-ahead, agreement check or compaction.
-            for (uint32_t j = tid; j < kStageBytes / 16; j += kThreads)
-                reinterpret_cast<uint4*>(s_stage)[j] = make_uint4(0u, 0u, 0u, 0u);
-            for (uint32_t r = 0; r < NR; ++r) {
-                uint32_t i = i_item;
-                asm volatile("" : "+v"(i));
-                const bool last = r + 1 == NR;
-                const Job& fj = last ? nxt : cur;
-                const uint32_t fr = last ? 0u : r + 1;
-                const uint32_t ent = F.ent;  // this round's entry, fetched with its words
-                __builtin_amdgcn_s_setprio(3);
-                fetch_issue<kMode, kTiny>(F, args, fj, fr, tid);
-                SmBatch<kMode> smb;
-                sm_issue<kMode, kGroup>(smb, T, chunk_base + ob - lead, i, tpc);
-                const uint32_t RB = round_len(cur, r);
-                const bool g_active = RB != 0;
-                // The round's bits up to the chunk's real end.
-                const uint32_t r_at = (r * S) << lg;
-                const uint32_t R_end = cur.rend > r_at ? (cur.rend - r_at < RB ? cur.rend - r_at : RB) : 0u;
-                const uint32_t seg_lo = i * S;
-                const bool active = seg_lo < R_end;
-                const uint32_t seg_hi = active ? (seg_lo + S < R_end ? seg_lo + S : R_end) : 0u;
-                // Counts above kSlotCap only come from a foreign index; the
-                // clamp keeps every placement inside the stage area.
-                const uint32_t ecnt = ent >> 4;
-                const uint32_t cnt = active ? (ecnt < kSlotCap ? ecnt : kSlotCap) : 0u;
-                __builtin_amdgcn_s_setprio(1);
-                const uint32_t excl = block_scan_excl(cnt, s_wsum);
-                if (i == 0) s_gpre[g] = excl;
-                if (tid == kThreads - 1) s_gpre[n_groups] = excl + cnt;
-                __syncthreads();
-                const uint32_t o = excl - s_gpre[g];
-                const uint32_t gtot = s_gpre[g + 1] - s_gpre[g];
-                const int64_t still = lim - ob;
-                const uint32_t want =
-                    g_active ? (gtot < still ? gtot : static_cast<uint32_t>(still > 0 ? still : 0)) : 0u;
-                const uint32_t avail = lead + want;
-                const uint32_t nfull = avail / kGroup;
-                const int64_t a0 = chunk_base + ob - lead;
-                __builtin_amdgcn_s_setprio(0);
-                if (active) {
-                    const uint32_t f = seg_lo + (ent & 15u);
-                    uint8_t* dst = stage + lead + o;
-                    if (global_esc) {
-                        decode_placed<true>(below, tb, f, seg_hi, dst);
-                    } else {
-                        decode_placed<false>(below, tb, f, seg_hi, dst);
-                    }
-                }
-                __syncthreads();  // the round is placed; the tile takes the next words
-                fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
-                __builtin_amdgcn_s_setprio(2);
-                store_round<kMode, kGroup, kLg == kLgThreads>(smb, T, args.gemv, stage, a0, nfull,
-                                                              i, tpc);
-                ob += want;
-                // The partial vector group (rem < 16 bytes at a multiple of
-                // kGroup) moves to the front; all else placed is cleared.
-                const uint32_t rem = avail - nfull * kGroup;
-                uint2 k0 = make_uint2(0u, 0u), k1 = make_uint2(0u, 0u);
-                if (i == 0 && rem != 0) {
-                    const uint2* src = reinterpret_cast<const uint2*>(stage + nfull * kGroup);
-                    k0 = src[0];
-                    k1 = src[1];
-                    const uint64_t a = static_cast<uint64_t>(k0.x) | static_cast<uint64_t>(k0.y) << 32;
-                    const uint64_t bb = static_cast<uint64_t>(k1.x) | static_cast<uint64_t>(k1.y) << 32;
-                    const uint64_t am = rem >= 8 ? a : a & ((uint64_t{1} << (8 * rem)) - 1);
-                    const uint64_t bm = rem <= 8 ? 0 : bb & ((uint64_t{1} << (8 * (rem - 8))) - 1);
-                    k0 = make_uint2(static_cast<uint32_t>(am), static_cast<uint32_t>(am >> 32));
-                    k1 = make_uint2(static_cast<uint32_t>(bm), static_cast<uint32_t>(bm >> 32));
-                }
-                const uint32_t placed = (lead + gtot + 4 + 15) & ~15u;
-                const uint32_t zend = placed < region ? placed : region;
-                __syncthreads();
-                for (uint32_t z = 16 + 16 * i; z < zend; z += 16 * tpc)
-                    *reinterpret_cast<uint4*>(stage + z) = make_uint4(0u, 0u, 0u, 0u);
-                if (i == 0) {
-                    reinterpret_cast<uint2*>(stage)[0] = k0;
-                    reinterpret_cast<uint2*>(stage)[1] = k1;
-                }
-                lead = rem;
-            }
-        } else {
         uint32_t p0 = 0;    // true start of the next round, relative to its first bit
         for (uint32_t r = 0; r < NR; ++r) {
             // Offsets derived from the thread index are cheap to recompute;
@@ -1485,9 +1374,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 // past its start) and codeword count; no output.
                 if (active && cur.ib != kNoIndex) {
                     const IndexLayout L = index_layout(T.packed_nbytes, T.n_chunks, S);
-                    __builtin_amdgcn_raw_buffer_store_b16(
-                        static_cast<uint16_t>((cnt << 4) | (f - seg_lo)),
-                        index_part(T, L.entries, 2 * L.capacity), 2u * (cur.ib + r * tpc + i), 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        (cnt << 4) | (f - seg_lo), index_part(T, L.entries, 4 * L.capacity),
+                        4u * (cur.ib + r * tpc + i), 0, 0);
                 }
                 fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
                 __syncthreads();
@@ -1555,7 +1444,6 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             if (i < rem) stage[i] = keep;
             lead = rem;
             if (g_active) p0 = e_last - RB;
-        }
         }
         if (NR == 0) {
             fetch_issue<kMode, kTiny>(F, args, nxt, 0, tid);
@@ -1631,7 +1519,20 @@ __global__ __launch_bounds__(kThreads) void index_plan_kernel(const LaunchArgs a
         __syncthreads();  // s_wsum is written again by the next block's scan
     }
     if (threadIdx.x == 0) {
-        if (fits) base[T.n_chunks] = static_cast<uint32_t>(run < kNoIndex ? run : kNoIndex - 1u);
+        if (fits) {
+            base[T.n_chunks] = static_cast<uint32_t>(run < kNoIndex ? run : kNoIndex - 1u);
+            // After the last round: the tensor's end (segment runs take a
+            // round's symbol count from the next round's first element).
+            const uint64_t m = (run + kIndexBlock - 1) / kIndexBlock;
+            if (m < L.n_rounds) {
+                RoundStart end;
+                end.chunk = static_cast<uint32_t>(T.n_jobs > 0 ? T.n_jobs - 1 : 0);
+                end.element = static_cast<uint32_t>(T.n_symbols);
+                end.byte = static_cast<uint32_t>(T.packed_nbytes);
+                end.chunk_base = static_cast<uint32_t>(run);
+                reinterpret_cast<RoundStart*>(ix + L.rounds)[m] = end;
+            }
+        }
         IndexHeader h{};
         h.magic = kIndexMagic;
         h.version = static_cast<uint32_t>(kAbiVersion);
@@ -1689,7 +1590,7 @@ __global__ __launch_bounds__(256) void index_finish_kernel(const LaunchArgs args
         const IndexLayout L = index_layout(T.packed_nbytes, T.n_chunks, S);
         const uint32_t* base = reinterpret_cast<const uint32_t*>(ix + L.base);
         uint32_t* rend = reinterpret_cast<uint32_t*>(ix + L.rend);
-        uint16_t* ent = reinterpret_cast<uint16_t*>(ix + L.entries);
+        uint32_t* ent = reinterpret_cast<uint32_t*>(ix + L.entries);
         RoundStart* rounds = reinterpret_cast<RoundStart*>(ix + L.rounds);
         const uint32_t b0 = base[c], b1 = base[c + 1];
         int64_t off, nb;
@@ -1701,7 +1602,7 @@ __global__ __launch_bounds__(256) void index_finish_kernel(const LaunchArgs args
         for (uint32_t g0 = b0; g0 < b1; g0 += 256) {
             const uint32_t g = g0 + threadIdx.x;
             const uint32_t e = g < b1 ? ent[g] : 0u;
-            const uint32_t cnt = e >> 4;
+            const uint32_t cnt = (e >> 4) & 127u;
             // Block scan (256 threads: waves 0..3).
             const uint32_t x = wave_scan_incl(cnt);
             __syncthreads();
@@ -1731,10 +1632,10 @@ __global__ __launch_bounds__(256) void index_finish_kernel(const LaunchArgs args
                     for (uint32_t k = 0; k < keep; ++k)
                         p += codeword_len_at(T.table, T.packed + off, static_cast<uint32_t>(nb), p);
                     rend[c] = p;
-                    ent[g] = static_cast<uint16_t>((e & 15u) | (keep << 4));
+                    ent[g] = (e & 15u) | (keep << 4);
                     s_found = p <= 8 * nb ? 1u : 2u;
                 } else if (excl >= static_cast<uint64_t>(lim)) {
-                    ent[g] = static_cast<uint16_t>(e & 15u);  // past the real end
+                    ent[g] = e & 15u;  // past the real end
                 }
             }
             pre += tot;
@@ -1771,21 +1672,60 @@ constexpr uint32_t kRunStageBytes =
         ? (kLeadBytes + kThreads * kSlotCap + 4 + 15) / 16 * 16
         : kStoreBatch * kThreads * 8;
 
+// Rounds, one workgroup per round of 512 segments (items numbered per
+// tensor from item_begin): each entry's count becomes its place in the
+// round (the counts of the round's segments before it, a block scan) and
+// its chunk's place in the round's chunk table (from the chunk bases).
+// Runs after the finish step, so the counts are final.
+__global__ __launch_bounds__(kThreads) void index_rounds_kernel(const LaunchArgs args,
+                                                                int64_t total) {
+    __shared__ uint32_t s_wsum[kWaves];
+    __shared__ uint32_t s_base[kRunChunks + 1];
+    const uint32_t tid = threadIdx.x;
+    for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+        int d = 0;
+        while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
+        const DevTensor& T = args.t[d];
+        const uint64_t m = static_cast<uint64_t>(item - T.item_begin);
+        uint8_t* const ix = T.index;
+        const auto* h = reinterpret_cast<const IndexHeader*>(ix);
+        const uint32_t G = h->n_segments;
+        if (h->magic != kIndexMagic || h->ok != 1u || m * kIndexBlock >= G) continue;
+        const IndexLayout L = index_layout(T.packed_nbytes, T.n_chunks, h->seg_bits);
+        const uint32_t* base = reinterpret_cast<const uint32_t*>(ix + L.base);
+        uint32_t* ent = reinterpret_cast<uint32_t*>(ix + L.entries);
+        const RoundStart* rounds = reinterpret_cast<const RoundStart*>(ix + L.rounds);
+        const uint32_t c0 = rounds[m].chunk;
+        if (tid <= kRunChunks)
+            s_base[tid] = c0 + tid <= static_cast<uint32_t>(T.n_chunks) ? base[c0 + tid] : kNoIndex;
+        const uint32_t g = static_cast<uint32_t>(m * kIndexBlock) + tid;
+        const uint32_t e = g < G ? ent[g] : 0u;
+        const uint32_t excl = block_scan_excl(g < G ? (e >> 4) & 127u : 0u, s_wsum);
+        // The last chunk of the table that starts at or before g (bases do
+        // not decrease; chunks without segments share their successor's).
+        uint32_t jj = 0;
+#pragma unroll
+        for (uint32_t step = kRunChunks / 2; step >= 1; step >>= 1)
+            if (jj + step < kRunChunks && s_base[jj + step] <= g) jj += step;
+        if (g < G)
+            ent[g] = (e & 15u) | (jj << kEntryJjShift) |
+                     ((excl < (kThreads - 1) * kSlotCap ? excl : (kThreads - 1) * kSlotCap)
+                      << kEntryExclShift);
+        __syncthreads();  // s_base and s_wsum are written again by the next item
+    }
+}
+
 struct __attribute__((aligned(16))) RunLds {
     uint8_t wmeta[kWinEntries];
     uint8_t len[256];
     uint16_t esc[kLdsEscBlocks * kEscBlockEntries];
     uint32_t wsyms[kWinEntries];
-    uint32_t wsum[kWaves];
-    uint32_t wmax[kWaves];
     // Chunks c0 .. c0 + kRunChunks - 1 of a round (c0: the chunk of its
     // first segment): first segment, byte offset, real end in bits. Two
     // sets, the current round's and the next one's.
     uint32_t cbase[2][kRunChunks];
     uint32_t coff[2][kRunChunks];
     uint32_t crend[2][kRunChunks];
-    // mark[i] = j when segment g0 + i is chunk c0 + j's first (j >= 1).
-    uint8_t mark[2][kThreads];
     uint32_t segs[AIMG_MAX_TENSORS];  // run_segments of each tensor of the launch
     uint32_t tile[kRunTileWords];
     __attribute__((aligned(16))) uint8_t stage[kRunStageBytes];
@@ -1815,14 +1755,28 @@ struct RunFetch {
     uint32_t raw[kTileBatch];
     uint32_t ent;
     uint32_t cb, co, cr;
+    v4u32 rn;  // the round start after the fetched round
 };
 
 struct RunPos {
     uint32_t c0;   // chunk of the round's first segment
     uint32_t g0;   // the round's first segment
     uint32_t A0;   // byte of the packed buffer where its bits start
+    uint32_t el;   // output element of its first symbol
 };
 
+// A round start (RoundStart) as the position of a round.
+__device__ __forceinline__ RunPos run_pos(v4u32 rs, uint32_t g0, uint32_t n_jobs) {
+    RunPos P;
+    P.c0 = uniform(rs[0] < n_jobs ? rs[0] : n_jobs - 1u);
+    P.g0 = g0;
+    P.A0 = uniform(rs[2]);
+    P.el = uniform(rs[1]);
+    return P;
+}
+
+// Requests the words of the round at P, each thread's entry, the round's
+// chunk table and the next round's start.
 __device__ __forceinline__ void run_fetch_issue(RunFetch& F, const DevTensor& T,
                                                 const IndexLayout& L, const RunPos& P,
                                                 uint32_t s_hi, uint32_t tid) {
@@ -1834,8 +1788,8 @@ __device__ __forceinline__ void run_fetch_issue(RunFetch& F, const DevTensor& T,
         F.raw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, word_at(A, last), 0, 0);
     }
     const uint32_t g = P.g0 + tid;
-    F.ent = g < s_hi ? __builtin_amdgcn_raw_buffer_load_b16(
-                           index_part(T, L.entries, 2 * L.capacity), 2 * g, 0, 0)
+    F.ent = g < s_hi ? __builtin_amdgcn_raw_buffer_load_b32(
+                           index_part(T, L.entries, 4 * L.capacity), 4 * g, 0, 0)
                      : 0u;
     // Every wave loads the table (each lane one chunk, the same addresses in
     // every wave), so each wave has the same loads in flight and the waits
@@ -1849,11 +1803,13 @@ __device__ __forceinline__ void run_fetch_issue(RunFetch& F, const DevTensor& T,
     F.cr = __builtin_amdgcn_raw_buffer_load_b32(index_part(T, L.rend, 4 * T.n_chunks), 4 * c, 0, 0);
     F.co = __builtin_amdgcn_raw_buffer_load_b32(
         buffer_of(T.offsets, static_cast<uint32_t>(4 * T.n_chunks)), 4 * c, 0, 0);
+    F.rn = __builtin_amdgcn_raw_buffer_load_b128(
+        index_part(T, L.rounds, sizeof(RoundStart) * L.n_rounds),
+        static_cast<uint32_t>(sizeof(RoundStart)) * (P.g0 / kIndexBlock + 1), 0, 0);
 }
 
 // The fetched words into the tile (big-endian, bytes past the packed
-// buffer zero), and the chunk table and chunk-start marks of the round into
-// set `b`.
+// buffer zero), and the chunk table of the round into set `b`.
 __device__ __forceinline__ void run_fetch_commit(const RunFetch& F, const DevTensor& T,
                                                  const RunPos& P, uint32_t tid, RunLds& lds,
                                                  uint32_t b) {
@@ -1863,6 +1819,8 @@ __device__ __forceinline__ void run_fetch_commit(const RunFetch& F, const DevTen
     consume(F.cb);
     consume(F.co);
     consume(F.cr);
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) consume(F.rn[k]);
     const uint32_t last = last_word(T);
     uint32_t* const top = lds.tile + kRunTileWords - 1;
 #pragma unroll
@@ -1876,48 +1834,10 @@ __device__ __forceinline__ void run_fetch_commit(const RunFetch& F, const DevTen
     }
     if (tid < kRunChunks) {
         const bool real = P.c0 + tid < static_cast<uint32_t>(T.n_jobs);
-        const uint32_t cb = real ? F.cb : kNoIndex;
-        lds.cbase[b][tid] = cb;
+        lds.cbase[b][tid] = real ? F.cb : kNoIndex;
         lds.coff[b][tid] = F.co;
         lds.crend[b][tid] = F.cr;
-        // Chunk c0 + tid starts inside the round: mark its first segment.
-        if (tid >= 1 && cb >= P.g0 && cb < P.g0 + kThreads)
-            lds.mark[b][cb - P.g0] = static_cast<uint8_t>(tid);
     }
-}
-
-__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
-
-// Inclusive max over the workgroup of v (every thread), and the exclusive
-// sum of u, with one barrier.
-__device__ __forceinline__ void block_scan_sum_max(uint32_t u, uint32_t v, uint32_t* s_wsum,
-                                                   uint32_t* s_wmax, uint32_t* excl,
-                                                   uint32_t* vmax, uint32_t* sum_all) {
-    const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
-    const uint32_t x = wave_scan_incl(u);
-    uint32_t m = v;
-    m = umax(m, dpp<0x111>(m));
-    m = umax(m, dpp<0x112>(m));
-    m = umax(m, dpp<0x114>(m));
-    m = umax(m, dpp<0x118>(m));
-    m = umax(m, dpp<0x142, 0xA>(m));
-    m = umax(m, dpp<0x143, 0xC>(m));
-    if (lane == 63) {
-        s_wsum[w] = x;
-        s_wmax[w] = m;
-    }
-    __syncthreads();
-    uint32_t pre = 0, pm = 0, tot = 0;
-#pragma unroll
-    for (int k = 0; k < kWaves; ++k) {
-        pre += k < w ? s_wsum[k] : 0u;
-        pm = k < w ? umax(pm, s_wmax[k]) : pm;
-        tot += s_wsum[k];
-    }
-    *excl = pre + x - u;
-    *vmax = umax(pm, m);
-    *sum_all = tot;
 }
 
 // Segments [s_lo, s_hi) of tensor T (usable index, table in LDS).
@@ -1933,12 +1853,7 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
     // chunk, the output element of its first symbol and its packed byte.
     static_assert(sizeof(RoundStart) == sizeof(v4u32), "a round start is one 16-byte load");
     const v4u32 rs = load_uniform(reinterpret_cast<const v4u32*>(ix + L.rounds) + s_lo / kIndexBlock);
-    const uint32_t rs_chunk = rs[0], rs_element = rs[1], rs_byte = rs[2];  // RoundStart fields
-    RunPos P;
-    P.c0 = rs_chunk < n_jobs ? rs_chunk : n_jobs - 1;
-    P.g0 = s_lo;
-    P.A0 = rs_byte;
-    int64_t ob = rs_element;  // next symbol's element
+    RunPos P = run_pos(rs, s_lo, n_jobs);
     // The first round's words are requested first; the table (when this
     // piece's differs from the one in LDS) and the cleared stage are
     // written while they arrive.
@@ -1951,48 +1866,35 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
     // The stage is zero wherever nothing is placed.
     for (uint32_t j = tid; j < kRunStageBytes / 16; j += kThreads)
         reinterpret_cast<uint4*>(lds.stage)[j] = make_uint4(0u, 0u, 0u, 0u);
-    for (uint32_t j = tid; j < 2 * kThreads; j += kThreads) (&lds.mark[0][0])[j] = 0;
-    __syncthreads();
     run_fetch_commit(F, T, P, tid, lds, 0);
-    __syncthreads();
 
     TileRef below = (TileRef)(lds.tile + kRunTileWords - 2);
     asm volatile("" : "+v"(below));
     uint8_t* const stage = lds.stage;
-    uint32_t lead = static_cast<uint32_t>(ob & (kGroup - 1));  // symbols staged before the round's
+    uint32_t lead = P.el & (kGroup - 1);  // symbols staged before the round's
     uint32_t skip = lead;  // of those, the ones another piece writes
     uint32_t r = 0;
     for (uint32_t g0 = s_lo; g0 < s_hi; g0 += kThreads, ++r) {
         const uint32_t b = r & 1u;
+        // This round's entry, and the next round's start (both fetched with
+        // this round's words): the next round's words are requested first.
         const uint32_t ent = F.ent;
-        const uint32_t m = lds.mark[b][tid];
-        // The next round's first segment gn: its chunk is the last of the
-        // table's chunks that start at or before it (every wave counts them,
-        // one table entry a lane), so its words are requested before the
-        // round's scan, like the next round's of a chunk.
-        static_assert(kRunChunks == 64, "one table entry per lane of a wave");
-        const uint32_t lane = tid & 63u;
         const uint32_t gn = g0 + kThreads;
-        const uint32_t jn = static_cast<uint32_t>(
-            __builtin_popcountll(__ballot(lane >= 1 && lds.cbase[b][lane] <= gn)));
-        RunPos N;
-        N.c0 = P.c0 + jn;
-        N.g0 = gn;
-        N.A0 = uniform(lds.coff[b][jn] + (gn - lds.cbase[b][jn]) * (S / 8));
+        const RunPos N = run_pos(F.rn, gn, n_jobs);
         __builtin_amdgcn_s_setprio(3);
         if (gn < s_hi) run_fetch_issue(F, T, L, N, s_hi, tid);
-        const int64_t a0 = ob - lead;
+        const int64_t a0 = static_cast<int64_t>(P.el) - lead;
         SmBatch<kMode> smb;
         sm_issue<kMode, kGroup>(smb, T, a0, tid, kThreads);
-        lds.mark[b][tid] = 0;
         const uint32_t g = g0 + tid;
         const bool active = g < s_hi;
-        const uint32_t ecnt = ent >> 4;
-        const uint32_t cnt = active ? (ecnt < kSlotCap ? ecnt : kSlotCap) : 0u;
-        __builtin_amdgcn_s_setprio(1);
-        uint32_t excl, jj, gtot;
-        block_scan_sum_max(cnt, m, lds.wsum, lds.wmax, &excl, &jj, &gtot);
-        jj = jj < kRunChunks ? jj : kRunChunks - 1;
+        // Entries above the round's room only come from an index that does
+        // not describe the tensor; the clamps keep every access in bounds.
+        const uint32_t ex = ent >> kEntryExclShift;
+        const uint32_t excl = ex < (kThreads - 1) * kSlotCap ? ex : (kThreads - 1) * kSlotCap;
+        const uint32_t jj = (ent >> kEntryJjShift) & (kRunChunks - 1);
+        const uint32_t gtot0 = N.el - P.el;
+        const uint32_t gtot = gtot0 < kThreads * kSlotCap ? gtot0 : kThreads * kSlotCap;
         const uint32_t avail = lead + gtot;
         // Whole groups, never past the tensor's end (only an index that does
         // not describe the tensor could place symbols there).
@@ -2000,6 +1902,7 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
         const uint32_t nfull = room < static_cast<int64_t>(avail / kGroup)
                                    ? static_cast<uint32_t>(room > 0 ? room : 0)
                                    : avail / kGroup;
+        __syncthreads();  // the stage is clear; the tile and chunk table hold this round's
         // This thread's segment: chunk c0 + jj, segment g - base of it.
         const uint32_t cbase = lds.cbase[b][jj];
         const uint32_t coff = lds.coff[b][jj];
@@ -2023,7 +1926,6 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
         __builtin_amdgcn_s_setprio(2);
         store_round<kMode, kGroup, true>(smb, T, args.gemv, stage, a0, nfull, tid, kThreads, skip);
         if (nfull != 0) skip = 0;
-        ob += gtot;
         // The partial vector group (rem < 16 bytes at a multiple of kGroup)
         // moves to the front; all else placed is cleared.
         const uint32_t rem0 = avail - nfull * kGroup;
@@ -2055,7 +1957,8 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
     // The symbols still staged (those of the piece's first group that
     // another piece writes excepted).
     __syncthreads();
-    if (tid >= skip && tid < lead) store_one<kMode>(T, args.gemv, ob - lead + tid, stage[tid]);
+    if (tid >= skip && tid < lead)
+        store_one<kMode>(T, args.gemv, static_cast<int64_t>(P.el) - lead + tid, stage[tid]);
     __syncthreads();
 }
 
@@ -2249,12 +2152,10 @@ int launch_run(Batch& B, hipStream_t s) {
 }
 
 // Tensors with a segment index (chunks of kRunMinChunk symbols or more, the
-// vector path's alignment) go to `run`, the segment-run kernel, when their
-// chunks take fewer than kThreads threads or `big_runs` says so; the others
-// decode chunk by chunk (with their index, when it is usable).
+// vector path's alignment) go to `run`, the segment-run kernel, when `run`
+// is given; the others decode chunk by chunk without it.
 template <int kMode>
-int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny, Batch* run = nullptr,
-               bool big_runs = false) {
+int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny, Batch* run = nullptr) {
     const std::string who = "tensor " + std::to_string(i) + ": ";
     if (t.chunk_size < 1) return fail(AIMG_ERR_INVALID_ARGUMENT, who + "chunk_size must be >= 1");
     if (t.n_chunks < 0 || t.n_symbols < 0 || t.packed_nbytes < 0)
@@ -2279,9 +2180,11 @@ int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny, Batch* r
     // An index smaller than its header, or misaligned, is not one.
     const bool has_index = t.index != nullptr && t.index_nbytes >= static_cast<int64_t>(sizeof(IndexHeader)) &&
                            reinterpret_cast<uintptr_t>(t.index) % 16 == 0;
+    // Decodes use the index only in segment runs; the index build is the
+    // chunk kernel's (kModeIndex) and is the one other user.
     const bool to_run = run != nullptr && has_index && t.chunk_size >= kRunMinChunk &&
-                        t.packed_nbytes >= 4 && vec_layout &&
-                        (threads_per_chunk(t.chunk_size) < static_cast<uint32_t>(kThreads) || big_runs);
+                        t.packed_nbytes >= 4 && vec_layout;
+    const bool keep_index = has_index && (to_run || kMode == kModeIndex);
     Batch& B = to_run ? *run : (t.packed_nbytes < 4 ? tiny : normal);
     if (!vec_layout) B.vec = false;
     DevTensor& dt = B.args.t[B.m++];
@@ -2297,8 +2200,8 @@ int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny, Batch* r
     dt.n_symbols = t.n_symbols;
     dt.chunk_size = t.chunk_size;
     dt.n_chunks = t.n_chunks;
-    dt.index = has_index ? static_cast<uint8_t*>(t.index) : nullptr;
-    dt.index_n32 = !has_index ? 0u
+    dt.index = keep_index ? static_cast<uint8_t*>(t.index) : nullptr;
+    dt.index_n32 = !keep_index ? 0u
                    : t.index_nbytes > static_cast<int64_t>(UINT32_MAX) ? UINT32_MAX
                    : static_cast<uint32_t>(t.index_nbytes);
     dt.tpc = static_cast<int32_t>(threads_per_chunk(t.chunk_size));
@@ -2323,30 +2226,15 @@ int launch(const aimg_tensor* ts, int n, const GemvArgs& gemv, bool vec_ok, void
     tiny.args.gemv = gemv;
     run.args.gemv = gemv;
     normal.vec = vec_ok;
-    // Chunks of a whole workgroup (kThreads threads) decode chunk by chunk,
-    // with their index, unless there are too few of them to spread evenly
-    // over the grid: with fewer than 4 per workgroup slot, some CUs get one
-    // chunk more than others (1360 chunks on 512 slots: 6 on some CUs, 5 on
-    // the rest), and segment runs, which split the work in rounds, are
-    // faster despite their dearer rounds (measured: 3.7% on a 1360-chunk
-    // layer; 7.5% slower on a 5042-chunk block).
-    // AIMG_SEGMENT_RUNS=1 sends every tensor with an index (that can) to the
-    // segment runs, =0 none; otherwise the choice above (tests and
-    // benchmarks use it to time and check each path).
+    // Tensors with an index and chunks of at least kRunMinChunk symbols
+    // decode in segment runs; the others chunk by chunk, without an index.
+    // AIMG_SEGMENT_RUNS=0 decodes every tensor chunk by chunk (tests and
+    // benchmarks use it to check and time the path without the index).
     const char* force = std::getenv("AIMG_SEGMENT_RUNS");
-    const int runs_mode = force == nullptr ? -1 : force[0] == '1' ? 1 : force[0] == '0' ? 0 : -1;
-    int64_t big_chunks = 0;
+    const bool no_runs = force != nullptr && force[0] == '0';
+    Batch* const to_run = vec_ok && !no_runs ? &run : nullptr;
     for (int i = 0; i < n; ++i) {
-        const aimg_tensor& t = ts[i];
-        if (t.index != nullptr && t.chunk_size > 0 && t.n_symbols > 0 &&
-            threads_per_chunk(t.chunk_size) == static_cast<uint32_t>(kThreads))
-            big_chunks += (t.n_symbols + t.chunk_size - 1) / t.chunk_size;
-    }
-    const bool big_runs = runs_mode == 1 ||
-                          big_chunks < 4 * static_cast<int64_t>(cu_count()) * kBlocksPerCu;
-    Batch* const to_run = vec_ok && runs_mode != 0 ? &run : nullptr;
-    for (int i = 0; i < n; ++i) {
-        const int rc = add_tensor<kMode>(ts[i], i, normal, tiny, to_run, big_runs);
+        const int rc = add_tensor<kMode>(ts[i], i, normal, tiny, to_run);
         if (rc != AIMG_OK) return rc;
     }
     const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -2465,6 +2353,26 @@ extern "C" int aimg_build_index(const aimg_tensor* tensors, int n_tensors, void*
     hipLaunchKernelGGL(aimg::index_finish_kernel,
                        dim3(static_cast<uint32_t>(chunks < slots ? chunks : slots)), dim3(256), 0, s,
                        plan, chunks);
+    err = hipGetLastError();
+    if (err != hipSuccess)
+        return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    // Rounds: items numbered per tensor, room for every round its index can
+    // hold (the kernel skips those past the tensor's segments).
+    aimg::LaunchArgs rounds = plan;
+    int64_t n_round_items = 0;
+    for (int k = 0; k < n_plan; ++k) {
+        const aimg::DevTensor& t = plan.t[k];
+        rounds.t[k].item_begin = n_round_items;
+        // The segment length is only known on the device (from the table);
+        // the shortest possible one (a 1-bit shortest code) bounds the rounds.
+        const aimg::IndexLayout L =
+            aimg::index_layout(t.packed_nbytes, t.n_chunks, aimg::segment_bits(1u));
+        n_round_items += static_cast<int64_t>(L.capacity / aimg::kIndexBlock + 1);
+    }
+    const int64_t rslots = static_cast<int64_t>(aimg::cu_count()) * aimg::kBlocksPerCu;
+    hipLaunchKernelGGL(aimg::index_rounds_kernel,
+                       dim3(static_cast<uint32_t>(n_round_items < rslots ? n_round_items : rslots)),
+                       dim3(aimg::kThreads), 0, s, rounds, n_round_items);
     err = hipGetLastError();
     if (err != hipSuccess)
         return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));

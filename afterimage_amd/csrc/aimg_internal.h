@@ -8,7 +8,7 @@
 
 namespace aimg {
 
-constexpr int kAbiVersion = 10;
+constexpr int kAbiVersion = 11;
 constexpr uint32_t kTableMagic = 0x474D4941u;  // "AIMG"
 
 // Window table: for each 12-bit window, the codewords that lie wholly inside
@@ -61,19 +61,25 @@ inline size_t table_nbytes() {
 // Segment index of one tensor (aimg_build_index). Segment k of chunk c
 // covers chunk bits [k * seg_bits, (k + 1) * seg_bits); the chunk's
 // segments are numbered base[c] .. base[c + 1] - 1 in one sequence over the
-// tensor (its chunks that hold output elements, n_jobs of them). For each,
-// one uint16 entry:
-//   offset | count << 4
-// offset: the first codeword boundary at or after the segment start, 0..15
-// bits past it; count: the codewords that start inside the segment and
+// tensor (its chunks that hold output elements, n_jobs of them). A
+// segment's count is the number of codewords that start inside it and
 // before the chunk's real end rend[c], the end of its lim-th codeword (lim:
 // the chunk's output elements). Codewords past rend[c] (the zero bits that
 // pad a chunk to whole bytes) are not counted, so a chunk's counts add up
-// to lim and the tensor's symbols run on from chunk to chunk.
+// to lim and the tensor's symbols run on from chunk to chunk. The
+// segments fall in rounds of 512 (segments 512 m .. 512 m + 511, across
+// chunk boundaries), and each has one uint32 entry:
+//   offset | jj << 4 | excl << 10
+// offset: the first codeword boundary at or after the segment start, 0..15
+// bits past it; jj: its chunk minus the chunk of its round's first segment
+// (below 64 for chunks of 1024 symbols or more); excl: the counts of its
+// round's segments before it (at most 511 * 84). While the index is built
+// an entry holds offset | count << 4.
 // Layout (index_layout): the header, uint32 base[n_chunks + 1] (entries
-// past n_jobs repeat the total), uint32 rend[n_chunks], uint16
-// entries[capacity], and RoundStart rounds[n_rounds]: where segment 512 * m
-// starts (a segment run begins at such a segment). The index is usable
+// past n_jobs repeat the total), uint32 rend[n_chunks], uint32
+// entries[capacity], and RoundStart rounds[n_rounds]: where each round
+// starts, and after the last round (m = ceil(n_segments / 512)) a
+// sentinel whose element is the tensor's symbol count. The index is usable
 // (ok == 1) only when the chunks lie back to back in the packed buffer,
 // every chunk holds its lim codewords within its bytes, and everything
 // fits; seg_bits and the table checksum tie it to the table it was built
@@ -111,6 +117,9 @@ static_assert(sizeof(RoundStart) == 16, "round start is 16 bytes");
 
 // Segments between two round starts (one round of a whole workgroup).
 constexpr uint32_t kIndexBlock = 512;
+// Fields of a finished entry (offset in bits 0..3).
+constexpr uint32_t kEntryJjShift = 4;
+constexpr uint32_t kEntryExclShift = 10;
 
 // Byte offsets of the real ends and the entries of an index over n_chunks
 // chunks (they do not depend on the segment count).
@@ -136,7 +145,7 @@ constexpr IndexLayout index_layout(int64_t packed_nbytes, int64_t n_chunks, uint
     l.base = sizeof(IndexHeader);
     l.rend = index_rend_at(n_chunks);
     l.entries = index_entries_at(n_chunks);
-    l.rounds = (l.entries + 2 * l.capacity + 15) & ~uint64_t{15};
+    l.rounds = (l.entries + 4 * l.capacity + 15) & ~uint64_t{15};
     l.total = l.rounds + sizeof(RoundStart) * l.n_rounds;
     return l;
 }

@@ -10,11 +10,12 @@ Decode tables are keyed by codebook content (the stored LUT bytes and width),
 so tensors that share a codebook share one device table, and a tensor can
 never be decoded with another codebook's table.
 
-A resident tensor may also carry a segment index (``build_index``): each
-168-bit segment's first codeword boundary and codeword count, 2 bytes per
-segment, built once by the GPU from the tensor itself. Decodes of a tensor
-with an index skip the speculative segment start, the agreement check and the
-compaction of the kernel's rounds; the output is the same.
+A resident tensor may also carry a segment index (``build_index``): for each
+168-bit segment its first codeword boundary, its chunk and its symbols' place
+in a round of 512 segments, 4 bytes per segment, built once by the GPU from the
+tensor itself. Decodes of a tensor with an index run in rounds of 512 segments
+across chunk boundaries, with no speculative segment start, agreement check,
+scan or compaction; the output is the same.
 """
 from __future__ import annotations
 
@@ -262,13 +263,15 @@ class DeviceTensor:
 
     @property
     def index_bytes_read(self) -> int:
-        """Index bytes a decode reads: the entries of the chunks' segments and
-        each chunk's first segment and real end (0 without an index)."""
+        """Index bytes a decode reads: the entries of the chunks' segments
+        (4 bytes each), each chunk's first segment and real end, and the start
+        of each round of 512 segments (0 without an index)."""
         if self.index is None:
             return 0
         seg = segment_bits(self.tables.host_blob)
         nb = self.chunk_nbytes.to(torch.int64)
-        return int(8 * self.n_chunks + 2 * ((nb * 8 + seg - 1) // seg).sum().item())
+        segments = int(((nb * 8 + seg - 1) // seg).sum().item())
+        return 8 * self.n_chunks + 4 * segments + 16 * (segments // 512 + 1)
 
     @property
     def algorithmic_bytes(self) -> int:

@@ -147,11 +147,15 @@ int aimg_recombine_bf16(const uint8_t* exponent, const uint8_t* sign_mantissa, v
 /* bits, one per thread, and find where each segment's first codeword starts */
 /* by decoding ahead of it and checking agreement with the thread before.    */
 /* A segment index records, once per resident tensor, each segment's first   */
-/* codeword boundary and codeword count (2 bytes per segment of 168 bits for */
-/* bf16 exponent codes: about 2.3% of a compressed layer). A decode given    */
-/* the index skips the look-ahead, the agreement check and the compaction    */
-/* of its symbols, and writes each segment's symbols straight to their       */
-/* place. Decoding without an index (index == NULL) gives the same result.   */
+/* codeword boundary, its chunk and where its symbols go in a round of 512   */
+/* segments (4 bytes per segment of 168 bits for bf16 exponent codes: about  */
+/* 4.7% of a compressed layer). A decode given the index runs in rounds of   */
+/* 512 segments across chunk boundaries with no look-ahead, agreement check, */
+/* scan or compaction, and writes each segment's symbols straight to their   */
+/* place. It is used for tensors whose chunks hold 1024 symbols or more and  */
+/* that take the vector path (16-byte aligned output, chunk_size % 8 == 0);  */
+/* other tensors decode without it. Decoding without an index (index ==      */
+/* NULL) gives the same result.                                              */
 /* An index describes one tensor's packed bytes, chunk offsets and lengths   */
 /* and table: the decoders use it only with the table it was built with      */
 /* (checked by checksum) and otherwise ignore it; with other packed bytes or */

@@ -173,17 +173,10 @@ inline uint32_t emu_dword(const __amdgpu_buffer_rsrc_t& r, uint64_t off) {
 inline uint32_t __builtin_amdgcn_raw_buffer_load_b32(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, int) {
     return emu_dword(r, (uint64_t)vo + so);
 }
-inline uint16_t __builtin_amdgcn_raw_buffer_load_b16(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, int) {
-    const uint64_t off = (uint64_t)vo + so;
-    if (off + 2 > r.n) return 0;
-    uint16_t v;
-    std::memcpy(&v, r.base + off, 2);
-    return v;
-}
-inline void __builtin_amdgcn_raw_buffer_store_b16(uint16_t v, __amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so,
+inline void __builtin_amdgcn_raw_buffer_store_b32(uint32_t v, __amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so,
                                                   int) {
     const uint64_t off = (uint64_t)vo + so;
-    if (off + 2 <= r.n) std::memcpy(const_cast<uint8_t*>(r.base) + off, &v, 2);
+    if (off + 4 <= r.n) std::memcpy(const_cast<uint8_t*>(r.base) + off, &v, 4);
 }
 typedef uint32_t emu_u32x2 __attribute__((ext_vector_type(2)));
 inline emu_u32x2 __builtin_amdgcn_raw_buffer_load_b64(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, int) {

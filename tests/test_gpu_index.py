@@ -52,7 +52,7 @@ def _starts(enc, c):
 
 
 def _expected_index(enc, seg):
-    """(bases, rends, entries) of the index: per chunk, per segment of seg
+    """(bases, rends, raw entries) of the index: per chunk, per segment of seg
     bits, the first boundary's offset from the segment start | count << 4,
     where count takes only the codewords before the chunk's real end (the
     end of its lim-th codeword, lim its output elements)."""
@@ -86,7 +86,7 @@ def _layout(t, seg):
     base = 64
     rend = base + 4 * (n + 1)
     entries = (rend + 4 * n + 15) & ~15
-    rounds = (entries + 2 * cap + 15) & ~15
+    rounds = (entries + 4 * cap + 15) & ~15
     return base, rend, entries, cap, rounds
 
 
@@ -96,8 +96,25 @@ def _index_arrays(t, seg):
     n = t.n_chunks
     base, rend, entries, cap, rounds = _layout(t, seg)
     return (hdr, ix[base: base + 4 * (n + 1)].view(np.uint32), ix[rend: rend + 4 * n].view(np.uint32),
-            ix[entries: entries + 2 * cap].view(np.uint16),
+            ix[entries: entries + 4 * cap].view(np.uint32),
             ix[rounds: rounds + 16 * (cap // 512 + 2)].view(np.uint32).reshape(-1, 4))
+
+
+def _final_entries(bases, raw):
+    """The entries as decodes read them: offset | jj << 4 | excl << 10, with
+    jj the segment's chunk minus its round's first chunk (at most 63: segment
+    runs take chunks of 1024 symbols or more, at most 40 to a round) and excl
+    the counts of its round's segments before it (rounds: 512 segments)."""
+    counts = raw.astype(np.int64) >> 4
+    out = np.zeros(len(raw), np.uint32)
+    for g0 in range(0, len(raw), 512):
+        c0 = int(np.searchsorted(bases, g0, side="right")) - 1
+        excl = 0
+        for g in range(g0, min(g0 + 512, len(raw))):
+            c = int(np.searchsorted(bases, g, side="right")) - 1
+            out[g] = (int(raw[g]) & 15) | (min(c - c0, 63) << 4) | (excl << 10)
+            excl += int(counts[g])
+    return out
 
 
 def _expected_rounds(enc, seg, bases, entries):
@@ -136,10 +153,13 @@ def test_index_entries_equal_a_cpu_walk_of_the_codeword_starts(kind, chunk):
     assert [int(r) for r, w in zip(rends, want_r) if w is not None] == \
         [w for w in want_r if w is not None]
     got = entries[: len(want_e)]
-    bad = np.nonzero(got != want_e)[0]
-    assert bad.size == 0, "entries differ at %s: %s vs %s" % (bad[:5], got[bad[:5]], want_e[bad[:5]])
+    want_f = _final_entries(want_b, want_e)
+    bad = np.nonzero(got != want_f)[0]
+    assert bad.size == 0, "entries differ at %s: %s vs %s" % (bad[:5], got[bad[:5]], want_f[bad[:5]])
     want_rs = _expected_rounds(enc, seg, want_b, want_e)
     assert np.array_equal(rounds[: len(want_rs)].astype(np.int64), want_rs)
+    # After the last round, the tensor's end.
+    assert int(rounds[len(want_rs)][1]) == int(enc.n_symbols)
     assert np.array_equal(decode_u8([t])[0].cpu().numpy(), exps.numpy().astype(np.uint8))
 
 
@@ -170,10 +190,10 @@ def test_bf16_full_layer_with_index_is_bit_exact():
     t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, DEV).build_index()
     out = decode_bf16([t])[0]
     assert torch.equal(out.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
-    # Index size: 2 bytes per 168-bit segment (2.6 bits per exponent), about
-    # 2.3% of the compressed layer.
+    # Index size: 4 bytes per 168-bit segment (2.6 bits per exponent), about
+    # 4.7% of the compressed layer.
     comp = t.packed.numel() + t.sign_mantissa.numel()
-    assert t.index.numel() < 0.025 * comp
+    assert t.index.numel() < 0.05 * comp
 
 
 def test_block_with_and_without_indexes_in_one_launch():

@@ -181,8 +181,11 @@ def test_u8_segment_guesses_all_wrong(emu):
 
 
 # Decoding with the segment index (aimg_build_index): the index is built by
-# the same kernel's build mode, then each segment decodes from its recorded
-# start straight into place; the result must equal the weights / exponents.
+# the chunk kernel's build mode and the round and finish steps, then tensors
+# whose chunks hold 1024 symbols or more decode in segment runs, each segment
+# from its recorded start straight into place (smaller chunks and the
+# element-wise path ignore the index); the result must equal the weights /
+# exponents.
 
 @pytest.mark.parametrize("chunk_size", [64, 1024, 4096])
 def test_u8_with_index(emu, chunk_size):
@@ -265,9 +268,8 @@ def test_unusable_index_fallback_over_several_workgroups(emu):
     _bf16(emu, "ix_fallback_many", W, 1024, index="index-foreign")
 
 
-# The same indexes decoded chunk by chunk (AIMG_SEGMENT_RUNS=0 forces it; on
-# its own the library takes that path for launches of many whole-workgroup
-# chunks) and in segment runs (=1).
+# The same tensors with AIMG_SEGMENT_RUNS=0, which decodes every tensor chunk
+# by chunk and ignores its index, and with =1 (segment runs, the default).
 
 @pytest.mark.parametrize("runs", ["0", "1"])
 def test_bf16_two_round_64k_chunks_with_index_both_paths(emu, runs):
@@ -281,10 +283,10 @@ def test_bf16_1024_chunks_with_index_both_paths(emu, runs):
     _bf16(emu, "ix_1024_paths%s" % runs, W, 1024, index="index", runs=runs)
 
 
-def test_gemv_with_index_chunk_by_chunk(emu):
+def test_gemv_with_index_ignored_chunk_by_chunk(emu):
     _gemv(emu, "ix_gemv512_items", 70, 1000, 32768, 4, 5, index="index", runs="0")
 
 
-def test_foreign_index_chunk_by_chunk(emu):
+def test_foreign_index_ignored_chunk_by_chunk(emu):
     W = workloads.bf16_normal((40, 5000), 6, 0.02, outlier_frac=1e-3)
     _bf16(emu, "ix_foreign_items", W, 4096, index="index-foreign", runs="0")

@@ -256,7 +256,7 @@ def test_table_blob_records_a_checksum_of_its_tables():
     assert int(blob[28:32].view(np.uint32)[0]) == h
 
 
-def test_index_size_is_two_bytes_per_segment_plus_chunk_tables():
+def test_index_size_is_four_bytes_per_segment_plus_chunk_tables():
     lib = _native.lib()
     enc, blob = _bf16_table()
     min_len = int(blob[12:16].view(np.uint32)[0])
@@ -265,14 +265,15 @@ def test_index_size_is_two_bytes_per_segment_plus_chunk_tables():
     packed, chunks = 1_000_003, 77
     assert lib.aimg_index_nbytes(blob.ctypes.data, packed, chunks, ctypes.byref(n)) == 0
     # 64-byte header, first segment (chunks + 1) and real end (chunks) of
-    # each chunk, 2 bytes per segment of the packed bytes (one partial
+    # each chunk, 4 bytes per segment of the packed bytes (one partial
     # segment per chunk), and 16 bytes for every 512th segment (where a
-    # segment run may start: chunk, element, byte, chunk's first segment).
+    # segment run may start: chunk, element, byte, chunk's first segment)
+    # and one more for the end.
     cap = -(-8 * packed // seg) + chunks
     entries_at = (64 + 4 * (chunks + 1) + 4 * chunks + 15) & ~15
-    rounds_at = (entries_at + 2 * cap + 15) & ~15
+    rounds_at = (entries_at + 4 * cap + 15) & ~15
     assert n.value == rounds_at + 16 * (cap // 512 + 2)
-    assert n.value < 2.05 * cap + 12 * chunks + 128
+    assert n.value < 4.05 * cap + 12 * chunks + 128
     bad = blob.copy()
     bad[0] ^= 1
     assert lib.aimg_index_nbytes(bad.ctypes.data, packed, chunks, ctypes.byref(n)) == \
