@@ -15,7 +15,8 @@ Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
                     [--workload layer|block|gemv|ring|api] [--chunk-size N]
-                    [--batch B] [--no-index] [--no-cpu-baseline] [--cpu-threads T]
+                    [--batch B] [--no-index] [--no-cold] [--no-cpu-baseline]
+                    [--cpu-threads T]
 """
 from __future__ import annotations
 
@@ -405,6 +406,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-index", action="store_true",
                     help="layer/block: time the decode without segment indexes only")
+    ap.add_argument("--no-cold", action="store_true",
+                    help="layer: skip the cold-input launches (kernel traces of the timed loop)")
     ap.add_argument("--index-only", action="store_true",
                     help="layer/block: skip the launches without the index (for profiling)")
     ap.add_argument("--cpu-threads", type=int, default=0,
@@ -563,7 +566,7 @@ def main() -> int:
     # cache between launches. Decoding three copies of the layer in turn
     # (354 MB of inputs) reads them from HBM, as a streamed model would.
     cold = None
-    if args.workload == "layer":
+    if args.workload == "layer" and not args.no_cold:
         import dataclasses
 
         copies = [(dts, outs)]
