@@ -148,6 +148,7 @@ struct LaunchArgs {
     DevTensor t[AIMG_MAX_TENSORS];
     int64_t total_items;
     int32_t n_tensors;
+    int32_t strided;  // segment runs: workgroup w takes rounds w, w + grid, ...
     GemvArgs gemv;  // kModeGemv only (one tensor)
 };
 
@@ -1755,7 +1756,8 @@ struct RunFetch {
     uint32_t raw[kTileBatch];
     uint32_t ent;
     uint32_t cb, co, cr;
-    v4u32 rn;  // the round start after the fetched round
+    v4u32 rn;   // the round start after the fetched round (its end)
+    v4u32 rnx;  // the start of the workgroup's round after it
 };
 
 struct RunPos {
@@ -1779,7 +1781,7 @@ __device__ __forceinline__ RunPos run_pos(v4u32 rs, uint32_t g0, uint32_t n_jobs
 // chunk table and the next round's start.
 __device__ __forceinline__ void run_fetch_issue(RunFetch& F, const DevTensor& T,
                                                 const IndexLayout& L, const RunPos& P,
-                                                uint32_t s_hi, uint32_t tid) {
+                                                uint32_t s_hi, uint32_t stride, uint32_t tid) {
     const __amdgpu_buffer_rsrc_t rs = buffer_of(T.packed, T.packed_n32);
     const uint32_t last = last_word(T);
 #pragma unroll
@@ -1803,9 +1805,11 @@ __device__ __forceinline__ void run_fetch_issue(RunFetch& F, const DevTensor& T,
     F.cr = __builtin_amdgcn_raw_buffer_load_b32(index_part(T, L.rend, 4 * T.n_chunks), 4 * c, 0, 0);
     F.co = __builtin_amdgcn_raw_buffer_load_b32(
         buffer_of(T.offsets, static_cast<uint32_t>(4 * T.n_chunks)), 4 * c, 0, 0);
+    const __amdgpu_buffer_rsrc_t rr = index_part(T, L.rounds, sizeof(RoundStart) * L.n_rounds);
     F.rn = __builtin_amdgcn_raw_buffer_load_b128(
-        index_part(T, L.rounds, sizeof(RoundStart) * L.n_rounds),
-        static_cast<uint32_t>(sizeof(RoundStart)) * (P.g0 / kIndexBlock + 1), 0, 0);
+        rr, static_cast<uint32_t>(sizeof(RoundStart)) * (P.g0 / kIndexBlock + 1), 0, 0);
+    F.rnx = __builtin_amdgcn_raw_buffer_load_b128(
+        rr, static_cast<uint32_t>(sizeof(RoundStart)) * (P.g0 / kIndexBlock + stride), 0, 0);
 }
 
 // The fetched words into the tile (big-endian, bytes past the packed
@@ -1820,7 +1824,10 @@ __device__ __forceinline__ void run_fetch_commit(const RunFetch& F, const DevTen
     consume(F.co);
     consume(F.cr);
 #pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) consume(F.rn[k]);
+    for (uint32_t k = 0; k < 4; ++k) {
+        consume(F.rn[k]);
+        consume(F.rnx[k]);
+    }
     const uint32_t last = last_word(T);
     uint32_t* const top = lds.tile + kRunTileWords - 1;
 #pragma unroll
@@ -1840,10 +1847,15 @@ __device__ __forceinline__ void run_fetch_commit(const RunFetch& F, const DevTen
     }
 }
 
-// Segments [s_lo, s_hi) of tensor T (usable index, table in LDS).
+// Rounds m0, m0 + stride, ... (n_rounds of them) of tensor T, whose
+// segments number G (usable index). With stride 1 the rounds are one run
+// and a round's last partial vector group carries into the next; otherwise
+// each round stores its own partial groups element by element.
 template <int kMode, int kGroup>
 __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const LaunchArgs& args,
-                          const DevTensor& T, uint32_t s_lo, uint32_t s_hi, const uint8_t* table) {
+                          const DevTensor& T, uint32_t m0, uint32_t n_rounds, uint32_t stride,
+                          uint32_t G, const uint8_t* table) {
+    const uint32_t s_lo = m0 * kThreads;
     const uint32_t tid = threadIdx.x;
     const uint32_t S = segment_bits(tb.min_len);
     const IndexLayout L = index_layout(T.packed_nbytes, T.n_chunks, S);
@@ -1858,7 +1870,8 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
     // piece's differs from the one in LDS) and the cleared stage are
     // written while they arrive.
     RunFetch F;
-    run_fetch_issue(F, T, L, P, s_hi, tid);
+    const uint32_t s_hi0 = s_lo + kThreads < G ? s_lo + kThreads : G;
+    run_fetch_issue(F, T, L, P, s_hi0, stride, tid);
     if (table != nullptr) {
         __syncthreads();  // every thread is done with the previous table
         load_table(table, tid, lds.wsyms, lds.wmeta, lds.len, lds.esc);
@@ -1873,16 +1886,20 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
     uint8_t* const stage = lds.stage;
     uint32_t lead = P.el & (kGroup - 1);  // symbols staged before the round's
     uint32_t skip = lead;  // of those, the ones another piece writes
-    uint32_t r = 0;
-    for (uint32_t g0 = s_lo; g0 < s_hi; g0 += kThreads, ++r) {
+    for (uint32_t r = 0; r < n_rounds; ++r) {
         const uint32_t b = r & 1u;
-        // This round's entry, and the next round's start (both fetched with
-        // this round's words): the next round's words are requested first.
+        const uint32_t g0 = P.g0;
+        const uint32_t s_hi = g0 + kThreads < G ? g0 + kThreads : G;
+        // This round's entry, its end and the workgroup's next round's start
+        // (all fetched with this round's words): the next round's words are
+        // requested first.
         const uint32_t ent = F.ent;
-        const uint32_t gn = g0 + kThreads;
-        const RunPos N = run_pos(F.rn, gn, n_jobs);
+        const uint32_t end_el = uniform(F.rn[1]);
+        const uint32_t gn = g0 + stride * kThreads;
+        const bool more = r + 1 < n_rounds;
+        const RunPos N = run_pos(F.rnx, gn, n_jobs);
         __builtin_amdgcn_s_setprio(3);
-        if (gn < s_hi) run_fetch_issue(F, T, L, N, s_hi, tid);
+        if (more) run_fetch_issue(F, T, L, N, gn + kThreads < G ? gn + kThreads : G, stride, tid);
         const int64_t a0 = static_cast<int64_t>(P.el) - lead;
         SmBatch<kMode> smb;
         sm_issue<kMode, kGroup>(smb, T, a0, tid, kThreads);
@@ -1893,7 +1910,7 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
         const uint32_t ex = ent >> kEntryExclShift;
         const uint32_t excl = ex < (kThreads - 1) * kSlotCap ? ex : (kThreads - 1) * kSlotCap;
         const uint32_t jj = (ent >> kEntryJjShift) & (kRunChunks - 1);
-        const uint32_t gtot0 = N.el - P.el;
+        const uint32_t gtot0 = end_el - P.el;
         const uint32_t gtot = gtot0 < kThreads * kSlotCap ? gtot0 : kThreads * kSlotCap;
         const uint32_t avail = lead + gtot;
         // Whole groups, never past the tensor's end (only an index that does
@@ -1922,13 +1939,31 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
             }
         }
         __syncthreads();  // the round is placed; the tile takes the next words
-        if (gn < s_hi) run_fetch_commit(F, T, N, tid, lds, b ^ 1u);
+        if (more) run_fetch_commit(F, T, N, tid, lds, b ^ 1u);
         __builtin_amdgcn_s_setprio(2);
         store_round<kMode, kGroup, true>(smb, T, args.gemv, stage, a0, nfull, tid, kThreads, skip);
+        const uint32_t rem0 = avail - nfull * kGroup;
+        // (The fused GEMV's rounds are never strided; compiling the path for
+        // it spills its registers to scratch.)
+        if (kMode != kModeGemv && kMode != kModeGemv1 && stride != 1) {
+            // Rounds of other workgroups follow: the partial group goes out
+            // element by element (the elements before `skip` of a round's
+            // first group are the previous round's).
+            const uint32_t t = nfull * kGroup + tid;
+            if (tid < rem0 && t >= skip) store_one<kMode>(T, args.gemv, a0 + t, stage[t]);
+            const uint32_t placed = (lead + gtot + 4 + 15) & ~15u;
+            const uint32_t zend = placed < kRunStageBytes ? placed : kRunStageBytes;
+            __syncthreads();
+            for (uint32_t z = 16 * tid; z < zend; z += 16 * kThreads)
+                *reinterpret_cast<uint4*>(stage + z) = make_uint4(0u, 0u, 0u, 0u);
+            lead = N.el & (kGroup - 1);
+            skip = lead;
+            P = N;
+            continue;
+        }
         if (nfull != 0) skip = 0;
         // The partial vector group (rem < 16 bytes at a multiple of kGroup)
         // moves to the front; all else placed is cleared.
-        const uint32_t rem0 = avail - nfull * kGroup;
         const uint32_t rem = rem0 < static_cast<uint32_t>(kGroup) ? rem0 : kGroup - 1u;
         uint2 k0 = make_uint2(0u, 0u), k1 = make_uint2(0u, 0u);
         if (tid == 0 && rem != 0) {
@@ -2007,11 +2042,13 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void run_kernel(const Laun
     tb.len = lds.len;
     tb.esc = lds.esc;
     const uint8_t* loaded = nullptr;
-    // The launch's work in rounds (512 consecutive segments of one tensor),
-    // whole rounds to each workgroup: the first `extra` workgroups take one
-    // more. (Workgroups b and b + 256 share a CU, so no CU takes two extra
-    // rounds while another takes none; an even split of segments instead
-    // gives every workgroup a last, mostly empty round.)
+    // The launch's work in rounds (512 consecutive segments of one tensor).
+    // Strided (the default): workgroup w takes rounds w, w + grid, ... of
+    // the launch's round sequence. Otherwise contiguous ranges of whole
+    // rounds, the first `extra` workgroups taking one more (workgroups b
+    // and b + 256 share a CU, so no CU takes two extra rounds while another
+    // takes none; an even split of segments instead gives every workgroup a
+    // last, mostly empty round).
     if (tid < static_cast<uint32_t>(args.n_tensors)) lds.segs[tid] = run_segments(args.t[tid]);
     __syncthreads();
     uint64_t units = 0;
@@ -2034,7 +2071,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void run_kernel(const Laun
         // Tensors without a usable index: an even share of their chunks.
         const int64_t c_lo = G != 0 ? 0 : T.n_jobs * static_cast<int64_t>(blockIdx.x) / gridDim.x;
         const int64_t c_hi = G != 0 ? 0 : T.n_jobs * static_cast<int64_t>(blockIdx.x + 1) / gridDim.x;
-        const bool work = G != 0 ? a < b : c_lo < c_hi;
+        const bool work = G != 0 ? (args.strided || a < b) : c_lo < c_hi;
         if (!work) {
             at += U;
             continue;
@@ -2045,11 +2082,23 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void run_kernel(const Laun
         tb.min_len = hdr->min_len >= 1 ? hdr->min_len : 1u;
         tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(table + kEscOffset);
         const bool global_esc = hdr->n_esc_blocks > static_cast<uint32_t>(kLdsEscBlocks);
-        if (G != 0 && a < b) {
+        if (kMode != kModeGemv && kMode != kModeGemv1 && G != 0 && args.strided) {
+            // Rounds u = blockIdx.x + k * grid of the launch's round sequence.
+            const uint64_t first = at + (blockIdx.x + gridDim.x - at % gridDim.x) % gridDim.x;
+            if (first < at + U) {
+                const uint32_t n = static_cast<uint32_t>((at + U - 1 - first) / gridDim.x + 1);
+                run_piece<kMode, kGroup>(lds, tb, global_esc, args, T,
+                                         static_cast<uint32_t>(first - at), n, gridDim.x, G,
+                                         table != loaded ? table : nullptr);
+                loaded = table;
+            }
+        } else if (G != 0 && a < b) {
             // The piece loads the table itself, once its first words are
             // requested.
-            run_piece<kMode, kGroup>(lds, tb, global_esc, args, T, static_cast<uint32_t>(a),
-                                     static_cast<uint32_t>(b), table != loaded ? table : nullptr);
+            run_piece<kMode, kGroup>(lds, tb, global_esc, args, T,
+                                     static_cast<uint32_t>(a / kThreads),
+                                     static_cast<uint32_t>((b - a + kThreads - 1) / kThreads), 1u,
+                                     G, table != loaded ? table : nullptr);
             loaded = table;
         } else if (G == 0 && c_lo < c_hi) {
             if (table != loaded) {
@@ -2136,6 +2185,18 @@ int launch_run(Batch& B, hipStream_t s) {
     if (B.m == 0) return AIMG_OK;
     B.args.n_tensors = B.m;
     B.args.total_items = 0;
+    // Rounds go to workgroups in turn (workgroup w takes rounds w, w + grid,
+    // ...), so the grid works through a window of consecutive rounds: with
+    // inputs read from HBM, 9% faster on a 5120x17408 layer and 5% on a 14B
+    // block than contiguous ranges of rounds per workgroup, which are 3%
+    // faster when the inputs are still in the last-level cache from the
+    // previous launch. The fused GEMV keeps contiguous ranges: its per-row
+    // atomics would all land on the few cache lines of y that a window of
+    // rounds covers (batch 4 was 6x slower strided). AIMG_RUN_STRIDED=0
+    // selects contiguous ranges for the decodes too.
+    const char* st = std::getenv("AIMG_RUN_STRIDED");
+    B.args.strided =
+        (kMode == kModeGemv || kMode == kModeGemv1) || (st != nullptr && st[0] == '0') ? 0 : 1;
     int64_t bits = 0;
     for (int d = 0; d < B.m; ++d) bits += 8 * B.args.t[d].packed_nbytes;
     // About 4 rounds of 512 segments per workgroup at least; a full grid for

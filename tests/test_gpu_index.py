@@ -261,10 +261,12 @@ def test_gemv_with_index_matches_without(batch):
     assert torch.allclose(y1, y0, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("strided", ["1", "0"])
 @pytest.mark.parametrize("chunk", [1024, 2048, 65536])
-def test_segment_runs_split_chunks_over_the_grid(chunk):
-    # Large enough for a full grid: every workgroup's slice of the segments
-    # starts and ends inside chunks.
+def test_segment_runs_split_chunks_over_the_grid(chunk, strided, monkeypatch):
+    # Large enough for a full grid: every workgroup's rounds (in turn, or a
+    # contiguous range with AIMG_RUN_STRIDED=0) start and end inside chunks.
+    monkeypatch.setenv("AIMG_RUN_STRIDED", strided)
     W = workloads.bf16_normal((2048, 8192), 16, 0.02, outlier_frac=1e-3)
     layer = compress_layer(W, chunk_size=chunk)
     t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, DEV).build_index()

@@ -73,12 +73,15 @@ def _write(d, enc, expect, sm=None):
         f.write("%d %d %d %d\n" % (enc.max_bits, enc.chunk_size, enc.n_symbols, len(enc.chunk_offsets)))
 
 
-def _run(emu, name, mode, index="", runs=None):
+def _run(emu, name, mode, index="", runs=None, strided=None):
     exe, d = emu
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0")
     env.pop("AIMG_SEGMENT_RUNS", None)
+    env.pop("AIMG_RUN_STRIDED", None)
     if runs is not None:
         env["AIMG_SEGMENT_RUNS"] = runs
+    if strided is not None:
+        env["AIMG_RUN_STRIDED"] = strided
     args = [exe, str(d / name), mode] + ([index] if index else [])
     r = subprocess.run(args, capture_output=True, text=True, env=env, timeout=600)
     assert r.returncode == 0 and ": ok" in r.stdout, (r.stdout + r.stderr)[-4000:]
@@ -91,11 +94,11 @@ def _u8(emu, name, exps, chunk_size, index=""):
     _run(emu, name, "u8", index)
 
 
-def _bf16(emu, name, W, chunk_size, index="", runs=None):
+def _bf16(emu, name, W, chunk_size, index="", runs=None, strided=None):
     layer = compress_layer(W, chunk_size=chunk_size)
     _write(emu[1] / name, layer.encoded, W.reshape(-1).view(torch.int16).numpy(),
            layer.sign_mantissa.numpy())
-    _run(emu, name, "bf16", index, runs)
+    _run(emu, name, "bf16", index, runs, strided)
 
 
 def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None):
@@ -244,13 +247,15 @@ def test_gemv_16_thread_chunks_with_index(emu):
     _gemv(emu, "ix_gemv16", 96, 40, 64, 2, 3, index="index")
 
 
-def test_bf16_segment_runs_cross_chunk_and_workgroup_boundaries(emu):
+@pytest.mark.parametrize("strided", ["1", "0"])
+def test_bf16_segment_runs_cross_chunk_and_workgroup_boundaries(emu, strided):
     # 1024-symbol chunks over 768K weights: about 20 segments of 168 bits a
     # chunk, and the launch's segments split over several workgroups, so
-    # rounds and workgroup slices start and end inside chunks and inside
+    # rounds (strided: rounds in turn to each workgroup; "0": a contiguous
+    # range of rounds per workgroup) start and end inside chunks and inside
     # vector groups.
     W = workloads.bf16_normal((96, 8192), 12, 0.02, outlier_frac=1e-3)
-    _bf16(emu, "ix_runs1024", W, 1024, index="index")
+    _bf16(emu, "ix_runs1024_s%s" % strided, W, 1024, index="index", strided=strided)
 
 
 def test_u8_segment_runs_of_a_ragged_tensor(emu):
