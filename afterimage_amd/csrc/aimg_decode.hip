@@ -800,10 +800,13 @@ struct SmBatch {
 // Buffer loads (zero past the tensor's last byte), so the batch needs no
 // clamping and is issued back to back; the batch offset is a scalar.
 template <int kMode, int kGroup>
+// `limit`: no byte at or past it is needed (the loads there return zero
+// without reading memory).
 __device__ __forceinline__ void sm_issue(SmBatch<kMode>& B, const DevTensor& T, int64_t a0,
-                                         uint32_t i, uint32_t tpc) {
+                                         uint32_t i, uint32_t tpc, uint32_t limit = 0xFFFFFFFFu) {
     if (!needs_sm(kMode) || kGroup == 1) return;
-    const __amdgpu_buffer_rsrc_t rs = buffer_of(T.sm, static_cast<uint32_t>(T.n_symbols));
+    const uint32_t n = static_cast<uint32_t>(T.n_symbols);
+    const __amdgpu_buffer_rsrc_t rs = buffer_of(T.sm, n < limit ? n : limit);
     const uint32_t v0 = static_cast<uint32_t>(a0) + i * kGroup;
 #pragma unroll
     for (uint32_t k = 0; k < kSmAhead; ++k) {
@@ -1902,7 +1905,9 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
         if (more) run_fetch_issue(F, T, L, N, gn + kThreads < G ? gn + kThreads : G, stride, tid);
         const int64_t a0 = static_cast<int64_t>(P.el) - lead;
         SmBatch<kMode> smb;
-        sm_issue<kMode, kGroup>(smb, T, a0, tid, kThreads);
+        // Only this round's bytes: the next round's are another workgroup's
+        // when rounds are strided (reading them here cost 3% more traffic).
+        sm_issue<kMode, kGroup>(smb, T, a0, tid, kThreads, (end_el + kGroup - 1) & ~(kGroup - 1u));
         const uint32_t g = g0 + tid;
         const bool active = g < s_hi;
         // Entries above the round's room only come from an index that does
