@@ -2204,10 +2204,10 @@ int launch_run(Batch& B, hipStream_t s) {
         (kMode == kModeGemv || kMode == kModeGemv1) || (st != nullptr && st[0] == '0') ? 0 : 1;
     int64_t bits = 0;
     for (int d = 0; d < B.m; ++d) bits += 8 * B.args.t[d].packed_nbytes;
-    // About 4 rounds of 512 segments per workgroup at least; a full grid for
-    // anything larger.
+    // A workgroup per round (of 168-bit segments) up to a full grid: each
+    // workgroup pays its start-up once, and its rounds follow one another.
     const int64_t slots = static_cast<int64_t>(cu_count()) * kBlocksPerCu;
-    const int64_t want = bits / (4 * static_cast<int64_t>(kThreads) * kMaxSegBits) + 1;
+    const int64_t want = bits / (static_cast<int64_t>(kThreads) * kMaxSegBits) + 1;
     const dim3 gdim(static_cast<uint32_t>(want < slots ? want : slots)), bdim(kThreads);
     constexpr int kVecGroup = kMode == kModeU8 ? 16 : 8;
     hipLaunchKernelGGL((run_kernel<kMode, kVecGroup>), gdim, bdim, 0, s, B.args);
