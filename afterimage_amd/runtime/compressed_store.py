@@ -17,7 +17,8 @@ import dataclasses
 import numpy as np
 import torch
 
-from .device import DeviceTensor, cpu_decode, decode_bf16, decode_gemv, recombine_bf16
+from .device import (GEMV_MAX_BATCH, DeviceTensor, cpu_decode, decode_bf16, decode_gemv,
+                     decode_linear, recombine_bf16)
 from .huffman_chunked import ChunkedEncoded, encode_chunked, lengths_from_counts, symbol_counts
 
 EXPONENT_SHIFT = 7
@@ -282,4 +283,49 @@ def decompress_matvec_gpu(layer: CompressedLayer, x: torch.Tensor,
                                   tables=_tables_for(layer.encoded, dev))
     y = decode_gemv(t, xb, rows, cols).to(torch.bfloat16)
     return y.reshape(rows) if squeeze else y
+
+
+def decompress_linear_gpu(layer: CompressedLayer, x: torch.Tensor, slice_rows: int = 8192,
+                          device: str | torch.device = "cuda",
+                          fused: bool | None = None) -> torch.Tensor:
+    """x @ W.T for the layer's 2-D bf16 weight W [rows, cols], as the
+    reference's chunked lm_head computes it (streaming_engine.py:2307-2332):
+    x [..., cols] times W a block of slice_rows rows at a time, each block
+    decoded (decompress_rows_gpu's chunk range) and multiplied with
+    torch.nn.functional.linear, the outputs concatenated along the last
+    dimension. Returns [..., rows] in x's dtype (bf16, as W).
+
+    The blocked path gives the reference's own result: the same weights, bit
+    for bit, in the same F.linear calls. Its blocks reuse one staging buffer.
+
+    fused: True multiplies inside the decode kernel (decompress_matvec_gpu;
+    fp32 sums, rounded once to bf16) without decoding any block to memory,
+    for at most 4 rows of x (speculative-verify widths and single tokens);
+    None (default) takes it whenever x has at most 4 rows, False never.
+    Neither path is bit-identical to one unblocked F.linear: the reference
+    marks its blocked head lossy for that reason (its
+    tests/test_chunked_lm_head_gpu.py:1-27)."""
+    dev = _gpu_device(device)
+    if len(layer.shape) != 2:
+        raise ValueError("decompress_linear_gpu needs a 2-D layer, got shape %s" % (layer.shape,))
+    rows, cols = (int(v) for v in layer.shape)
+    if x.dim() < 1 or x.shape[-1] != cols:
+        raise ValueError("x must end in a dimension of %d, got shape %s" % (cols, tuple(x.shape)))
+    lead = tuple(x.shape[:-1])
+    tokens = int(np.prod(lead)) if lead else 1
+    if fused and not 1 <= tokens <= GEMV_MAX_BATCH:
+        raise ValueError("the fused product takes 1..%d rows of x, got %d"
+                         % (GEMV_MAX_BATCH, tokens))
+    x = x.to(dev)
+    if rows == 0:
+        return x.new_zeros(lead + (0,))
+    t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, dev,
+                                  tables=_tables_for(layer.encoded, dev))
+    if fused is None:
+        fused = 1 <= tokens <= GEMV_MAX_BATCH
+    if fused:
+        xb = x.reshape(tokens, cols).to(torch.bfloat16).contiguous()
+        y = decode_gemv(t, xb, rows, cols).to(x.dtype)
+        return y.reshape(lead + (rows,))
+    return decode_linear(t, x, rows, cols, slice_rows)
 

@@ -246,6 +246,8 @@ class DeviceTensor:
     n_symbols: int
     shape: tuple[int, ...]
     index: torch.Tensor | None = None  # uint8 segment index (build_index), or None
+    # indexed_ranges' views, by their chunk ranges
+    range_cache: dict = dataclasses.field(default_factory=dict, repr=False, compare=False)
 
     @property
     def n_chunks(self) -> int:
@@ -253,8 +255,9 @@ class DeviceTensor:
 
     @property
     def index_nbytes(self) -> int:
-        """Bytes of this tensor's segment index (header, chunk bases and one
-        2-byte entry per segment)."""
+        """Bytes of this tensor's segment index (header, chunk bases and real
+        ends, one 4-byte entry per segment, one 16-byte start per round of 512
+        segments)."""
         n = ctypes.c_size_t(0)
         _native.check(_native.lib().aimg_index_nbytes(
             self.tables.host_blob.ctypes.data, int(self.packed.numel()), self.n_chunks,
@@ -288,18 +291,7 @@ class DeviceTensor:
         it); later decodes use it. An index the build marks unusable (chunks
         not back to back in the packed buffer, or a chunk that does not hold
         its symbols) is dropped unless keep_unusable. Returns self."""
-        dev = self.packed.device
-        if dev.type != "cuda":
-            raise RuntimeError("the segment index is built on the GPU; tensor is on %s" % dev)
-        ix = torch.empty(self.index_nbytes, dtype=torch.uint8, device=dev)
-        d = (_native.AimgTensor * 1)()
-        d[0] = _descriptor(self, None, self.n_symbols)
-        d[0].index = ix.data_ptr()
-        d[0].index_nbytes = int(ix.numel())
-        with torch.cuda.device(dev):
-            _native.check(_native.lib().aimg_build_index(d, 1, _stream_handle(dev)))
-        usable = int(ix[16:20].cpu().numpy().view(np.uint32)[0]) == 1
-        self.index = ix if usable or keep_unusable else None
+        build_indexes([self], keep_unusable)
         return self
 
     @property
@@ -309,6 +301,59 @@ class DeviceTensor:
 
     def drop_index(self) -> None:
         self.index = None
+
+    def chunk_range(self, c0: int, c1: int) -> "DeviceTensor":
+        """Chunks [c0, c1) as a tensor of their own, sharing this tensor's
+        memory: chunk offsets point into the same packed buffer, and the
+        sign/mantissa bytes are the range's slice. It holds the range's
+        symbols, min(n_symbols, c1 * chunk_size) - c0 * chunk_size, and no
+        segment index (an index covers a whole tensor)."""
+        if not 0 <= c0 <= c1 <= self.n_chunks:
+            raise ValueError("chunk range [%d, %d) outside [0, %d)" % (c0, c1, self.n_chunks))
+        if c0 == 0 and c1 == self.n_chunks:
+            return self
+        base = c0 * self.chunk_size
+        n = max(0, min(self.n_symbols, c1 * self.chunk_size) - base)
+        sm = None if self.sign_mantissa is None else self.sign_mantissa[base: base + n]
+        return DeviceTensor(packed=self.packed, chunk_offsets=self.chunk_offsets[c0:c1],
+                            chunk_nbytes=self.chunk_nbytes[c0:c1], sign_mantissa=sm,
+                            tables=self.tables, chunk_size=self.chunk_size, n_symbols=n,
+                            shape=(n,))
+
+    def indexed_ranges(self, ranges: list[tuple[int, int]]) -> list["DeviceTensor"]:
+        """Chunk ranges as tensors that each carry a segment index of their
+        own, built now (one batched build and one wait): each range's
+        packed bytes are a view of this tensor's packed buffer from its first
+        chunk's first byte to its last chunk's last byte, and its chunk
+        offsets are rebased to that view (a new int32 array per range), so
+        that an index holds only the range's segments. The views are cached
+        on this tensor by their ranges. Needs chunks back to back in the
+        packed buffer, as an index does; a range whose index comes out
+        unusable decodes without one."""
+        key = tuple((int(a), int(b)) for a, b in ranges)
+        hit = self.range_cache.get(key)
+        if hit is not None:
+            return hit
+        offs = self.chunk_offsets.cpu().numpy().astype(np.int64)
+        lens = self.chunk_nbytes.cpu().numpy().astype(np.int64)
+        views = []
+        for c0, c1 in key:
+            v = self.chunk_range(c0, c1)
+            if v is self or c1 <= c0:
+                views.append(v)
+                continue
+            # The view starts on the 16-byte boundary at or before the range's
+            # first byte, so its base keeps the buffer's alignment.
+            lo = int(offs[c0]) & ~15
+            hi = int(offs[c1 - 1] + lens[c1 - 1])
+            if not 0 <= lo <= hi <= self.packed.numel():
+                raise ValueError("chunks %d..%d lie outside the packed buffer" % (c0, c1 - 1))
+            v.packed = self.packed[lo:hi]
+            v.chunk_offsets = (self.chunk_offsets[c0:c1] - lo).contiguous()
+            views.append(v)
+        build_indexes([v for v in views if v is not self and v.n_chunks > 0])
+        self.range_cache[key] = views
+        return views
 
     @classmethod
     def from_encoded(cls, enc, sign_mantissa, device, tables: DecodeTables | None = None):
@@ -326,6 +371,35 @@ class DeviceTensor:
                 np.ascontiguousarray(enc.chunk_nbytes, dtype=np.int32)).to(device),
             sign_mantissa=sm, tables=tables, chunk_size=int(enc.chunk_size),
             n_symbols=int(enc.n_symbols), shape=tuple(enc.shape))
+
+
+def build_indexes(tensors: list[DeviceTensor], keep_unusable: bool = False) -> None:
+    """Build the segment indexes of resident tensors on one device, up to
+    MAX_TENSORS per aimg_build_index call, then wait once and drop (unless
+    keep_unusable) every index the build marked unusable."""
+    if not tensors:
+        return
+    dev = tensors[0].packed.device
+    if dev.type != "cuda":
+        raise RuntimeError("the segment index is built on the GPU; tensor is on %s" % dev)
+    ixs = []
+    lib = _native.lib()
+    for i in range(0, len(tensors), MAX_TENSORS):
+        group = tensors[i: i + MAX_TENSORS]
+        d = (_native.AimgTensor * len(group))()
+        for j, t in enumerate(group):
+            if t.packed.device != dev:
+                raise ValueError("tensors on %s and %s" % (dev, t.packed.device))
+            ix = torch.empty(t.index_nbytes, dtype=torch.uint8, device=dev)
+            d[j] = _descriptor(t, None, t.n_symbols)
+            d[j].index = ix.data_ptr()
+            d[j].index_nbytes = int(ix.numel())
+            ixs.append(ix)
+        with torch.cuda.device(dev):
+            _native.check(lib.aimg_build_index(d, len(group), _stream_handle(dev)))
+    ok = torch.stack([ix[16:20] for ix in ixs]).cpu().numpy().view(np.uint32).reshape(-1)
+    for t, ix, flag in zip(tensors, ixs, ok):
+        t.index = ix if flag == 1 or keep_unusable else None
 
 
 def _stream_handle(device) -> int:
@@ -458,6 +532,66 @@ def decode_gemv(t: DeviceTensor, x: torch.Tensor, rows: int, cols: int,
         _native.check(_native.lib().aimg_decode_gemv_bf16(
             d, rows, cols, x.data_ptr(), b, y.data_ptr(), _stream_handle(dev)))
     return y
+
+
+def row_blocks(rows: int, cols: int, chunk_size: int, n_chunks: int, slice_rows: int):
+    """The blocks of a blocked x @ W.T: (r0, r1, c0, c1) for each block of
+    slice_rows rows (the last one shorter), with [c0, c1) the chunks that
+    hold its elements [r0 * cols, r1 * cols)."""
+    step = max(1, int(slice_rows))
+    out = []
+    for r0 in range(0, rows, step):
+        r1 = min(r0 + step, rows)
+        c0 = (r0 * cols) // chunk_size
+        c1 = min(n_chunks, -(-(r1 * cols) // chunk_size))
+        out.append((r0, r1, c0, c1))
+    return out
+
+
+def decode_linear(t: DeviceTensor, x: torch.Tensor, rows: int, cols: int,
+                  slice_rows: int, staging: torch.Tensor | None = None) -> torch.Tensor:
+    """torch.nn.functional.linear(x, W) for the rows x cols bf16 weight W held
+    by ``t``, slice_rows rows of W at a time: each block's chunks are decoded
+    into one staging buffer, which every block reuses, the GEMM library
+    multiplies x by the block, and the blocks' outputs are concatenated along
+    the last dimension. This is the blocked lm_head projection of
+    streaming_engine.py:2307-2332 (decompress_rows_gpu, F.linear, torch.cat):
+    the same calls on the same bytes, at the same offsets from a buffer
+    start, so the same result, with one buffer of about slice_rows * cols
+    weights live instead of one per block. When ``t`` has a segment index,
+    each block decodes through an index of its own (indexed_ranges, built on
+    the first call for these blocks). Runs on the current stream."""
+    dev = x.device
+    if dev.type != "cuda":
+        raise RuntimeError("the decoder runs on the GPU only; got x on %s" % dev)
+    if x.dim() < 1 or x.shape[-1] != cols:
+        raise ValueError("x must end in a dimension of %d, got shape %s" % (cols, tuple(x.shape)))
+    if rows * cols != t.n_symbols:
+        raise ValueError("rows * cols = %d, the tensor has %d weights" % (rows * cols, t.n_symbols))
+    blocks = row_blocks(rows, cols, t.chunk_size, t.n_chunks, slice_rows)
+    if not blocks:
+        return torch.nn.functional.linear(
+            x, torch.empty((0, cols), dtype=torch.bfloat16, device=dev))
+    need = max(min(t.n_symbols, c1 * t.chunk_size) - c0 * t.chunk_size
+               for _, _, c0, c1 in blocks)
+    if staging is None:
+        staging = torch.empty(need, dtype=torch.bfloat16, device=dev)
+    elif staging.dtype != torch.bfloat16 or staging.device != dev or \
+            not staging.is_contiguous() or staging.numel() < need:
+        raise ValueError("staging must be a contiguous bf16 tensor of >= %d elements on %s"
+                         % (need, dev))
+    # A tensor with a segment index decodes its blocks through indexes of
+    # their own (built on the first call for these blocks, then cached).
+    ranges = [(c0, c1) for _, _, c0, c1 in blocks]
+    views = t.indexed_ranges(ranges) if t.index is not None else \
+        [t.chunk_range(c0, c1) for c0, c1 in ranges]
+    parts = []
+    for (r0, r1, c0, _), part in zip(blocks, views):
+        decode_bf16([part], [staging])
+        e0 = r0 * cols - c0 * t.chunk_size
+        w = staging[e0: e0 + (r1 - r0) * cols].view(r1 - r0, cols)
+        parts.append(torch.nn.functional.linear(x, w))
+    return parts[0] if len(parts) == 1 else torch.cat(parts, dim=-1)
 
 
 

@@ -14,8 +14,9 @@ last-level cache between launches. --workload block does the same for a whole
 Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
-                    [--workload layer|block|gemv|ring|api] [--chunk-size N]
-                    [--batch B] [--no-index] [--no-cold] [--no-cpu-baseline]
+                    [--workload layer|block|gemv|ring|api|head] [--chunk-size N]
+                    [--batch B] [--slice-rows R] [--no-index] [--no-cold]
+                    [--no-cpu-baseline]
                     [--cpu-threads T]
 """
 from __future__ import annotations
@@ -331,6 +332,141 @@ def _bench_gemv(args) -> int:
     return 0
 
 
+def _bench_head(args) -> int:
+    """The output projection of a 14B-class model (lm_head 151936x5120 bf16,
+    resident compressed in HBM at the reference store's default 1024-symbol
+    chunks) applied to x [1, tokens, 5120]. One step = one blocked forward
+    as the reference's chunked head computes it: 8192-row blocks, each
+    decoded (through a segment index of its own) into one staging buffer and
+    multiplied by the GEMM library, outputs concatenated. Also timed: the
+    whole head decoded at once (through its segment index) then one
+    F.linear, the fused decode->GEMV for at most 4 tokens, and F.linear on
+    the already-decoded weight alone."""
+    import torch.nn.functional as F
+
+    from afterimage_amd import workloads
+    from afterimage_amd.runtime.compressed_store import compress_layer
+    from afterimage_amd.runtime.device import (GEMV_MAX_BATCH, DeviceTensor, decode_bf16,
+                                               decode_gemv, decode_linear, row_blocks)
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    rows, cols, slice_rows, tokens = 151936, 5120, args.slice_rows, args.batch
+    t0 = time.perf_counter()
+    W = workloads.bf16_normal((rows, cols), 5, 0.02, outlier_frac=1e-3)
+    layer = compress_layer(W, chunk_size=args.chunk_size)
+    _log("head built in %.1fs: %d chunks, packed %.1f MB"
+         % (time.perf_counter() - t0, layer.encoded.n_chunks, layer.encoded.packed.nbytes / 1e6))
+    enc = layer.encoded
+    n = enc.n_symbols
+    t = DeviceTensor.from_encoded(enc, layer.sign_mantissa, dev).build_index()
+    g = np.random.default_rng(29)
+    x = torch.from_numpy(g.standard_normal((1, tokens, cols), dtype=np.float32)) \
+        .to(torch.bfloat16).to(dev)
+    blocks = row_blocks(rows, cols, enc.chunk_size, enc.n_chunks, slice_rows)
+    need = max(min(n, c1 * enc.chunk_size) - c0 * enc.chunk_size for _, _, c0, c1 in blocks)
+    staging = torch.empty(need, dtype=torch.bfloat16, device=dev)
+    whole = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    y_fused = torch.zeros((tokens, rows), dtype=torch.float32, device=dev)
+    fused_ok = tokens <= GEMV_MAX_BATCH
+
+    def blocked():
+        return decode_linear(t, x, rows, cols, slice_rows, staging=staging)
+
+    def unblocked():
+        decode_bf16([t], [whole])
+        return F.linear(x, whole.view(rows, cols))
+
+    def fused():
+        y_fused.zero_()
+        decode_gemv(t, x.reshape(tokens, cols), rows, cols, y_fused)
+
+    # Parity before timing: the decoded head is the original bit for bit,
+    # and the blocked forward is the reference's blocked F.linear calls on
+    # those weights (block views at the same offsets, so the same GEMMs).
+    y_blocked = blocked()
+    unblocked()
+    torch.cuda.synchronize(dev)
+    Wd = W.to(dev)
+    bit_exact = torch.equal(whole.view(rows, cols).view(torch.int16), Wd.view(torch.int16))
+    ref = []
+    flat = Wd.reshape(-1)
+    for r0, r1, c0, c1 in blocks:
+        base = c0 * enc.chunk_size
+        buf = flat[base: min(n, c1 * enc.chunk_size)].clone()
+        ref.append(F.linear(x, buf[r0 * cols - base: r1 * cols - base].view(r1 - r0, cols)))
+    same_as_reference = torch.equal(y_blocked, torch.cat(ref, dim=-1))
+    del ref, buf, flat
+    if not bit_exact:
+        print("decoded head differs from the original weights", file=sys.stderr)
+        return 1
+    fused_within = None
+    if fused_ok:
+        fused()
+        yf = torch.matmul(x.reshape(tokens, cols).float(), Wd.float().t().contiguous())
+        yb = y_fused.to(torch.bfloat16).float()
+        fused_within = bool(((yb - yf).abs() <= 1e-3 + 1e-2 * yf.abs()).all())
+        del yf, yb
+    del Wd
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(dev)
+        e0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        return e0.elapsed_time(e1) / 1e3 / args.steps
+
+    wall0 = time.perf_counter()
+    blocked_s = timed(blocked)
+    wall = (time.perf_counter() - wall0) / (args.steps + args.warmup)
+    unblocked_s = timed(unblocked)
+    decode_s = timed(lambda: decode_bf16([t], [whole]))
+    gemm_s = timed(lambda: F.linear(x, whole.view(rows, cols)))
+    fused_s = timed(fused) if fused_ok else None
+    rec = {
+        "metric": "blocked lm_head forward: decompressed BF16 GB/s (decode + GEMM per block)",
+        "value": round(2 * n / blocked_s / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(blocked_s * 1e3, 4),
+        "wall_ms_per_step": round(wall * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "lm_head 151936x5120 bf16 (seed 5, 0.1%% outliers, %d-symbol "
+                               "chunks) resident compressed, x [1, %d, 5120] bf16 N(0,1) "
+                               "(seed 29), %d-row blocks" % (enc.chunk_size, tokens, slice_rows),
+                   "tokens": tokens, "slice_rows": slice_rows, "chunk_size": enc.chunk_size,
+                   "blocks": len(blocks), "staging_bytes": 2 * need,
+                   "weights_bit_exact": bit_exact,
+                   "blocked_equals_reference_forward": same_as_reference,
+                   "fused_within_tolerance": fused_within,
+                   "tolerance": "fused: rel 1e-2, abs 1e-3 against the fp32 product"},
+        "paths_us": {
+            "blocked_decode_and_gemm": round(blocked_s * 1e6, 1),
+            "whole_decode_then_gemm": round(unblocked_s * 1e6, 1),
+            "whole_decode_alone": round(decode_s * 1e6, 1),
+            "gemm_alone_on_decoded_weight": round(gemm_s * 1e6, 1),
+            "fused_decode_gemv": None if fused_s is None else round(fused_s * 1e6, 1),
+        },
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
 def _bench_api(args) -> int:
     """The reference API path: decompress_layer_gpu on the 5120x17408 layer
     from host arrays, as the reference engine calls it (pageable H2D of the
@@ -394,15 +530,19 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=["layer", "block", "gemv", "ring", "api"],
+    ap.add_argument("--workload", choices=["layer", "block", "gemv", "ring", "api", "head"],
                     default="layer",
                     help="layer: one 5120x17408 weight (the headline); block: a whole "
                          "14B-class decoder block in one launch; gemv: fused decode->GEMV "
                          "of the 5120x17408 weight with a [batch, 17408] activation; ring: 40 "
                          "streamed blocks from pinned host memory through a 2-slot ring; api: "
-                         "decompress_layer_gpu from host arrays, H2D included")
+                         "decompress_layer_gpu from host arrays, H2D included; head: a 151936x5120 "
+                         "lm_head applied to [1, batch, 5120] in row blocks (the reference's "
+                         "chunked head)")
     ap.add_argument("--layers", type=int, default=40, help="ring: layers streamed per step")
-    ap.add_argument("--batch", type=int, default=1, help="gemv batch (1..4)")
+    ap.add_argument("--batch", type=int, default=1,
+                    help="gemv: batch (1..4); head: tokens of x")
+    ap.add_argument("--slice-rows", type=int, default=8192, help="head: rows per block")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-index", action="store_true",
                     help="layer/block: time the decode without segment indexes only")
@@ -412,8 +552,9 @@ def main() -> int:
                     help="layer/block: skip the launches without the index (for profiling)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="CPU-baseline threads (0: OpenMP's count, i.e. every CPU given)")
-    ap.add_argument("--chunk-size", type=int, default=65536,
-                    help="layer / gemv / api: symbols per chunk of the 5120x17408 weight")
+    ap.add_argument("--chunk-size", type=int, default=None,
+                    help="layer / gemv / api: symbols per chunk of the 5120x17408 weight "
+                         "(default 65536); head: of the lm_head (default 1024)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of decoding, time a plain device copy of this many MiB "
                          "(the reference kernel for scaling HBM byte counters)")
@@ -430,6 +571,8 @@ def main() -> int:
     if args.steps < 1 or args.warmup < 0:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
+    if args.chunk_size is None:
+        args.chunk_size = 1024 if args.workload == "head" else 65536
 
     if args.copy_mib:
         return _copy_calibration(args.copy_mib, args.steps, args.warmup)
@@ -439,6 +582,8 @@ def main() -> int:
         return _bench_ring(args)
     if args.workload == "api":
         return _bench_api(args)
+    if args.workload == "head":
+        return _bench_head(args)
 
     from afterimage_amd import _native, workloads
     from afterimage_amd.runtime.device import DeviceTensor, _descriptor

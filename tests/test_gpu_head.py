@@ -1,0 +1,139 @@
+"""Blocked x @ W.T (the reference's chunked lm_head, streaming_engine.py:2307-2332)
+through decompress_linear_gpu and decode_linear. The blocked path must give
+exactly what the reference's forward gives on the original weights: the same
+F.linear calls on the same (bit-exact) blocks, concatenated. The fused path
+(at most 4 rows of x) is held to the GEMV tolerance, rel 1e-2 / abs 1e-3
+against the fp32 product."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from afterimage_amd import workloads
+from afterimage_amd.runtime.compressed_store import compress_layer, decompress_linear_gpu
+from afterimage_amd.runtime.device import DeviceTensor, decode_linear
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-2, 1e-3
+
+
+def _x(shape, seed):
+    g = np.random.default_rng(seed)
+    return torch.from_numpy(g.standard_normal(shape, dtype=np.float32)).to(torch.bfloat16).cuda()
+
+
+def _reference_forward(W, x, step, chunk):
+    """The reference's blocked forward on the original weights, each block a
+    view into a fresh buffer holding its covering chunk range, at the offset
+    decompress_rows_gpu gives it (compressed_store.py:254-303), so that the
+    GEMM library sees the same shapes and alignments."""
+    rows, cols = W.shape
+    flat = W.cuda().reshape(-1)
+    n_chunks = -(-flat.numel() // chunk)
+    parts = []
+    for r0 in range(0, rows, step):
+        r1 = min(r0 + step, rows)
+        e0, e1 = r0 * cols, r1 * cols
+        base = (e0 // chunk) * chunk
+        avail = min(flat.numel(), min(n_chunks, -(-e1 // chunk)) * chunk) - base
+        buf = torch.empty(avail, dtype=torch.bfloat16, device="cuda")
+        buf.copy_(flat[base: base + avail])
+        parts.append(F.linear(x, buf[e0 - base: e1 - base].view(r1 - r0, cols)))
+    return torch.cat(parts, dim=-1)
+
+
+@pytest.mark.parametrize("shape,chunk", [((300, 64), 32), ((301, 100), 256),
+                                         ((1500, 200), 65536), ((97, 1000), 1024)])
+def test_blocked_head_is_the_reference_forward(shape, chunk):
+    """Row blocks that start on chunk boundaries (64 cols, 32-symbol chunks,
+    the reference's own test layout), inside chunks (100 and 1000 cols) and
+    several blocks in one chunk (65536-symbol chunks)."""
+    torch.manual_seed(17)
+    W = torch.randn(shape, dtype=torch.float32).to(torch.bfloat16)
+    layer = compress_layer(W, chunk_size=chunk)
+    for x in (_x((1, 5, shape[1]), 1), _x((9, shape[1]), 2)):
+        for step in (shape[0], 128, 64, 7, 1):
+            y = decompress_linear_gpu(layer, x, slice_rows=step, fused=False)
+            assert y.shape == x.shape[:-1] + (shape[0],)
+            assert torch.equal(y, _reference_forward(W, x, step, chunk)), "step=%d" % step
+
+
+def test_blocked_head_at_the_reference_production_shape():
+    """hidden 5120, 9496 rows in blocks of 2374 (the shape of the reference's
+    test_blocked_matmul_is_not_bit_exact_at_production_shape), 1024-symbol
+    chunks (the reference's default), 8 verify tokens."""
+    W = workloads.bf16_normal((9496, 5120), 23, 0.02, outlier_frac=1e-3)
+    layer = compress_layer(W, chunk_size=1024)
+    x = _x((1, 8, 5120), 3)
+    y = decompress_linear_gpu(layer, x, slice_rows=2374)
+    assert torch.equal(y, _reference_forward(W, x, 2374, 1024))
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4])
+def test_fused_head_for_up_to_four_rows_of_x(tokens):
+    W = workloads.bf16_normal((2000, 1536), 4 + tokens, 0.02, outlier_frac=1e-3)
+    layer = compress_layer(W, chunk_size=1024)
+    x = _x((1, tokens, 1536), tokens)
+    y = decompress_linear_gpu(layer, x)  # fused by default at <= 4 rows of x
+    assert y.shape == (1, tokens, 2000) and y.dtype == torch.bfloat16
+    ref = torch.matmul(x.float().reshape(tokens, 1536),
+                       W.cuda().float().t().contiguous()).reshape(1, tokens, 2000)
+    err = (y.float() - ref).abs()
+    bound = ATOL + RTOL * ref.abs()
+    assert bool((err <= bound).all()), "max excess %.3g" % float((err - bound).max())
+
+
+def test_resident_tensor_with_index_and_given_staging():
+    """decode_linear on a resident tensor: one block covering the whole
+    tensor decodes through its segment index; smaller blocks decode chunk
+    ranges into the caller's staging buffer."""
+    W = workloads.bf16_normal((640, 5120), 8, 0.02, outlier_frac=1e-3)
+    layer = compress_layer(W, chunk_size=65536)
+    t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, "cuda").build_index()
+    assert t.index_usable
+    x = _x((6, 5120), 5)
+    assert torch.equal(decode_linear(t, x, 640, 5120, 640), F.linear(x, W.cuda()))
+    staging = torch.empty(200 * 5120 + 2 * 65536, dtype=torch.bfloat16, device="cuda")
+    for step in (200, 33):
+        y = decode_linear(t, x, 640, 5120, step, staging=staging)
+        assert torch.equal(y, _reference_forward(W, x, step, 65536)), "step=%d" % step
+    with pytest.raises(ValueError):
+        decode_linear(t, x, 640, 5120, 640, staging=staging[:1000])
+
+
+@pytest.mark.parametrize("shape,chunk,step", [((97, 1000), 1024, 7), ((300, 4100), 1024, 64),
+                                              ((1500, 200), 65536, 333)])
+def test_blocks_decode_through_indexes_of_their_own(shape, chunk, step):
+    """A resident tensor with an index: each block's chunk range gets an index
+    of its own over a view of the packed bytes (starting on a 16-byte
+    boundary, offsets rebased), built once and reused by later calls."""
+    W = workloads.bf16_normal(shape, 31, 0.02, outlier_frac=1e-2)
+    layer = compress_layer(W, chunk_size=chunk)
+    t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, "cuda").build_index()
+    x = _x((2, 3, shape[1]), 7)
+    ref = _reference_forward(W, x, step, chunk)
+    assert torch.equal(decode_linear(t, x, shape[0], shape[1], step), ref)
+    (key, views), = t.range_cache.items()
+    assert len(views) == -(-shape[0] // step)
+    for v in views:
+        if v is not t:
+            assert v.index_usable
+            assert v.packed.data_ptr() % 16 == 0
+            assert 0 <= int(v.chunk_offsets[0]) < 16
+    assert torch.equal(decode_linear(t, x, shape[0], shape[1], step), ref)
+    assert t.range_cache[key] is views
+
+
+def test_errors_and_empty_inputs():
+    W = workloads.bf16_normal((40, 64), 2, 0.02)
+    layer = compress_layer(W, chunk_size=128)
+    with pytest.raises(ValueError):
+        decompress_linear_gpu(layer, _x((5, 64), 1), fused=True)   # more than 4 rows of x
+    with pytest.raises(ValueError):
+        decompress_linear_gpu(layer, _x((2, 63), 1))               # wrong width
+    flat = compress_layer(W.reshape(-1), chunk_size=128)
+    with pytest.raises(ValueError):
+        decompress_linear_gpu(flat, _x((2, 64), 1))                # not 2-D
+    y = decompress_linear_gpu(layer, _x((0, 64), 1))               # no rows of x
+    assert y.shape == (0, 40)
