@@ -14,7 +14,7 @@ last-level cache between launches. --workload block does the same for a whole
 Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
-                    [--workload layer|block|gemv|ring|api|head] [--chunk-size N]
+                    [--workload layer|block|gemv|ring|api|head|resync] [--chunk-size N]
                     [--batch B] [--slice-rows R] [--no-index] [--no-cold]
                     [--no-cpu-baseline]
                     [--cpu-threads T]
@@ -467,6 +467,68 @@ def _bench_head(args) -> int:
     return 0
 
 
+def _bench_resync(args) -> int:
+    """Exponent-byte decode of 16,777,216 symbols whose speculative segment
+    starts are all wrong (eight equiprobable symbols, 3-bit codes: every
+    168-bit segment starts inside a codeword and a guess never finds the
+    boundary), with and without the segment index, beside the exponents of a
+    bf16 weight of the same size. Both decodes are checked equal."""
+    from afterimage_amd import workloads
+    from afterimage_amd.runtime.device import DeviceTensor, decode_u8
+    from afterimage_amd.runtime.huffman_chunked import encode_chunked
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    n = 1 << 24
+    rng = np.random.default_rng(8)
+    W = workloads.bf16_normal((1024, n // 1024), 2, 0.02, outlier_frac=1e-3)
+    exps = ((W.view(torch.int16).to(torch.int32) & 0xFFFF) >> 7 & 0xFF).reshape(-1)
+    cases = [("all segment guesses wrong (3-bit codes)",
+              encode_chunked(torch.from_numpy(rng.integers(0, 8, n)), chunk_size=65536)),
+             ("bf16 exponents of a 1024x16384 weight", encode_chunked(exps, chunk_size=65536))]
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(t, out):
+        for _ in range(args.warmup):
+            decode_u8([t], outs=[out])
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(dev)
+        e0.record(stream)
+        for _ in range(args.steps):
+            decode_u8([t], outs=[out])
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        return e0.elapsed_time(e1) * 1e3 / args.steps
+
+    res = []
+    for name, enc in cases:
+        t = DeviceTensor.from_encoded(enc, None, dev)
+        a = torch.empty(n, dtype=torch.uint8, device=dev)
+        b = torch.empty(n, dtype=torch.uint8, device=dev)
+        plain_us = timed(t, a)
+        t.build_index()
+        index_us = timed(t, b)
+        same = torch.equal(a, b)
+        if not same:
+            print("%s: decodes with and without the index differ" % name, file=sys.stderr)
+            return 1
+        res.append({"stream": name, "symbols": n,
+                    "bits_per_symbol": round(8 * int(np.asarray(enc.chunk_nbytes).sum()) / n, 3),
+                    "no_index_us": round(plain_us, 1), "with_index_us": round(index_us, 1),
+                    "index_usable": t.index is not None, "outputs_equal": same})
+    rec = {
+        "metric": "exponent-byte decode time of streams that never resynchronise",
+        "value": res[0]["no_index_us"], "unit": "us", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "higher_is_better": False, "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic",
+        "config": {"workload": "16,777,216 symbols in 65536-symbol chunks, aimg_decode_u8"},
+        "cases": res, "roofline": None, "cpu_baseline": None,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
 def _bench_api(args) -> int:
     """The reference API path: decompress_layer_gpu on the 5120x17408 layer
     from host arrays, as the reference engine calls it (pageable H2D of the
@@ -530,7 +592,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=["layer", "block", "gemv", "ring", "api", "head"],
+    ap.add_argument("--workload", choices=["layer", "block", "gemv", "ring", "api", "head", "resync"],
                     default="layer",
                     help="layer: one 5120x17408 weight (the headline); block: a whole "
                          "14B-class decoder block in one launch; gemv: fused decode->GEMV "
@@ -538,7 +600,8 @@ def main() -> int:
                          "streamed blocks from pinned host memory through a 2-slot ring; api: "
                          "decompress_layer_gpu from host arrays, H2D included; head: a 151936x5120 "
                          "lm_head applied to [1, batch, 5120] in row blocks (the reference's "
-                         "chunked head)")
+                         "chunked head); resync: streams whose segment guesses are all wrong, "
+                         "with and without the index")
     ap.add_argument("--layers", type=int, default=40, help="ring: layers streamed per step")
     ap.add_argument("--batch", type=int, default=1,
                     help="gemv: batch (1..4); head: tokens of x")
@@ -584,6 +647,8 @@ def main() -> int:
         return _bench_api(args)
     if args.workload == "head":
         return _bench_head(args)
+    if args.workload == "resync":
+        return _bench_resync(args)
 
     from afterimage_amd import _native, workloads
     from afterimage_amd.runtime.device import DeviceTensor, _descriptor

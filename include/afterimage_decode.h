@@ -175,12 +175,14 @@ int aimg_index_nbytes(const void* host_table, int64_t packed_nbytes, int32_t n_c
 /*
  * Build the segment index of each tensor into its `index` (device memory of
  * index_nbytes >= aimg_index_nbytes bytes; tensors with a NULL index are
- * skipped; index must be 16-byte aligned). Three launches on `stream`
- * (segment numbering, the entries, then a walk that fixes each chunk's
- * counts at its real end); the decoders that follow on the stream use the
- * index. When the chunks' segments do not fit index_nbytes (chunks not
- * back to back) the index is marked unusable and decoders ignore it. Other
- * fields as for aimg_decode_u8.
+ * skipped; index must be 16-byte aligned). Four launches on `stream`
+ * (segment numbering, the raw entries, a walk that fixes each chunk's
+ * counts at its real end and writes the round starts, then each round's
+ * chunk numbers and output places); the decoders that follow on the stream
+ * use the index. When the chunks' segments do not fit index_nbytes (chunks
+ * not back to back) or a chunk does not hold its symbols, the index is
+ * marked unusable and decoders ignore it. Other fields as for
+ * aimg_decode_u8.
  */
 int aimg_build_index(const aimg_tensor* tensors, int n_tensors, void* stream);
 
