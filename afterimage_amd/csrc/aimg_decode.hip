@@ -1503,24 +1503,39 @@ __global__ __launch_bounds__(kThreads) void index_plan_kernel(const LaunchArgs a
     __syncthreads();
     uint32_t* const base = reinterpret_cast<uint32_t*>(ix + L.base);
     uint64_t run = 0;
-    for (int64_t c0 = 0; c0 < T.n_chunks; c0 += kThreads) {
-        const int64_t c = c0 + threadIdx.x;
-        uint32_t nseg = 0;
-        if (c < T.n_jobs) {
-            int64_t off, nb;
-            chunk_range(T, c, &off, &nb);
-            nseg = static_cast<uint32_t>((nb * 8 + S - 1) / S);
-            // Back to back: the next chunk starts where this one ends.
-            if (c + 1 < T.n_jobs && T.offsets[c + 1] != off + nb) s_bad = 1u;
+    // kPlanChunks consecutive chunks per thread and step: their segment
+    // counts are summed in the thread, the sums scanned over the workgroup.
+    constexpr int kPlanChunks = 4;
+    for (int64_t c0 = 0; c0 < T.n_chunks; c0 += kPlanChunks * kThreads) {
+        const int64_t cb = c0 + kPlanChunks * static_cast<int64_t>(threadIdx.x);
+        uint32_t nseg[kPlanChunks];
+        uint32_t mine = 0;
+#pragma unroll
+        for (int j = 0; j < kPlanChunks; ++j) {
+            const int64_t c = cb + j;
+            nseg[j] = 0;
+            if (c < T.n_jobs) {
+                int64_t off, nb;
+                chunk_range(T, c, &off, &nb);
+                nseg[j] = static_cast<uint32_t>((nb * 8 + S - 1) / S);
+                // Back to back: the next chunk starts where this one ends.
+                if (c + 1 < T.n_jobs && T.offsets[c + 1] != off + nb) s_bad = 1u;
+            }
+            mine += nseg[j];
         }
-        const uint32_t excl = block_scan_excl(nseg, s_wsum);
+        const uint32_t excl = block_scan_excl(mine, s_wsum);
         uint32_t tot = 0;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) tot += s_wsum[w];
-        const uint64_t at = run + excl;
-        if (fits && c < T.n_chunks) base[c] = static_cast<uint32_t>(at < kNoIndex ? at : kNoIndex - 1u);
+        uint64_t at = run + excl;
+#pragma unroll
+        for (int j = 0; j < kPlanChunks; ++j) {
+            const int64_t c = cb + j;
+            if (fits && c < T.n_chunks) base[c] = static_cast<uint32_t>(at < kNoIndex ? at : kNoIndex - 1u);
+            at += nseg[j];
+        }
         run += tot;
-        __syncthreads();  // s_wsum is written again by the next block's scan
+        __syncthreads();  // s_wsum is written again by the next step's scan
     }
     if (threadIdx.x == 0) {
         if (fits) {
@@ -1550,103 +1565,193 @@ __global__ __launch_bounds__(kThreads) void index_plan_kernel(const LaunchArgs a
     }
 }
 
-// The first codeword at bit p of a chunk's bytes (zero past nb): its length.
-// The table blob is read from global memory (the finish step runs once).
-__device__ __forceinline__ uint32_t codeword_len_at(const uint8_t* table, const uint8_t* bytes,
-                                                    uint32_t nb, uint32_t p) {
-    uint32_t w = 0;
-    const uint32_t b0 = p >> 3;
-#pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) w = (w << 8) | (b0 + k < nb ? bytes[b0 + k] : 0u);
-    w <<= (p & 7u);  // bits p.. at the top
+constexpr uint32_t kFinishThreads = 256;
+constexpr uint32_t kWalkBytes = 32;  // a segment's bytes and the 32 bits read past its last start
+
+// The first `keep` codewords from bit q of `seg` (a segment's bytes staged in
+// LDS, zero past the chunk's end): the bit where the last of them ends,
+// relative to seg. Whole windows are taken while they hold no more
+// codewords than are left; the last window's codewords are counted one by
+// one from their code lengths. These are the boundaries of reading one
+// codeword at a time (escape windows, and windows no codeword starts, take
+// their first codeword only): a window holds the codewords that lie wholly
+// inside it, read one after another from its first bit.
+__device__ __forceinline__ uint32_t walk_codewords(const uint8_t* seg, uint32_t q, uint32_t keep,
+                                                   const uint32_t* wsyms, const uint8_t* wmeta,
+                                                   const uint8_t* len, const uint16_t* esc,
+                                                   const uint8_t* table) {
     const auto* hdr = header_of(table);
-    const uint32_t idx = w >> (32 - kWinBits);
-    const uint8_t meta = table[kMetaOffset + idx];
-    const uint32_t ent = reinterpret_cast<const uint32_t*>(table + kSymsOffset)[idx];
     const uint32_t min_len = hdr->min_len >= 1 ? hdr->min_len : 1u;
-    if (meta != 0) return table[kLenOffset + (ent & 0xFFu)];
-    const uint32_t blk = ent & 0xFFFFu;
-    if (blk == kUnusedBlock || blk >= hdr->n_esc_blocks) return min_len;
-    const uint16_t v = reinterpret_cast<const uint16_t*>(table + kEscOffset)[
-        blk * kEscBlockEntries + ((w >> (28 - kWinBits)) & 15u)];
-    return (v >> 8) ? (v >> 8) : min_len;
+    const uint32_t n_esc = hdr->n_esc_blocks;
+    const uint16_t* gesc = reinterpret_cast<const uint16_t*>(table + kEscOffset);
+    uint32_t left = keep;
+    while (left > 0) {
+        // Only an index that does not describe its stream reads past the
+        // segment's bytes; the clamp keeps it in the buffer.
+        const uint32_t b = (q >> 3) < kWalkBytes - 4 ? (q >> 3) : kWalkBytes - 4;
+        uint32_t w = (static_cast<uint32_t>(seg[b]) << 24) | (static_cast<uint32_t>(seg[b + 1]) << 16) |
+                     (static_cast<uint32_t>(seg[b + 2]) << 8) | seg[b + 3];
+        w <<= (q & 7u);
+        const uint32_t idx = w >> (32 - kWinBits);
+        const uint32_t meta = wmeta[idx];
+        const uint32_t ent = wsyms[idx];
+        if (meta != 0) {
+            const uint32_t cnt = meta >> 5;
+            if (left >= cnt) {
+                q += meta & 31u;
+                left -= cnt;
+            } else {
+                for (uint32_t j = 0; j < left; ++j) q += len[(ent >> (8 * j)) & 0xFFu];
+                left = 0;
+            }
+        } else {
+            const uint32_t blk = ent & 0xFFFFu;
+            uint32_t l = min_len;
+            if (blk != kUnusedBlock && blk < n_esc) {
+                const uint32_t at = blk * kEscBlockEntries + ((w >> (28 - kWinBits)) & 15u);
+                const uint16_t v = blk < static_cast<uint32_t>(kLdsEscBlocks) ? esc[at] : gesc[at];
+                l = (v >> 8) ? (v >> 8) : min_len;
+            }
+            q += l;
+            --left;
+        }
+    }
+    return q;
 }
 
-// Finish, one workgroup per chunk (c < n_jobs): the chunk's lim-th codeword
-// is found from the entries' counts; its end is the chunk's real end rend,
+// Finish, one wave per chunk (c < n_jobs): the chunk's lim-th codeword is
+// found from the entries' counts; its end is the chunk's real end rend,
 // that segment keeps only the codewords up to it and later segments none.
 // A chunk with fewer than lim codewords, or whose lim-th codeword runs past
 // its bytes, makes the index unusable. The round starts (segments 512 m)
 // that fall in the chunk are written too: with the counts so fixed, the
 // codewords before segment g of the chunk are min(raw count before g, lim).
-__global__ __launch_bounds__(256) void index_finish_kernel(const LaunchArgs args, int64_t total) {
-    __shared__ uint32_t s_wsum[kWaves];
-    __shared__ uint32_t s_found;
-    for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
-        int d = 0;
-        while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
-        const DevTensor& T = args.t[d];
-        const int64_t c = item - T.item_begin;
-        uint8_t* const ix = T.index;
-        const auto* h = reinterpret_cast<const IndexHeader*>(ix);
-        if (h->magic != kIndexMagic || h->ok != 1u) continue;
-        const uint32_t S = h->seg_bits;
-        const IndexLayout L = index_layout(T.packed_nbytes, T.n_chunks, S);
-        const uint32_t* base = reinterpret_cast<const uint32_t*>(ix + L.base);
-        uint32_t* rend = reinterpret_cast<uint32_t*>(ix + L.rend);
-        uint32_t* ent = reinterpret_cast<uint32_t*>(ix + L.entries);
-        RoundStart* rounds = reinterpret_cast<RoundStart*>(ix + L.rounds);
-        const uint32_t b0 = base[c], b1 = base[c + 1];
-        int64_t off, nb;
-        chunk_range(T, c, &off, &nb);
-        int64_t lim = T.n_symbols - c * T.chunk_size;
-        lim = lim > T.chunk_size ? T.chunk_size : lim;
-        if (threadIdx.x == 0) s_found = 0;
-        uint32_t pre = 0;  // codewords of the chunk before this block of segments
-        for (uint32_t g0 = b0; g0 < b1; g0 += 256) {
-            const uint32_t g = g0 + threadIdx.x;
-            const uint32_t e = g < b1 ? ent[g] : 0u;
-            const uint32_t cnt = (e >> 4) & 127u;
-            // Block scan (256 threads: waves 0..3).
-            const uint32_t x = wave_scan_incl(cnt);
-            __syncthreads();
-            if ((threadIdx.x & 63) == 63) s_wsum[threadIdx.x >> 6] = x;
-            __syncthreads();
-            uint32_t before = 0, tot = 0;
-            for (uint32_t k = 0; k < 4; ++k) {
-                before += k < (threadIdx.x >> 6) ? s_wsum[k] : 0u;
-                tot += s_wsum[k];
-            }
-            const uint32_t excl = pre + before + x - cnt;  // codewords before segment g
-            if (g < b1 && g % kIndexBlock == 0 && g / kIndexBlock < L.n_rounds) {
-                RoundStart rs;
-                rs.chunk = static_cast<uint32_t>(c);
-                rs.element = static_cast<uint32_t>(c * T.chunk_size +
-                                                   (excl < static_cast<uint64_t>(lim) ? excl : lim));
-                rs.byte = static_cast<uint32_t>(off + (g - b0) * (S / 8));
-                rs.chunk_base = b0;
-                rounds[g / kIndexBlock] = rs;
-            }
-            if (g < b1) {
-                if (excl < static_cast<uint64_t>(lim) && excl + cnt >= static_cast<uint64_t>(lim)) {
-                    // The lim-th codeword is in this segment: walk to its end.
-                    const uint32_t keep = static_cast<uint32_t>(lim - excl);
-                    const uint32_t lo = (g - b0) * S;
-                    uint32_t p = lo + (e & 15u);
-                    for (uint32_t k = 0; k < keep; ++k)
-                        p += codeword_len_at(T.table, T.packed + off, static_cast<uint32_t>(nb), p);
-                    rend[c] = p;
-                    ent[g] = (e & 15u) | (keep << 4);
-                    s_found = p <= 8 * nb ? 1u : 2u;
-                } else if (excl >= static_cast<uint64_t>(lim)) {
-                    ent[g] = e & 15u;  // past the real end
-                }
-            }
-            pre += tot;
+// A wave goes through its chunk's segments 64 at a time with wave scans, so
+// the waves of a workgroup finish four chunks at once with no barrier. The
+// walk reads the decode table from LDS (the table of the tensor of each
+// group of four chunks' first chunk; a wave whose tensor has another table
+// reads it from global memory).
+constexpr uint32_t kFinishWaves = kFinishThreads / 64;
+
+template <bool kLdsTable>
+__device__ __forceinline__ void finish_chunk(const LaunchArgs& args, int64_t item, uint32_t lane,
+                                             uint8_t* seg, const uint32_t* f_wsyms,
+                                             const uint8_t* f_wmeta, const uint8_t* f_len,
+                                             const uint16_t* f_esc) {
+    int d = 0;
+    while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
+    const DevTensor& T = args.t[d];
+    const int64_t c = item - T.item_begin;
+    uint8_t* const ix = T.index;
+    const auto* h = reinterpret_cast<const IndexHeader*>(ix);
+    if (h->magic != kIndexMagic || h->ok != 1u) return;
+    const uint32_t S = h->seg_bits;
+    const IndexLayout L = index_layout(T.packed_nbytes, T.n_chunks, S);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(ix + L.base);
+    uint32_t* rend = reinterpret_cast<uint32_t*>(ix + L.rend);
+    uint32_t* ent = reinterpret_cast<uint32_t*>(ix + L.entries);
+    RoundStart* rounds = reinterpret_cast<RoundStart*>(ix + L.rounds);
+    const uint32_t b0 = base[c], b1 = base[c + 1];
+    int64_t off, nb;
+    chunk_range(T, c, &off, &nb);
+    int64_t lim = T.n_symbols - c * T.chunk_size;
+    lim = lim > T.chunk_size ? T.chunk_size : lim;
+    uint32_t found = 0;  // 1: this lane walked to the lim-th codeword's end within the chunk
+    uint32_t pre = 0;    // codewords of the chunk before this block of segments
+    for (uint32_t g0 = b0; g0 < b1; g0 += 64) {
+        const uint32_t g = g0 + lane;
+        const uint32_t e = g < b1 ? ent[g] : 0u;
+        const uint32_t cnt = (e >> 4) & 127u;
+        const uint32_t x = wave_scan_incl(cnt);
+        const uint32_t tot = __builtin_amdgcn_readlane(x, 63);
+        const uint32_t excl = pre + x - cnt;  // codewords before segment g
+        if (g < b1 && g % kIndexBlock == 0 && g / kIndexBlock < L.n_rounds) {
+            RoundStart rs;
+            rs.chunk = static_cast<uint32_t>(c);
+            rs.element = static_cast<uint32_t>(c * T.chunk_size +
+                                               (excl < static_cast<uint64_t>(lim) ? excl : lim));
+            rs.byte = static_cast<uint32_t>(off + (g - b0) * (S / 8));
+            rs.chunk_base = b0;
+            rounds[g / kIndexBlock] = rs;
         }
-        __syncthreads();
-        if (threadIdx.x == 0 && s_found != 1u) reinterpret_cast<IndexHeader*>(ix)->ok = 0u;
-        __syncthreads();
+        if (g < b1) {
+            if (excl < static_cast<uint64_t>(lim) && excl + cnt >= static_cast<uint64_t>(lim)) {
+                // The lim-th codeword is in this segment: walk to its end
+                // over the segment's bytes.
+                const uint32_t keep = static_cast<uint32_t>(lim - excl);
+                const uint32_t lo = (g - b0) * S;  // a whole byte
+                const uint8_t* bytes = T.packed + off;
+                const uint32_t blo = lo >> 3;
+#pragma unroll
+                for (uint32_t k = 0; k < kWalkBytes; ++k)
+                    seg[k] = blo + k < static_cast<uint64_t>(nb) ? bytes[blo + k] : 0u;
+                uint32_t q;
+                if (kLdsTable) {
+                    q = walk_codewords(seg, e & 15u, keep, f_wsyms, f_wmeta, f_len, f_esc, T.table);
+                } else {
+                    q = walk_codewords(seg, e & 15u, keep,
+                                       reinterpret_cast<const uint32_t*>(T.table + kSymsOffset),
+                                       T.table + kMetaOffset, T.table + kLenOffset,
+                                       reinterpret_cast<const uint16_t*>(T.table + kEscOffset),
+                                       T.table);
+                }
+                const uint32_t p = lo + q;
+                rend[c] = p;
+                ent[g] = (e & 15u) | (keep << 4);
+                found = p <= 8 * nb ? 1u : 2u;
+            } else if (excl >= static_cast<uint64_t>(lim)) {
+                ent[g] = e & 15u;  // past the real end
+            }
+        }
+        pre += tot;
+    }
+    // Every lane of the wave is here (the item test is per wave).
+    const bool ok = __ballot(found == 1u) != 0 && __ballot(found == 2u) == 0;
+    if (lane == 0 && !ok) reinterpret_cast<IndexHeader*>(ix)->ok = 0u;
+}
+
+__global__ __launch_bounds__(kFinishThreads) void index_finish_kernel(const LaunchArgs args,
+                                                                      int64_t total) {
+    __shared__ uint32_t f_wsyms[kWinEntries];
+    __shared__ uint8_t f_wmeta[kWinEntries];
+    __shared__ uint8_t f_len[256];
+    __shared__ uint16_t f_esc[kLdsEscBlocks * kEscBlockEntries];
+    __shared__ __attribute__((aligned(16))) uint8_t f_seg[kFinishWaves][kWalkBytes];
+    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+    const uint8_t* loaded = nullptr;
+    for (int64_t first = static_cast<int64_t>(blockIdx.x) * kFinishWaves; first < total;
+         first += static_cast<int64_t>(gridDim.x) * kFinishWaves) {
+        int d0 = 0;
+        while (d0 + 1 < args.n_tensors && first >= args.t[d0 + 1].item_begin) ++d0;
+        const uint8_t* const table = args.t[d0].table;
+        if (table != loaded) {
+            __syncthreads();  // every wave is done with the previous table
+            loaded = table;
+            const uint4* src = reinterpret_cast<const uint4*>(table + kSymsOffset);
+            for (uint32_t j = threadIdx.x; j < kWinEntries / 4; j += kFinishThreads)
+                reinterpret_cast<uint4*>(f_wsyms)[j] = src[j];
+            const uint4* msrc = reinterpret_cast<const uint4*>(table + kMetaOffset);
+            for (uint32_t j = threadIdx.x; j < kWinEntries / 16; j += kFinishThreads)
+                reinterpret_cast<uint4*>(f_wmeta)[j] = msrc[j];
+            const uint4* lsrc = reinterpret_cast<const uint4*>(table + kLenOffset);
+            for (uint32_t j = threadIdx.x; j < 256 / 16; j += kFinishThreads)
+                reinterpret_cast<uint4*>(f_len)[j] = lsrc[j];
+            const uint32_t nb_esc = header_of(table)->n_esc_blocks;
+            const uint32_t n_esc = nb_esc < static_cast<uint32_t>(kLdsEscBlocks) ? nb_esc : kLdsEscBlocks;
+            const uint16_t* gesc = reinterpret_cast<const uint16_t*>(table + kEscOffset);
+            for (uint32_t j = threadIdx.x; j < n_esc * kEscBlockEntries; j += kFinishThreads)
+                f_esc[j] = gesc[j];
+            __syncthreads();
+        }
+        const int64_t item = first + wv;
+        if (item >= total) continue;
+        int d = d0;
+        while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
+        if (args.t[d].table == loaded) {
+            finish_chunk<true>(args, item, lane, f_seg[wv], f_wsyms, f_wmeta, f_len, f_esc);
+        } else {
+            finish_chunk<false>(args, item, lane, f_seg[wv], f_wsyms, f_wmeta, f_len, f_esc);
+        }
     }
 }
 
@@ -2415,10 +2520,12 @@ extern "C" int aimg_build_index(const aimg_tensor* tensors, int n_tensors, void*
     if (rc != AIMG_OK) return rc;
     rc = aimg::launch_batch<aimg::kModeIndex>(tiny, s, true);
     if (rc != AIMG_OK) return rc;
+    // The finish step: a wave per chunk, four per workgroup.
     const int64_t slots = static_cast<int64_t>(aimg::cu_count()) * 8;
+    const int64_t groups = (chunks + aimg::kFinishWaves - 1) / aimg::kFinishWaves;
     hipLaunchKernelGGL(aimg::index_finish_kernel,
-                       dim3(static_cast<uint32_t>(chunks < slots ? chunks : slots)), dim3(256), 0, s,
-                       plan, chunks);
+                       dim3(static_cast<uint32_t>(groups < slots ? groups : slots)),
+                       dim3(aimg::kFinishThreads), 0, s, plan, chunks);
     err = hipGetLastError();
     if (err != hipSuccess)
         return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
