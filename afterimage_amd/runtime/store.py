@@ -19,11 +19,21 @@ and returns non-owning, possibly unaligned views, as the reference's
 straight into one pinned buffer laid out for ``LayerRing`` (each array at an
 alignment the kernel reads it with), so a streamed layer goes disk -> pinned
 memory -> GPU with no intermediate copy.
+
+``StoreReader(store_dir, direct=True)`` reads with O_DIRECT where the file
+system takes it, as the reference's directio.py does for its weight reads
+(afterimage/runtime/directio.py:1-107): the page cache is bypassed, so read
+rates are the storage's own. O_DIRECT needs block-aligned offsets, lengths
+and memory, so each read goes through a page-aligned bounce buffer that
+holds the aligned span around it. Where O_DIRECT is refused the reader falls
+back to buffered reads and says so (``used_direct``).
 """
 from __future__ import annotations
 
 import dataclasses
 import json
+import mmap
+import os
 import pathlib
 import zlib
 
@@ -34,6 +44,9 @@ from .compressed_store import CompressedLayer, compress_layer
 from .huffman_chunked import ChunkedEncoded
 
 SCHEMA_VERSION = 2
+DIRECT_ALIGNMENT = 4096           # O_DIRECT offsets, lengths and addresses
+DIRECT_BOUNCE_BYTES = 8 << 20     # the bounce buffer of one direct reader
+_O_DIRECT = getattr(os, "O_DIRECT", None)
 COMPRESSED_BLOBS = ("sign_mantissa", "packed", "chunk_offsets", "chunk_nbytes", "sym_lut",
                     "len_lut")
 
@@ -153,7 +166,7 @@ class StoreReader:
     engine's always-on startup checks (streaming_engine.py:843-870): the
     schema version, and a file at least as long as every blob it lists."""
 
-    def __init__(self, store_dir):
+    def __init__(self, store_dir, direct: bool = False):
         self.dir = pathlib.Path(store_dir)
         self.manifest = json.loads((self.dir / "manifest.json").read_text())
         version = self.manifest.get("schema_version")
@@ -170,12 +183,39 @@ class StoreReader:
             raise StoreError("weights.bin at %s is truncated: the manifest references bytes up "
                              "to offset %d but the file has %d" % (self.dir, need, size))
         self._fh = open(path, "rb", buffering=0)
+        self._dfd = None
+        self._bounce = None
+        # True while reads go through O_DIRECT; False when not asked for, or
+        # when the file system refused it (reads are then buffered).
+        self.used_direct = False
+        if direct and _O_DIRECT is not None:
+            try:
+                self._dfd = os.open(str(path), os.O_RDONLY | _O_DIRECT)
+                self._bounce = mmap.mmap(-1, DIRECT_BOUNCE_BYTES)  # page-aligned
+                self.used_direct = True
+            except OSError:
+                self._close_direct()
 
     @property
     def tensors(self) -> dict:
         return self.manifest["tensors"]
 
+    def _close_direct(self) -> None:
+        if self._dfd is not None:
+            os.close(self._dfd)
+        if self._bounce is not None:
+            self._bounce.close()
+        self._dfd = self._bounce = None
+        self.used_direct = False
+
     def _readinto(self, offset: int, view: memoryview) -> None:
+        if self._dfd is not None:
+            try:
+                direct_readinto(lambda b, at: os.preadv(self._dfd, [b], at),
+                                self._bounce, offset, view)
+                return
+            except OSError:
+                self._close_direct()  # this read and later ones go buffered
         self._fh.seek(offset)
         got = 0
         while got < view.nbytes:
@@ -324,6 +364,7 @@ class StoreReader:
                     raise _crc_error(ref, got)
 
     def close(self) -> None:
+        self._close_direct()
         self._fh.close()
 
     def __enter__(self):
@@ -331,6 +372,33 @@ class StoreReader:
 
     def __exit__(self, *exc):
         self.close()
+
+
+def direct_readinto(pread, bounce: mmap.mmap, offset: int, view: memoryview,
+                    alignment: int = DIRECT_ALIGNMENT) -> None:
+    """view.nbytes bytes of the file from `offset` into `view`, through
+    reads that are all aligned (offset, length and memory) to `alignment`:
+    pread(buffer, file_offset) -> bytes read, as os.preadv on an O_DIRECT
+    descriptor, into the page-aligned `bounce` buffer, whose part around
+    each requested span is then copied out. A read that ends before the
+    requested bytes (the end of the file) raises StoreError."""
+    cap = (len(bounce) // alignment) * alignment
+    n = view.nbytes
+    got = 0
+    with memoryview(bounce) as b:
+        while got < n:
+            pos = offset + got
+            a0 = pos - pos % alignment
+            lead = pos - a0
+            want = min(n - got, cap - lead)
+            span = -(-(lead + want) // alignment) * alignment
+            r = pread(b[:span], a0)
+            take = min(want, r - lead)
+            if take <= 0:
+                raise StoreError("short read at offset %d: wanted %d bytes, got %d"
+                                 % (offset, n, got))
+            view[got: got + take] = b[lead: lead + take]
+            got += take
 
 
 def verify_store(store_dir) -> tuple[bool, list[str]]:

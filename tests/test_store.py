@@ -217,3 +217,60 @@ def test_host_block_read_from_the_store_equals_one_built_in_memory(tmp_path):
         assert (x.chunk_size, x.n_symbols, x.shape, x.max_bits) == \
                (y.chunk_size, y.n_symbols, y.shape, y.max_bits)
         assert np.array_equal(x.sym_lut, y.sym_lut) and np.array_equal(x.len_lut, y.len_lut)
+
+
+def _aligned_pread(data: bytes, alignment: int, calls: list):
+    """A pread over `data` that enforces what O_DIRECT enforces: block-aligned
+    file offset and length (a shorter read only at the end of the file)."""
+    def pread(buf, at):
+        assert at % alignment == 0 and buf.nbytes % alignment == 0
+        calls.append((at, buf.nbytes))
+        chunk = data[at: at + buf.nbytes]
+        buf[: len(chunk)] = chunk
+        return len(chunk)
+    return pread
+
+
+@pytest.mark.parametrize("offset,n", [(0, 1), (1, 4095), (4095, 2), (4096, 4096), (5000, 12000),
+                                      (123, 30000), (40000 - 7, 7), (0, 40000)])
+def test_direct_reads_are_aligned_and_exact(offset, n):
+    import mmap
+    from afterimage_amd.runtime.store import direct_readinto
+
+    data = np.random.default_rng(offset + n).integers(0, 256, 40000, dtype=np.uint8).tobytes()
+    bounce = mmap.mmap(-1, 3 * 4096)  # smaller than some reads: several bounces
+    calls = []
+    out = np.zeros(n, np.uint8)
+    direct_readinto(_aligned_pread(data, 4096, calls), bounce, offset, memoryview(out))
+    assert out.tobytes() == data[offset: offset + n]
+    assert all(sz <= 3 * 4096 for _, sz in calls)
+    with pytest.raises(StoreError):  # past the end of the file
+        direct_readinto(_aligned_pread(data, 4096, []), bounce, 40000 - 3, memoryview(np.zeros(8, np.uint8)))
+    bounce.close()
+
+
+def test_direct_reader_reads_what_the_buffered_one_does(tmp_path):
+    W = workloads.bf16_normal((300, 700), seed=3, scale=0.02, outlier_frac=1e-3)
+    with StoreWriter(tmp_path) as sw:
+        sw.add_compressed("w", compress_layer(W, chunk_size=1024))
+        sw.add_tensor("norm", torch.ones(700, dtype=torch.bfloat16))
+    with StoreReader(tmp_path) as rd, StoreReader(tmp_path, direct=True) as dd:
+        # O_DIRECT where the file system takes it (tmpfs and overlay file
+        # systems refuse it: the reader then reads buffered and says so).
+        assert isinstance(dd.used_direct, bool)
+        a, b = rd.layer("w", verify=True), dd.layer("w", verify=True)
+        for f in ("packed", "chunk_offsets", "chunk_nbytes", "sym_lut", "len_lut"):
+            assert np.array_equal(getattr(a.encoded, f), getattr(b.encoded, f))
+        assert torch.equal(a.sign_mantissa, b.sign_mantissa)
+        assert torch.equal(_bits(rd.raw("norm")), _bits(dd.raw("norm")))
+        ha, hb = rd.host_block(["w"], pin=False, verify=True), dd.host_block(["w"], pin=False,
+                                                                             verify=True)
+        # The arrays' regions of the two pinned blocks (the padding between
+        # them is not written).
+        ba, bb = ha.buf.numpy(), hb.buf.numpy()
+        for la, lb in zip(ha.layout, hb.layout):
+            for f in ("packed", "chunk_offsets", "chunk_nbytes", "sign_mantissa"):
+                (a0, an), (b0, bn) = getattr(la, f), getattr(lb, f)
+                size = an * (4 if f.startswith("chunk") else 1)
+                assert (a0, an) == (b0, bn) and np.array_equal(ba[a0:a0 + size], bb[b0:b0 + size])
+        assert torch.equal(_bits(decompress_layer_gpu(b, device="cpu")), _bits(W))
