@@ -15,6 +15,7 @@
 #pragma once
 #include <barrier>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <thread>
 #include <vector>
@@ -43,7 +44,13 @@ enum { hipSuccess = 0 };
 typedef void* hipStream_t;
 enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 0 };
 inline hipError_t hipGetDevice(int* d) { *d = 0; return hipSuccess; }
-inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) { *v = 256; return hipSuccess; }
+// 256 CUs, or AIMG_EMU_CUS of them: a small count gives each workgroup of a
+// persistent grid several items and rounds.
+inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
+    const char* e = std::getenv("AIMG_EMU_CUS");
+    *v = e != nullptr && std::atoi(e) > 0 ? std::atoi(e) : 256;
+    return hipSuccess;
+}
 inline hipError_t hipGetLastError() { return hipSuccess; }
 inline const char* hipGetErrorString(hipError_t) { return "cpu"; }
 

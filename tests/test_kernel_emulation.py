@@ -73,11 +73,14 @@ def _write(d, enc, expect, sm=None):
         f.write("%d %d %d %d\n" % (enc.max_bits, enc.chunk_size, enc.n_symbols, len(enc.chunk_offsets)))
 
 
-def _run(emu, name, mode, index="", runs=None, strided=None):
+def _run(emu, name, mode, index="", runs=None, strided=None, cus=None):
     exe, d = emu
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0")
     env.pop("AIMG_SEGMENT_RUNS", None)
     env.pop("AIMG_RUN_STRIDED", None)
+    env.pop("AIMG_EMU_CUS", None)
+    if cus is not None:
+        env["AIMG_EMU_CUS"] = str(cus)  # a grid of 2 * cus workgroups
     if runs is not None:
         env["AIMG_SEGMENT_RUNS"] = runs
     if strided is not None:
@@ -87,21 +90,21 @@ def _run(emu, name, mode, index="", runs=None, strided=None):
     assert r.returncode == 0 and ": ok" in r.stdout, (r.stdout + r.stderr)[-4000:]
 
 
-def _u8(emu, name, exps, chunk_size, index=""):
+def _u8(emu, name, exps, chunk_size, index="", cus=None):
     exps = np.asarray(exps)
     enc = encode_chunked(torch.as_tensor(exps), chunk_size=chunk_size)
     _write(emu[1] / name, enc, exps.astype(np.uint8))
-    _run(emu, name, "u8", index)
+    _run(emu, name, "u8", index, cus=cus)
 
 
-def _bf16(emu, name, W, chunk_size, index="", runs=None, strided=None):
+def _bf16(emu, name, W, chunk_size, index="", runs=None, strided=None, cus=None):
     layer = compress_layer(W, chunk_size=chunk_size)
     _write(emu[1] / name, layer.encoded, W.reshape(-1).view(torch.int16).numpy(),
            layer.sign_mantissa.numpy())
-    _run(emu, name, "bf16", index, runs, strided)
+    _run(emu, name, "bf16", index, runs, strided, cus)
 
 
-def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None):
+def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None, cus=None):
     W = workloads.bf16_normal((rows, cols), seed, 0.02, outlier_frac=1e-3)
     layer = compress_layer(W, chunk_size=chunk_size)
     g = np.random.default_rng(seed + 1)
@@ -113,7 +116,7 @@ def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None):
     want.numpy().tofile(os.path.join(d, "expect_y.bin"))
     with open(os.path.join(d, "gemv.txt"), "w") as f:
         f.write("%d %d %d\n" % (rows, cols, batch))
-    _run(emu, name, "gemv", index, runs)
+    _run(emu, name, "gemv", index, runs, cus=cus)
 
 
 @pytest.mark.parametrize("batch", [1, 4])
@@ -178,9 +181,11 @@ def test_u8_segment_guesses_all_wrong(emu):
     # codeword boundary, which fixed-length codes never leave. Every thread
     # but the first is wrong on its first pass, so the result rests entirely
     # on the re-decode from the predecessor's end.
+    # The 65536-symbol chunk holds 30000 symbols: 536 segments, two rounds of
+    # 512 threads (the second with 24 segments).
     rng = np.random.default_rng(8)
     _u8(emu, "guess4096", rng.integers(0, 8, 20000), 4096)
-    _u8(emu, "guess65536", rng.integers(0, 8, 70000), 65536)
+    _u8(emu, "guess65536", rng.integers(0, 8, 30000), 65536)
 
 
 # Decoding with the segment index (aimg_build_index): the index is built by
@@ -212,7 +217,7 @@ def test_u8_tiny_packed_buffer_with_index(emu):
 
 def test_u8_index_built_where_every_guess_is_wrong(emu):
     rng = np.random.default_rng(8)
-    _u8(emu, "ix_guess", rng.integers(0, 8, 70000), 65536, index="index")
+    _u8(emu, "ix_guess", rng.integers(0, 8, 30000), 65536, index="index")
 
 
 def test_bf16_vector_path_with_index(emu):
@@ -250,22 +255,26 @@ def test_gemv_16_thread_chunks_with_index(emu):
 @pytest.mark.parametrize("strided", ["1", "0"])
 def test_bf16_segment_runs_cross_chunk_and_workgroup_boundaries(emu, strided):
     # 1024-symbol chunks over 768K weights: about 20 segments of 168 bits a
-    # chunk, and the launch's segments split over several workgroups, so
-    # rounds (strided: rounds in turn to each workgroup; "0": a contiguous
-    # range of rounds per workgroup) start and end inside chunks and inside
-    # vector groups.
+    # chunk, and the launch's 24 rounds on a 4-CU grid of 8 workgroups, 3
+    # rounds each (strided: rounds in turn; "0": a contiguous range of rounds
+    # per workgroup, the partial group carried from round to round), so
+    # rounds start and end inside chunks and inside vector groups, and each
+    # workgroup goes from round to round.
     W = workloads.bf16_normal((96, 8192), 12, 0.02, outlier_frac=1e-3)
-    _bf16(emu, "ix_runs1024_s%s" % strided, W, 1024, index="index", strided=strided)
+    _bf16(emu, "ix_runs1024_s%s" % strided, W, 1024, index="index", strided=strided, cus=4)
 
 
 def test_u8_segment_runs_of_a_ragged_tensor(emu):
-    # The last chunk holds 700 of its 2048 symbols.
+    # The last chunk holds 700 of its 2048 symbols; a 2-CU grid of 4
+    # workgroups takes several rounds each.
     rng = np.random.default_rng(13)
-    _u8(emu, "ix_runs_ragged", rng.integers(90, 135, 2048 * 150 + 700), 2048, index="index")
+    _u8(emu, "ix_runs_ragged", rng.integers(90, 135, 2048 * 150 + 700), 2048, index="index",
+        cus=2)
 
 
 def test_gemv_segment_runs_at_chunk_1024(emu):
-    _gemv(emu, "ix_gemv1024", 128, 2048, 1024, 2, 14, index="index")
+    # A 2-CU grid: each workgroup's contiguous range holds several rounds.
+    _gemv(emu, "ix_gemv1024", 128, 2048, 1024, 2, 14, index="index", cus=2)
 
 
 def test_unusable_index_fallback_over_several_workgroups(emu):
