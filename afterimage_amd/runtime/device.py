@@ -327,8 +327,8 @@ class DeviceTensor:
         chunk's first byte to its last chunk's last byte, and its chunk
         offsets are rebased to that view (a new int32 array per range), so
         that an index holds only the range's segments. The views are cached
-        on this tensor by their ranges. Needs chunks back to back in the
-        packed buffer, as an index does; a range whose index comes out
+        on this tensor by their ranges. An index needs the range's chunks
+        back to back in the packed buffer; a range whose index comes out
         unusable decodes without one."""
         key = tuple((int(a), int(b)) for a, b in ranges)
         hit = self.range_cache.get(key)
@@ -342,10 +342,11 @@ class DeviceTensor:
             if v is self or c1 <= c0:
                 views.append(v)
                 continue
-            # The view starts on the 16-byte boundary at or before the range's
-            # first byte, so its base keeps the buffer's alignment.
-            lo = int(offs[c0]) & ~15
-            hi = int(offs[c1 - 1] + lens[c1 - 1])
+            # The view spans every byte of the range's chunks (wherever they
+            # lie in the buffer) and starts on the 16-byte boundary at or
+            # before the first, so its base keeps the buffer's alignment.
+            lo = int(offs[c0:c1].min()) & ~15
+            hi = int((offs[c0:c1] + np.maximum(lens[c0:c1], 0)).max())
             if not 0 <= lo <= hi <= self.packed.numel():
                 raise ValueError("chunks %d..%d lie outside the packed buffer" % (c0, c1 - 1))
             v.packed = self.packed[lo:hi]
