@@ -1,8 +1,9 @@
 """CPU oracle for the BF16 decode path -- TEST INFRASTRUCTURE, not product code.
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's CPU-baseline leg may
-import this package: as the checker of the GPU decoder, or as the timed CPU
-baseline. ``afterimage_amd`` never imports it.
+import this package: as the reference that the GPU decoder's outputs are
+compared with, or as the timed CPU baseline. ``afterimage_amd`` never imports
+it.
 
 The arithmetic is C (aimg_oracle.c, built by ``make -C oracle``); this module
 loads it with ctypes. What each function restates:

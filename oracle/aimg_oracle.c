@@ -2,8 +2,9 @@
  * CPU oracle for the Afterimage BF16 decode path -- TEST INFRASTRUCTURE.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may
- * load this library, and only as the checker or the timed CPU baseline. The
- * product (afterimage_amd) never calls it.
+ * load this library, and only as the reference that the GPU decoder's
+ * outputs are compared with, or as the timed CPU baseline. The product
+ * (afterimage_amd) never calls it.
  *
  * Each function restates one piece of the reference algorithm:
  *   oracle_decode_chunks    bounded 32-bit MSB-aligned bit reader, one chunk
