@@ -293,7 +293,8 @@ def decompress_linear_gpu(layer: CompressedLayer, x: torch.Tensor, slice_rows: i
     x [..., cols] times W a block of slice_rows rows at a time, each block
     decoded (decompress_rows_gpu's chunk range) and multiplied with
     torch.nn.functional.linear, the outputs concatenated along the last
-    dimension. Returns [..., rows] in x's dtype (bf16, as W).
+    dimension. x must be bf16, the weight's dtype (F.linear refuses mixed
+    dtypes). Returns [..., rows] in bf16.
 
     The blocked path gives the reference's own result: the same weights, bit
     for bit, in the same F.linear calls. Its blocks reuse one staging buffer.
@@ -311,6 +312,8 @@ def decompress_linear_gpu(layer: CompressedLayer, x: torch.Tensor, slice_rows: i
     rows, cols = (int(v) for v in layer.shape)
     if x.dim() < 1 or x.shape[-1] != cols:
         raise ValueError("x must end in a dimension of %d, got shape %s" % (cols, tuple(x.shape)))
+    if x.dtype != torch.bfloat16:
+        raise ValueError("x must be bf16, the weight's dtype; got %s" % x.dtype)
     lead = tuple(x.shape[:-1])
     tokens = int(np.prod(lead)) if lead else 1
     if fused and not 1 <= tokens <= GEMV_MAX_BATCH:
@@ -324,8 +327,8 @@ def decompress_linear_gpu(layer: CompressedLayer, x: torch.Tensor, slice_rows: i
     if fused is None:
         fused = 1 <= tokens <= GEMV_MAX_BATCH
     if fused:
-        xb = x.reshape(tokens, cols).to(torch.bfloat16).contiguous()
-        y = decode_gemv(t, xb, rows, cols).to(x.dtype)
+        xb = x.reshape(tokens, cols).contiguous()
+        y = decode_gemv(t, xb, rows, cols).to(torch.bfloat16)
         return y.reshape(lead + (rows,))
     return decode_linear(t, x, rows, cols, slice_rows)
 

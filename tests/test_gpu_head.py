@@ -132,6 +132,8 @@ def test_errors_and_empty_inputs():
         decompress_linear_gpu(layer, _x((5, 64), 1), fused=True)   # more than 4 rows of x
     with pytest.raises(ValueError):
         decompress_linear_gpu(layer, _x((2, 63), 1))               # wrong width
+    with pytest.raises(ValueError):
+        decompress_linear_gpu(layer, _x((2, 64), 1).float())       # not the weight's dtype
     flat = compress_layer(W.reshape(-1), chunk_size=128)
     with pytest.raises(ValueError):
         decompress_linear_gpu(flat, _x((2, 64), 1))                # not 2-D
