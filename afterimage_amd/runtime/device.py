@@ -323,10 +323,10 @@ class DeviceTensor:
     def indexed_ranges(self, ranges: list[tuple[int, int]]) -> list["DeviceTensor"]:
         """Chunk ranges as tensors that each carry a segment index of their
         own, built now (one batched build and one wait): each range's
-        packed bytes are a view of this tensor's packed buffer from its first
-        chunk's first byte to its last chunk's last byte, and its chunk
-        offsets are rebased to that view (a new int32 array per range), so
-        that an index holds only the range's segments. The views are cached
+        packed bytes are a view of this tensor's packed buffer that spans its
+        chunks' bytes, starting on a 16-byte boundary, and its chunk offsets
+        are rebased to that view (a new int32 array per range), so that an
+        index holds only the range's segments. The views are cached
         on this tensor by their ranges. An index needs the range's chunks
         back to back in the packed buffer; a range whose index comes out
         unusable decodes without one."""
