@@ -300,7 +300,10 @@ class DeviceTensor:
             int(self.index[16:20].cpu().numpy().view(np.uint32)[0]) == 1
 
     def drop_index(self) -> None:
+        """Free this tensor's segment index and the per-range indexes of
+        indexed_ranges."""
         self.index = None
+        self.range_cache.clear()
 
     def chunk_range(self, c0: int, c1: int) -> "DeviceTensor":
         """Chunks [c0, c1) as a tensor of their own, sharing this tensor's

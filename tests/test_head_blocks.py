@@ -51,6 +51,9 @@ def test_chunk_range_views_share_memory():
         if v.n_symbols:
             assert v.sign_mantissa.data_ptr() == t.sign_mantissa.data_ptr() + c0 * 64
         assert v.sign_mantissa.numel() == v.n_symbols
+    t.range_cache[((0, 1),)] = [t.chunk_range(0, 1)]
+    t.drop_index()
+    assert t.index is None and not t.range_cache
     with pytest.raises(ValueError):
         t.chunk_range(2, 1)
     with pytest.raises(ValueError):
