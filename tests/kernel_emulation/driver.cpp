@@ -8,7 +8,9 @@
 // usable; "index-small" gives the build room for the chunk bases only (the
 // index must come out marked unusable, and decoding ignores it);
 // "index-foreign" changes the table checksum the index records after the
-// build (decoding must ignore it).
+// build (decoding must ignore it). AIMG_EMU_COPIES=n decodes the tensor n
+// times in one launch (n descriptors sharing its inputs and index, each with
+// an output of its own), so that workgroups go from tensor to tensor.
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -113,23 +115,28 @@ int main(int argc, char** argv) {
                batch * rows);
         return bad ? 1 : 0;
     }
+    const char* ce = getenv("AIMG_EMU_COPIES");
+    const int copies = ce != nullptr && atoi(ce) > 1 ? atoi(ce) : 1;
     std::vector<uint8_t> outv(n_symbols * (bf16 ? 2 : 1));
-    void* out = exact<uint8_t>(outv);
-    memset(out, 0xAB, outv.size());
-    t.out = out;
-    int rc;
     if (bf16) {
         auto sm = readf(d + "/sm.bin");
         t.sign_mantissa = exact<uint8_t>(sm);
-        rc = aimg_decode_bf16(&t, 1, nullptr);
-    } else {
-        rc = aimg_decode_u8(&t, 1, nullptr);
     }
+    std::vector<aimg_tensor> ts(copies, t);
+    std::vector<void*> outs(copies);
+    for (int c = 0; c < copies; ++c) {
+        outs[c] = exact<uint8_t>(outv);
+        memset(outs[c], 0xAB, outv.size());
+        ts[c].out = outs[c];
+    }
+    const int rc = bf16 ? aimg_decode_bf16(ts.data(), copies, nullptr)
+                        : aimg_decode_u8(ts.data(), copies, nullptr);
     if (rc) { fprintf(stderr, "decode rc=%d: %s\n", rc, aimg_last_error()); return 6; }
     if (expect.size() != outv.size()) { fprintf(stderr, "size mismatch\n"); return 7; }
     size_t bad = 0;
-    for (size_t k = 0; k < outv.size(); ++k) bad += ((const uint8_t*)out)[k] != expect[k];
+    for (int c = 0; c < copies; ++c)
+        for (size_t k = 0; k < outv.size(); ++k) bad += ((const uint8_t*)outs[c])[k] != expect[k];
     printf("%s %s %s: %s (%zu bad bytes of %zu)\n", d.c_str(), argv[2], ix_mode.c_str(),
-           bad ? "MISMATCH" : "ok", bad, outv.size());
+           bad ? "MISMATCH" : "ok", bad, outv.size() * copies);
     return bad ? 1 : 0;
 }

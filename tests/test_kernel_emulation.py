@@ -73,14 +73,17 @@ def _write(d, enc, expect, sm=None):
         f.write("%d %d %d %d\n" % (enc.max_bits, enc.chunk_size, enc.n_symbols, len(enc.chunk_offsets)))
 
 
-def _run(emu, name, mode, index="", runs=None, strided=None, cus=None):
+def _run(emu, name, mode, index="", runs=None, strided=None, cus=None, copies=None):
     exe, d = emu
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0")
     env.pop("AIMG_SEGMENT_RUNS", None)
     env.pop("AIMG_RUN_STRIDED", None)
     env.pop("AIMG_EMU_CUS", None)
+    env.pop("AIMG_EMU_COPIES", None)
     if cus is not None:
         env["AIMG_EMU_CUS"] = str(cus)  # a grid of 2 * cus workgroups
+    if copies is not None:
+        env["AIMG_EMU_COPIES"] = str(copies)  # the tensor decoded this many times in one launch
     if runs is not None:
         env["AIMG_SEGMENT_RUNS"] = runs
     if strided is not None:
@@ -97,11 +100,11 @@ def _u8(emu, name, exps, chunk_size, index="", cus=None):
     _run(emu, name, "u8", index, cus=cus)
 
 
-def _bf16(emu, name, W, chunk_size, index="", runs=None, strided=None, cus=None):
+def _bf16(emu, name, W, chunk_size, index="", runs=None, strided=None, cus=None, copies=None):
     layer = compress_layer(W, chunk_size=chunk_size)
     _write(emu[1] / name, layer.encoded, W.reshape(-1).view(torch.int16).numpy(),
            layer.sign_mantissa.numpy())
-    _run(emu, name, "bf16", index, runs, strided, cus)
+    _run(emu, name, "bf16", index, runs, strided, cus, copies)
 
 
 def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None, cus=None):
@@ -262,6 +265,16 @@ def test_bf16_segment_runs_cross_chunk_and_workgroup_boundaries(emu, strided):
     # workgroup goes from round to round.
     W = workloads.bf16_normal((96, 8192), 12, 0.02, outlier_frac=1e-3)
     _bf16(emu, "ix_runs1024_s%s" % strided, W, 1024, index="index", strided=strided, cus=4)
+
+
+@pytest.mark.parametrize("strided", ["1", "0"])
+def test_bf16_segment_runs_of_several_tensors_in_one_launch(emu, strided):
+    # The tensor three times in one launch on a 4-CU grid: each workgroup
+    # takes rounds of every copy (a piece per tensor), in turn or as
+    # contiguous ranges that cross tensor boundaries.
+    W = workloads.bf16_normal((48, 8192), 19, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "ix_runs_multi_s%s" % strided, W, 1024, index="index", strided=strided, cus=4,
+          copies=3)
 
 
 def test_u8_segment_runs_of_a_ragged_tensor(emu):
