@@ -148,9 +148,11 @@ struct GemvArgs {
 
 struct LaunchArgs {
     DevTensor t[AIMG_MAX_TENSORS];
-    int64_t total_items;
+    int64_t total_items;  // speculative runs: the tensors' elements
     int32_t n_tensors;
-    int32_t strided;  // segment runs: workgroup w takes rounds w, w + grid, ...
+    // Segment runs: workgroup w takes rounds w, w + grid, ... Speculative
+    // runs: a full grid, whose workgroups b and b + grid / 2 split a CU's share.
+    int32_t strided;
     GemvArgs gemv;  // kModeGemv only (one tensor)
 };
 
@@ -2113,9 +2115,11 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
 // chunk decodes it whole, codeword by codeword, as the reference does (table
 // in LDS). Correct for any input, slow; decoders take this path only when a
 // caller passes an index that does not match the tensor's table.
+// el_from: elements below it are left alone (the fused GEMV must not add a
+// product twice).
 template <int kMode>
 __device__ void run_fallback(const Tables& tb, const LaunchArgs& args, const DevTensor& T,
-                             int64_t c_lo, int64_t c_hi) {
+                             int64_t c_lo, int64_t c_hi, int64_t el_from = 0) {
     for (int64_t c = c_lo + threadIdx.x; c < c_hi; c += kThreads) {
         int64_t off, nb;
         chunk_range(T, c, &off, &nb);
@@ -2138,7 +2142,7 @@ __device__ void run_fallback(const Tables& tb, const LaunchArgs& args, const Dev
             } else {
                 sym = escape<true>(tb, tb.syms[idx], w, &len);
             }
-            store_one<kMode>(T, args.gemv, c * T.chunk_size + k, sym);
+            if (c * T.chunk_size + k >= el_from) store_one<kMode>(T, args.gemv, c * T.chunk_size + k, sym);
             p += len;
         }
     }
@@ -2222,6 +2226,546 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void run_kernel(const Laun
             run_fallback<kMode>(tb, args, T, c_lo, c_hi);
         }
         at += U;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Speculative segment runs: decode without an index of tensors whose chunks
+// hold kRunMinChunk symbols or more (vector path).
+//
+// A workgroup takes a contiguous range of the launch's chunks and walks it in
+// rounds of 512 segments that run across chunk boundaries: segment k of a
+// chunk covers its bits [k S, (k + 1) S) (its last segment is shorter), and a
+// round is any 512 consecutive segments of the range. A chunk's first
+// segment starts at a known codeword boundary (the chunk's first bit), and
+// so does a round's first segment (the end of the previous round's last);
+// every other thread starts 32 bits early on a guess and is checked against
+// its predecessor's end, as in decode_kernel. Each codeword gets its rank in
+// its chunk (a scan over the round that restarts at each chunk's first
+// segment and carries on from round to round): the symbol of rank r of chunk
+// c is element c * chunk_size + r, and ranks at or past the chunk's output
+// count (the zero bits that pad a chunk to whole bytes) are dropped. A
+// round's output is therefore one run of elements, compacted in LDS and
+// stored whole, as the segment runs with an index store theirs.
+//
+// The threads' slots are interleaved by lane: word j of lane l of wave w sits
+// at row j, column l of the wave's block, so the lanes of a wave write and
+// read their slots in 64 different banks whatever their positions.
+// ---------------------------------------------------------------------------
+
+constexpr uint32_t kSpecChunks = 64;            // chunks a round's table holds
+constexpr uint32_t kSlotRows = kSlotWords + 1;  // a slot's words: kSlotCap symbols and the word after
+constexpr uint32_t kSpecSlotBytes = kWaves * kSlotRows * 64 * 4;
+constexpr uint32_t kSpecStageBytes = kLeadBytes + kSpecSlotBytes;
+// Dense stage limit: a carried partial group and kSlotCap symbols a segment.
+constexpr uint32_t kSpecDense = kLeadBytes + kThreads * kSlotCap;
+static_assert(kSpecStageBytes >= kSpecDense + 4, "a dense round fits the stage");
+static_assert(kSpecStageBytes >= kStoreBatch * kThreads * 8, "store batches read inside the stage");
+static_assert(kSpecStageBytes >= kStoreBatch * kThreads * 16 / 2, "u8 store batches too");
+// Chunks larger than this go to decode_kernel (their bit counts must fit 32 bits).
+constexpr int64_t kSpecMaxChunkBytes = int64_t{1} << 28;
+
+struct __attribute__((aligned(16))) SpecLds {
+    uint8_t wmeta[kWinEntries];
+    uint8_t len[256];
+    uint16_t esc[kLdsEscBlocks * kEscBlockEntries];
+    uint32_t wsyms[kWinEntries];
+    // A round's table: the chunk of its first segment and the next ones, two
+    // sets (this round's and the next one's). cseg: a chunk's first segment
+    // counted from the round's first ([kSpecChunks]: the end of the table's
+    // segments); coff: byte offset ([kSpecChunks]: the table's last byte + 1);
+    // cbits: bits.
+    int32_t cseg[2][kSpecChunks + 1];
+    uint32_t coff[2][kSpecChunks + 1];
+    uint32_t cbits[2][kSpecChunks];
+    // Per wave, from its last lane: codewords, the wave-exclusive count of its
+    // last chunk head + 1 (0: none), that lane's end, disagreement inside the
+    // wave. From lane 0: its start and whether that start is known.
+    uint32_t rec[kWaves][4];
+    uint32_t rec0[kWaves][2];
+    // The round's last segment: its end (chunk bit), its chunk's codewords up
+    // to its end, the stage byte after the round's symbols.
+    uint32_t last[4];
+    uint32_t bad;  // a chunk of the round does not hold its symbols
+    uint32_t tile[kRunTileWords];
+    __attribute__((aligned(16))) uint8_t stage[kSpecStageBytes];
+};
+
+// Inclusive max over the wave (every lane active).
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint32_t wave_scan_max(uint32_t v) {
+    uint32_t x = v;
+    x = umax(x, dpp<0x111>(x));
+    x = umax(x, dpp<0x112>(x));
+    x = umax(x, dpp<0x114>(x));
+    x = umax(x, dpp<0x118>(x));
+    x = umax(x, dpp<0x142, 0xA>(x));
+    x = umax(x, dpp<0x143, 0xC>(x));
+    return x;
+}
+
+// One lookup's symbols into an interleaved slot (`lane` points at the lane's
+// word 0; word j is lane[64 j]) at byte q, as slot_put does it.
+__device__ __forceinline__ void slot_put_il(uint32_t* lane, uint32_t q, uint32_t syms) {
+    const uint32_t b = q & 3u;
+    const uint64_t v = static_cast<uint64_t>(syms) << (8 * b);
+    uint32_t* w = lane + (q >> 2) * 64;
+    lds_or(w, static_cast<uint32_t>(v));
+    w[64] = static_cast<uint32_t>(v >> 32);
+}
+
+// decode_run into an interleaved slot. cend: the bit where the segment's
+// chunk ends. The tile holds the next chunk's bits after it; the bounded
+// reader reads zeros there, and only the last window can meet them (every
+// earlier codeword ends before x <= cend), so that window is looked up again
+// with the bits from cend on cleared when it reaches past cend.
+template <bool kGlobalEsc>
+__device__ __forceinline__ Adv decode_run_il(TileRef below, const Tables& tb, uint32_t p,
+                                             uint32_t x, uint32_t cend, uint32_t* lane) {
+    lane[0] = 0u;
+    if (p >= x) return {p, 0u};
+    uint32_t q = 0;
+    const Reader rd = reader_at(below, p);
+    Step s = lookup<true>(below, tb, rd.p, rd.sh, rd.pair);
+    uint32_t syms, adv, c;
+    take<kGlobalEsc>(tb, s, &syms, &adv, &c);
+    uint32_t pn = s.p + adv;
+    while (pn < x) {
+        Step t = lookup<false>(below, tb, pn, pn - s.m, s.next);
+        slot_put_il(lane, q, syms);
+        q += c;
+        t.syms = tb.syms[t.idx];
+        s = t;
+        take<kGlobalEsc>(tb, s, &syms, &adv, &c);
+        pn = s.p + adv;
+    }
+    if (cend - s.p < 16u) {
+        const uint32_t w = s.w & ~(0xFFFFFFFFu >> (cend - s.p));
+        const uint32_t idx = w >> (32 - kWinBits);
+        const uint32_t meta = tb.meta[idx];
+        syms = tb.syms[idx];
+        adv = meta & 31u;
+        c = meta >> 5;
+        if (adv == 0) {
+            syms = escape<kGlobalEsc>(tb, syms, w, &adv);
+            c = 1;
+        }
+    }
+    uint32_t kept;  // 1..4
+    const uint32_t e = cut_window(tb, s.p, s.p + adv, syms, c, x, &kept);
+    slot_put_il(lane, q, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
+    return {e, q + kept};
+}
+
+// One chunk per lane (chunk c0 + lane) of a round's table, in flight.
+struct SpecTabFetch {
+    uint32_t co, cn;
+};
+
+__device__ __forceinline__ void spec_tab_issue(SpecTabFetch& F, const DevTensor& T, uint32_t c0,
+                                               uint32_t lane) {
+    const uint64_t n4 = 4 * static_cast<uint64_t>(T.n_chunks);
+    const uint32_t lim = n4 < 0xFFFFFFFFull ? static_cast<uint32_t>(n4) : 0xFFFFFFFCu;
+    const uint32_t at = 4 * (c0 + lane);
+    F.co = __builtin_amdgcn_raw_buffer_load_b32(buffer_of(T.offsets, lim), at, 0, 0);
+    F.cn = __builtin_amdgcn_raw_buffer_load_b32(buffer_of(T.nbytes, lim), at, 0, 0);
+}
+
+struct SpecTab {
+    uint32_t n_tab;  // chunks of the table (those below the piece's end)
+    int32_t end;     // segments of the table counted from the round's first
+    bool bad;        // chunks not back to back, empty, or too large
+    uint32_t off0;   // byte offset of the table's first chunk
+};
+
+// The fetched chunks into table set `set` (written by one wave; every wave
+// computes the same result). k0: the round's first segment in chunk c0;
+// first_off: where chunk c0 must start (the previous table's view of it).
+__device__ __forceinline__ SpecTab spec_tab_commit(const SpecTabFetch& F, const DevTensor& T,
+                                                   SpecLds& lds, uint32_t set, uint32_t c0,
+                                                   uint32_t cb, uint32_t k0, uint32_t first_off,
+                                                   bool check_first, uint32_t S, uint32_t lane,
+                                                   bool writer) {
+    consume(F.co);
+    consume(F.cn);
+    const uint32_t c = c0 + lane;
+    const bool valid = c < cb;
+    int64_t off = static_cast<int32_t>(F.co), nb = static_cast<int32_t>(F.cn);
+    off = off < 0 ? 0 : (off > T.packed_nbytes ? T.packed_nbytes : off);
+    nb = nb < 0 ? 0 : (nb > T.packed_nbytes - off ? T.packed_nbytes - off : nb);
+    const bool huge = nb >= kSpecMaxChunkBytes;
+    const uint32_t nbv = valid && !huge ? static_cast<uint32_t>(nb) : 0u;
+    const uint32_t offv = static_cast<uint32_t>(off);
+    const uint32_t nseg = (8 * nbv + S - 1) / S;
+    const int64_t lim = T.n_symbols - static_cast<int64_t>(c) * T.chunk_size;
+    const uint32_t incl = wave_scan_incl(nseg);
+    const uint32_t prev_end = lane_below(offv + nbv);
+    const bool bad = valid && (huge || (nseg == 0 && lim > 0) ||
+                               (lane > 0 && offv != prev_end) ||
+                               (lane == 0 && check_first && offv != first_off));
+    const uint64_t vm = __ballot(valid);
+    const uint32_t n_tab = static_cast<uint32_t>(__builtin_popcountll(vm));  // lanes 0 .. n_tab - 1
+    const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
+    const uint32_t end_off = static_cast<uint32_t>(__builtin_amdgcn_readlane(
+        static_cast<int>(offv + nbv), static_cast<int>(n_tab > 0 ? n_tab - 1 : 0)));
+    const bool any_bad = __ballot(bad) != 0;
+    const uint32_t off0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(offv), 0));
+    if (writer) {
+        lds.cseg[set][lane] = static_cast<int32_t>(incl - nseg) - static_cast<int32_t>(k0);
+        lds.coff[set][lane] = valid ? offv : end_off;
+        lds.cbits[set][lane] = 8 * nbv;
+        if (lane == 0) {
+            lds.cseg[set][kSpecChunks] = static_cast<int32_t>(total) - static_cast<int32_t>(k0);
+            lds.coff[set][kSpecChunks] = end_off;
+        }
+    }
+    return {n_tab, static_cast<int32_t>(total) - static_cast<int32_t>(k0), any_bad, uniform(off0)};
+}
+
+__device__ __forceinline__ void spec_tile_issue(uint32_t (&raw)[kTileBatch], const DevTensor& T,
+                                                uint32_t A0, uint32_t tid) {
+    const __amdgpu_buffer_rsrc_t rs = buffer_of(T.packed, T.packed_n32);
+    const uint32_t last = last_word(T);
+#pragma unroll
+    for (uint32_t k = 0; k < kTileBatch; ++k) {
+        const uint32_t A = A0 + 4 * (k * kThreads + tid);
+        raw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, word_at(A, last), 0, 0);
+    }
+}
+
+__device__ __forceinline__ void spec_tile_commit(const uint32_t (&raw)[kTileBatch], const DevTensor& T,
+                                                 uint32_t A0, uint32_t tid, uint32_t* tile) {
+#pragma unroll
+    for (uint32_t k = 0; k < kTileBatch; ++k) consume(raw[k]);
+    const uint32_t last = last_word(T);
+    uint32_t* const top = tile + kRunTileWords - 1;
+#pragma unroll
+    for (uint32_t k = 0; k < kTileBatch; ++k) {
+        const uint32_t j = k * kThreads + tid;
+        if (j >= kRunTileWords) continue;
+        const uint32_t A = A0 + 4 * j;
+        uint32_t v = raw[k];
+        v >>= 8 * ((A - word_at(A, last)) & 3u);
+        *(top - j) = A < T.packed_n32 ? be_word(v, T.packed_n32 - A, 0) : 0u;
+    }
+}
+
+// The chunk of the table set that holds segment g of the round: the last of
+// the n_tab chunks whose first segment is at or before g.
+__device__ __forceinline__ uint32_t spec_chunk_of(const SpecLds& lds, uint32_t set, uint32_t n_tab,
+                                                  uint32_t g) {
+    uint32_t j = 0;
+#pragma unroll
+    for (uint32_t step = kSpecChunks / 2; step >= 1; step >>= 1)
+        if (j + step < n_tab && lds.cseg[set][j + step] <= static_cast<int32_t>(g)) j += step;
+    return j;
+}
+
+// Chunks [ca, cb) of tensor T (all of them below n_jobs).
+template <int kMode, int kGroup>
+__device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, const LaunchArgs& args,
+                           const DevTensor& T, uint32_t ca, uint32_t cb, const uint8_t* table) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u, w = tid >> 6;
+    const uint32_t S = segment_bits(tb.min_len);
+    const int64_t cs = T.chunk_size;
+    // The piece's first table and words; the decode table (when it changes)
+    // loads while they arrive.
+    SpecTabFetch TF;
+    spec_tab_issue(TF, T, ca, lane);
+    if (table != nullptr) {
+        __syncthreads();  // every thread is done with the previous table
+        load_table(table, tid, lds.wsyms, lds.wmeta, lds.len, lds.esc);
+    }
+    uint32_t b = 0;
+    SpecTab tab = spec_tab_commit(TF, T, lds, b, ca, cb, 0u, 0u, false, S, lane, w == 0);
+    uint32_t c0 = ca;     // chunk of the round's first segment
+    uint32_t p0 = 0;      // chunk bit where its first codeword starts (k0 > 0)
+    uint32_t rank0 = 0;   // codewords of chunk c0 before the round
+    uint32_t lead = 0;    // carried symbols at the front of the stage
+    int64_t a0 = static_cast<int64_t>(ca) * cs;  // element of stage byte 0
+    uint32_t A0 = tab.off0;  // packed byte of the round's first segment
+    int64_t fall_from = tab.bad ? a0 : -1;  // the first element the exact fallback writes
+    uint32_t raw[kTileBatch];
+    if (fall_from < 0) spec_tile_issue(raw, T, A0, tid);
+    if (tid == 0) lds.bad = 0u;
+    __syncthreads();  // table set 0 is written
+    uint32_t jj = 0;
+    if (fall_from < 0) {
+        spec_tile_commit(raw, T, A0, tid, lds.tile);
+        jj = spec_chunk_of(lds, b, tab.n_tab, tid);
+    }
+    __syncthreads();  // the first round's words are in the tile
+
+    TileRef below = (TileRef)(lds.tile + kRunTileWords - 2);
+    asm volatile("" : "+v"(below));
+    uint8_t* const stage = lds.stage;
+    uint32_t* const slot = reinterpret_cast<uint32_t*>(lds.stage + kLeadBytes) + w * kSlotRows * 64 + lane;
+    const int64_t piece_end = static_cast<int64_t>(cb) * cs < T.n_symbols ? static_cast<int64_t>(cb) * cs
+                                                                         : T.n_symbols;
+    while (fall_from < 0) {
+        const int32_t tab_end = tab.end;
+        const uint32_t ns = uniform(static_cast<uint32_t>(tab_end < static_cast<int32_t>(kThreads) ? tab_end
+                                                                                     : kThreads));
+        // The next round: its first segment is segment ns of this one.
+        const int32_t nx = lds.cseg[b][lane + 1];
+        const uint32_t done = static_cast<uint32_t>(
+            __builtin_popcountll(__ballot(lane < tab.n_tab && nx <= static_cast<int32_t>(ns))));
+        const uint32_t c0n = c0 + done;
+        const bool more = c0n < cb;
+        const uint32_t k0n = done < tab.n_tab ? uniform(static_cast<uint32_t>(
+                                                    static_cast<int32_t>(ns) - lds.cseg[b][done]))
+                                              : 0u;
+        const uint32_t offn = uniform(lds.coff[b][done]);
+        const uint32_t A0n = offn + k0n * (S / 8);
+        __builtin_amdgcn_s_setprio(3);
+        if (more) {
+            spec_tile_issue(raw, T, A0n, tid);
+            spec_tab_issue(TF, T, c0n, lane);
+        }
+        SmBatch<kMode> smb;
+        sm_issue<kMode, kGroup>(smb, T, a0, tid, kThreads, static_cast<uint32_t>(piece_end));
+
+        // This thread's segment: segment kseg of chunk c0 + jj.
+        const bool active = tid < ns;
+        const int32_t kseg = static_cast<int32_t>(tid) - lds.cseg[b][jj];
+        const uint32_t rel = 8u * (lds.coff[b][jj] - A0);  // tile bit of the chunk's bit 0 (mod 2^32)
+        const uint32_t cbits = lds.cbits[b][jj];
+        const uint32_t lo_c = static_cast<uint32_t>(kseg) * S;
+        const uint32_t hi_c = lo_c + S < cbits ? lo_c + S : cbits;
+        const uint32_t lo = rel + lo_c, hi = rel + hi_c, cend = rel + cbits;
+        const bool known = !active || kseg == 0 || tid == 0;
+        uint32_t f = 0, e = 0, cnt = 0;
+        __builtin_amdgcn_s_setprio(0);
+        if (active) {
+            Adv a;
+            if (global_esc) {
+                f = kseg == 0 ? lo : tid == 0 ? rel + p0 : advance<true>(below, tb, lo - kOverlapBits, lo);
+                a = decode_run_il<true>(below, tb, f, hi, cend, slot);
+            } else {
+                f = kseg == 0 ? lo : tid == 0 ? rel + p0 : advance<false>(below, tb, lo - kOverlapBits, lo);
+                a = decode_run_il<false>(below, tb, f, hi, cend, slot);
+            }
+            e = a.p;
+            cnt = a.n;
+        }
+        __builtin_amdgcn_s_setprio(1);
+        // Agreement and scans. Each wave checks its lanes against the lane
+        // below and scans its counts; its last lane and lane 0 leave a record,
+        // from which, after one barrier, every wave checks the waves' first
+        // lanes and finds its codewords' ranks.
+        const bool head = active && kseg == 0;
+        uint32_t incl, hm;
+        for (;;) {
+            const uint32_t ep0 = lane_below(e);
+            incl = wave_scan_incl(cnt);
+            hm = wave_scan_max(head ? incl - cnt + 1u : 0u);
+            const bool wbad = __ballot(!known && lane != 0 && f != ep0) != 0;
+            if (lane == 63) {
+                lds.rec[w][0] = incl;
+                lds.rec[w][1] = hm;
+                lds.rec[w][2] = e;
+                lds.rec[w][3] = wbad ? 1u : 0u;
+            }
+            if (lane == 0) {
+                lds.rec0[w][0] = f;
+                lds.rec0[w][1] = known ? 1u : 0u;
+            }
+            __syncthreads();
+            const uint32_t lw = lane & (kWaves - 1);
+            const bool xbad = lw > 0 && lds.rec0[lw][1] == 0u && lds.rec0[lw][0] != lds.rec[lw - 1][2];
+            if (__ballot(lane < kWaves && (lds.rec[lw][3] != 0u || xbad)) == 0) break;
+            // Rare: threads whose start disagrees with their predecessor's
+            // end decode again from it. Thread 0 and chunk starts are always
+            // right, so pass k puts thread k right at the latest.
+            const uint32_t ep = lane == 0 ? (w > 0 ? lds.rec[w - 1][2] : 0u) : ep0;
+            const bool redo = !known && f != ep;
+            __syncthreads();  // the records are read before they are written again
+            if (redo) {
+                f = ep;
+                const Adv a = global_esc ? decode_run_il<true>(below, tb, f, hi, cend, slot)
+                                         : decode_run_il<false>(below, tb, f, hi, cend, slot);
+                e = a.p;
+                cnt = a.n;
+            }
+        }
+        // Codewords of this lane's chunk before it: from its last head in the
+        // wave, or carried from the waves before (and the rounds before).
+        const uint32_t r_tot = lds.rec[lane & (kWaves - 1)][0];
+        const uint32_t r_hm = lds.rec[lane & (kWaves - 1)][1];
+        uint32_t carry = 0;
+        bool found = false;
+        for (int32_t v = static_cast<int32_t>(w) - 1; v >= 0; --v) {
+            const uint32_t tv = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(r_tot), v));
+            const uint32_t hv = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(r_hm), v));
+            if (hv != 0u) {
+                carry += tv - (hv - 1u);
+                found = true;
+                break;
+            }
+            carry += tv;
+        }
+        if (!found) carry += rank0;
+        const uint32_t xw = incl - cnt;
+        const uint32_t rank = hm != 0u ? xw - (hm - 1u) : carry + xw;
+        // Stage place: chunk jj's element r is stage byte
+        // lead + jj cs + r - min(rank0, lim of chunk c0).
+        const int64_t lim64 = T.n_symbols - static_cast<int64_t>(c0 + jj) * cs;
+        const uint32_t lim = static_cast<uint32_t>(lim64 < cs ? lim64 : cs);
+        const int64_t lim0_64 = T.n_symbols - static_cast<int64_t>(c0) * cs;
+        const uint32_t lim0 = static_cast<uint32_t>(lim0_64 < cs ? lim0_64 : cs);
+        const uint32_t base0 = rank0 < lim0 ? rank0 : lim0;
+        const uint32_t kept = rank < lim ? (cnt < lim - rank ? cnt : lim - rank) : 0u;
+        const int64_t pos64 = static_cast<int64_t>(lead) + static_cast<int64_t>(jj) * cs +
+                              (rank < lim ? rank : lim) - base0;
+        const bool at_end = hi_c == cbits;  // the chunk's last segment
+        const bool broken = active && ((at_end && static_cast<uint64_t>(rank) + cnt < lim) || pos64 < 0 ||
+                                       pos64 + kept > kSpecDense);
+        if (broken) lds.bad = 1u;
+        const uint32_t dpos = broken ? 0u : static_cast<uint32_t>(pos64);
+        if (active && tid == ns - 1) {
+            lds.last[0] = e - rel;
+            lds.last[1] = rank + cnt;
+            lds.last[2] = dpos + kept;
+        }
+        // Compaction, part 1: the slot into registers (the dense stage
+        // overlaps the slots).
+        const uint32_t m = active && !broken ? kept : 0u;
+        const uint32_t head0 = (4u - (dpos & 3u)) & 3u;
+        const uint32_t hb = head0 < m ? head0 : m;  // bytes before the first aligned word
+        const uint32_t nbody = (m - hb) >> 2;
+        const uint32_t ntail = m - hb - 4 * nbody;
+        uint32_t rw[kSlotRows];
+        {
+            const auto* sl = lds_ptr(slot);
+#pragma unroll
+            for (uint32_t j = 0; j < kSlotRows; ++j) rw[j] = sl[j * 64];
+        }
+        const uint32_t tv = __builtin_amdgcn_alignbyte(
+            slot[(nbody + 1 < kSlotRows ? nbody + 1 : kSlotRows - 1) * 64], slot[nbody * 64], hb);
+        // Every thread is past its decode: the next round's words and table.
+        SpecTab tabn = tab;
+        if (more) {
+            spec_tile_commit(raw, T, A0n, tid, lds.tile);
+            tabn = spec_tab_commit(TF, T, lds, b ^ 1u, c0n, cb, k0n, offn, true, S, lane, w == 0);
+        }
+        __syncthreads();  // B: slots read; the next table and words written
+        const bool bad_round = lds.bad != 0u;
+        const uint32_t avail = uniform(lds.last[2]);
+        const uint32_t p0n = uniform(lds.last[0]);
+        const uint32_t rank0n = uniform(lds.last[1]);
+        if (!bad_round) {
+            // Head: the last hb bytes of a word (a byte at an odd address,
+            // then an aligned pair); body: whole words; tail: the first
+            // ntail bytes of a word (an aligned pair, then a byte).
+            uint8_t* dst = stage + dpos;
+            if (hb & 1u) dst[0] = static_cast<uint8_t>(rw[0]);
+            if (hb >= 2) *reinterpret_cast<uint16_t*>(dst + hb - 2) = static_cast<uint16_t>(rw[0] >> (8 * (hb - 2)));
+            uint32_t* body = reinterpret_cast<uint32_t*>(dst + hb);
+#pragma unroll
+            for (uint32_t j = 0; j + 1 < kSlotRows; ++j)
+                if (j < nbody) body[j] = __builtin_amdgcn_alignbyte(rw[j + 1], rw[j], hb);
+            uint8_t* tl = dst + hb + 4 * nbody;
+            if (ntail >= 2) *reinterpret_cast<uint16_t*>(tl) = static_cast<uint16_t>(tv);
+            if (ntail & 1u) tl[ntail - 1] = static_cast<uint8_t>(tv >> (8 * (ntail - 1)));
+        }
+        const uint32_t jjn = more ? spec_chunk_of(lds, b ^ 1u, tabn.n_tab, tid) : 0u;
+        __syncthreads();  // C: the round's symbols are in place
+        if (bad_round) {
+            fall_from = a0;
+            break;
+        }
+        // Whole vector groups, never past the piece's end.
+        const int64_t room = (piece_end - a0) / kGroup;
+        const uint32_t nfull0 = avail / kGroup;
+        const uint32_t nfull = room < static_cast<int64_t>(nfull0) ? static_cast<uint32_t>(room > 0 ? room : 0)
+                                                                  : nfull0;
+        __builtin_amdgcn_s_setprio(2);
+        store_round<kMode, kGroup, true>(smb, T, args.gemv, stage, a0, nfull, tid, kThreads);
+        // The partial vector group moves to the front.
+        const uint32_t rem0 = avail - nfull * kGroup;
+        const uint32_t rem = rem0 < static_cast<uint32_t>(kGroup) ? rem0 : kGroup - 1u;
+        uint2 keep0 = make_uint2(0u, 0u), keep1 = make_uint2(0u, 0u);
+        if (tid == 0 && rem != 0) {
+            const uint2* src = reinterpret_cast<const uint2*>(stage + nfull * kGroup);
+            keep0 = src[0];
+            keep1 = src[1];
+        }
+        __syncthreads();  // D: the round is stored
+        if (tid == 0) {
+            reinterpret_cast<uint2*>(stage)[0] = keep0;
+            reinterpret_cast<uint2*>(stage)[1] = keep1;
+            lds.bad = 0u;
+        }
+        a0 += static_cast<int64_t>(nfull) * kGroup;
+        lead = rem;
+        if (!more) break;
+        if (tabn.bad) {
+            fall_from = a0;
+            break;
+        }
+        // The next round continues chunk c0n at segment k0n (> 0), or starts it.
+        rank0 = k0n > 0 ? rank0n : 0u;
+        p0 = k0n > 0 ? p0n : 0u;
+        c0 = c0n;
+        A0 = A0n;
+        b ^= 1u;
+        tab = tabn;
+        jj = jjn;
+    }
+    __syncthreads();  // the carried symbols are at the front
+    if (fall_from < 0) {
+        if (tid < lead) store_one<kMode>(T, args.gemv, a0 + tid, stage[tid]);
+    } else {
+        // A chunk that does not hold its symbols, or chunks not back to back:
+        // from fall_from on, each chunk is decoded by one thread codeword by
+        // codeword (exact on any input).
+        run_fallback<kMode>(tb, args, T, fall_from / cs, cb, fall_from);
+    }
+    __syncthreads();  // LDS is free for the next piece
+}
+
+// The launch's tensors in one sequence of elements; each workgroup takes the
+// chunks whose first element lies in its share. On a full grid (args.strided
+// set) workgroups b and b + grid / 2 are taken to share a CU and split one
+// CU's share.
+template <int kMode, int kGroup>
+__global__ __launch_bounds__(kThreads, kWavesPerSimd) void spec_kernel(const LaunchArgs args) {
+    __shared__ SpecLds lds;
+    Tables tb;
+    tb.syms = lds.wsyms;
+    tb.meta = lds.wmeta;
+    tb.len = lds.len;
+    tb.esc = lds.esc;
+    const uint8_t* loaded = nullptr;
+    const int64_t N = args.total_items;
+    const uint32_t G = gridDim.x;
+    const uint32_t P = args.strided != 0 && G % 2 == 0 ? G / 2 : G;
+    const uint32_t s = blockIdx.x % P, h = blockIdx.x / P;
+    const int64_t lo_cu = N * s / P, hi_cu = N * (s + 1) / P;
+    const int64_t mid = (lo_cu + hi_cu) / 2;
+    const int64_t L = P == G ? lo_cu : (h == 0 ? lo_cu : mid);
+    const int64_t R = P == G ? hi_cu : (h == 0 ? mid : hi_cu);
+    int64_t O = 0;  // first element of tensor d in the sequence
+    for (int d = 0; d < args.n_tensors; ++d) {
+        const DevTensor& T = args.t[d];
+        const int64_t cs = T.chunk_size;
+        int64_t ca = L - O <= 0 ? 0 : (L - O + cs - 1) / cs;
+        int64_t cb = R - O <= 0 ? 0 : (R - O + cs - 1) / cs;
+        ca = ca < T.n_jobs ? ca : T.n_jobs;
+        cb = cb < T.n_jobs ? cb : T.n_jobs;
+        O += T.n_symbols;
+        if (ca >= cb) continue;
+        const uint8_t* const table = uniform(T.table);
+        const auto* hdr = header_of(table);
+        tb.sym0 = hdr->sym0;
+        tb.min_len = hdr->min_len >= 1 ? hdr->min_len : 1u;
+        tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(table + kEscOffset);
+        const bool global_esc = hdr->n_esc_blocks > static_cast<uint32_t>(kLdsEscBlocks);
+        spec_piece<kMode, kGroup>(lds, tb, global_esc, args, T, static_cast<uint32_t>(ca),
+                                  static_cast<uint32_t>(cb), table != loaded ? table : nullptr);
+        loaded = table;
     }
 }
 
@@ -2324,11 +2868,40 @@ int launch_run(Batch& B, hipStream_t s) {
     return AIMG_OK;
 }
 
+// The speculative segment-run kernel over the batch's tensors: each workgroup
+// takes the chunks whose first element lies in its share of the tensors'
+// elements (a grid of one workgroup per chunk up to two per CU).
+template <int kMode>
+int launch_spec(Batch& B, hipStream_t s) {
+    if (B.m == 0) return AIMG_OK;
+    B.args.n_tensors = B.m;
+    int64_t elements = 0, chunks = 0;
+    for (int d = 0; d < B.m; ++d) {
+        elements += B.args.t[d].n_symbols;
+        chunks += B.args.t[d].n_jobs;
+    }
+    B.args.total_items = elements;
+    const int64_t slots = static_cast<int64_t>(cu_count()) * kBlocksPerCu;
+    const int64_t grid = chunks < slots ? chunks : slots;
+    // A full grid: workgroups b and b + grid / 2 share a CU and split its share.
+    B.args.strided = grid == slots ? 1 : 0;
+    constexpr int kVecGroup = kMode == kModeU8 ? 16 : 8;
+    hipLaunchKernelGGL((spec_kernel<kMode, kVecGroup>), dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0,
+                       s, B.args);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+        return fail(AIMG_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+    return AIMG_OK;
+}
+
 // Tensors with a segment index (chunks of kRunMinChunk symbols or more, the
 // vector path's alignment) go to `run`, the segment-run kernel, when `run`
-// is given; the others decode chunk by chunk without it.
+// is given; tensors without one that meet the same conditions go to `spec`,
+// the speculative segment-run kernel, when `spec` is given; the others decode
+// chunk by chunk.
 template <int kMode>
-int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny, Batch* run = nullptr) {
+int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny, Batch* run = nullptr,
+               Batch* spec = nullptr) {
     const std::string who = "tensor " + std::to_string(i) + ": ";
     if (t.chunk_size < 1) return fail(AIMG_ERR_INVALID_ARGUMENT, who + "chunk_size must be >= 1");
     if (t.n_chunks < 0 || t.n_symbols < 0 || t.packed_nbytes < 0)
@@ -2357,8 +2930,12 @@ int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny, Batch* r
     // chunk kernel's (kModeIndex) and is the one other user.
     const bool to_run = run != nullptr && has_index && t.chunk_size >= kRunMinChunk &&
                         t.packed_nbytes >= 4 && vec_layout;
+    // (The speculative runs keep byte offsets within a round below 2^32.)
+    const bool to_spec = !to_run && spec != nullptr && t.chunk_size >= kRunMinChunk &&
+                         t.packed_nbytes >= 4 && t.packed_nbytes < (int64_t{1} << 32) - (int64_t{1} << 20) &&
+                         vec_layout;
     const bool keep_index = has_index && (to_run || kMode == kModeIndex);
-    Batch& B = to_run ? *run : (t.packed_nbytes < 4 ? tiny : normal);
+    Batch& B = to_run ? *run : to_spec ? *spec : (t.packed_nbytes < 4 ? tiny : normal);
     if (!vec_layout) B.vec = false;
     DevTensor& dt = B.args.t[B.m++];
     dt.packed = t.packed;
@@ -2394,24 +2971,31 @@ int launch(const aimg_tensor* ts, int n, const GemvArgs& gemv, bool vec_ok, void
     if (n < 0 || n > AIMG_MAX_TENSORS)
         return fail(AIMG_ERR_INVALID_ARGUMENT,
                     "n_tensors must be in 0.." + std::to_string(AIMG_MAX_TENSORS));
-    Batch normal, tiny, run;
+    Batch normal, tiny, run, spec;
     normal.args.gemv = gemv;
     tiny.args.gemv = gemv;
     run.args.gemv = gemv;
+    spec.args.gemv = gemv;
     normal.vec = vec_ok;
     // Tensors with an index and chunks of at least kRunMinChunk symbols
-    // decode in segment runs; the others chunk by chunk, without an index.
-    // AIMG_SEGMENT_RUNS=0 decodes every tensor chunk by chunk (tests and
-    // benchmarks use it to check and time the path without the index).
+    // decode in segment runs; such tensors without an index in speculative
+    // segment runs; the others chunk by chunk. AIMG_SEGMENT_RUNS=0 ignores
+    // every index and AIMG_SPEC_RUNS=0 turns the speculative runs off (tests
+    // and benchmarks use them to check and time each path on the same inputs).
     const char* force = std::getenv("AIMG_SEGMENT_RUNS");
     const bool no_runs = force != nullptr && force[0] == '0';
+    const char* force_spec = std::getenv("AIMG_SPEC_RUNS");
+    const bool no_spec = force_spec != nullptr && force_spec[0] == '0';
     Batch* const to_run = vec_ok && !no_runs ? &run : nullptr;
+    Batch* const to_spec = vec_ok && !no_spec ? &spec : nullptr;
     for (int i = 0; i < n; ++i) {
-        const int rc = add_tensor<kMode>(ts[i], i, normal, tiny, to_run);
+        const int rc = add_tensor<kMode>(ts[i], i, normal, tiny, to_run, to_spec);
         if (rc != AIMG_OK) return rc;
     }
     const hipStream_t s = static_cast<hipStream_t>(stream);
     int rc = launch_run<kMode>(run, s);
+    if (rc != AIMG_OK) return rc;
+    rc = launch_spec<kMode>(spec, s);
     if (rc != AIMG_OK) return rc;
     rc = launch_batch<kMode>(normal, s, false);
     if (rc != AIMG_OK) return rc;

@@ -73,13 +73,16 @@ def _write(d, enc, expect, sm=None):
         f.write("%d %d %d %d\n" % (enc.max_bits, enc.chunk_size, enc.n_symbols, len(enc.chunk_offsets)))
 
 
-def _run(emu, name, mode, index="", runs=None, strided=None, cus=None, copies=None):
+def _run(emu, name, mode, index="", runs=None, strided=None, cus=None, copies=None, spec=None):
     exe, d = emu
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0")
     env.pop("AIMG_SEGMENT_RUNS", None)
     env.pop("AIMG_RUN_STRIDED", None)
     env.pop("AIMG_EMU_CUS", None)
     env.pop("AIMG_EMU_COPIES", None)
+    env.pop("AIMG_SPEC_RUNS", None)
+    if spec is not None:
+        env["AIMG_SPEC_RUNS"] = spec  # "0": tensors without an index decode chunk by chunk
     if cus is not None:
         env["AIMG_EMU_CUS"] = str(cus)  # a grid of 2 * cus workgroups
     if copies is not None:
@@ -93,21 +96,22 @@ def _run(emu, name, mode, index="", runs=None, strided=None, cus=None, copies=No
     assert r.returncode == 0 and ": ok" in r.stdout, (r.stdout + r.stderr)[-4000:]
 
 
-def _u8(emu, name, exps, chunk_size, index="", cus=None):
+def _u8(emu, name, exps, chunk_size, index="", cus=None, spec=None):
     exps = np.asarray(exps)
     enc = encode_chunked(torch.as_tensor(exps), chunk_size=chunk_size)
     _write(emu[1] / name, enc, exps.astype(np.uint8))
-    _run(emu, name, "u8", index, cus=cus)
+    _run(emu, name, "u8", index, cus=cus, spec=spec)
 
 
-def _bf16(emu, name, W, chunk_size, index="", runs=None, strided=None, cus=None, copies=None):
+def _bf16(emu, name, W, chunk_size, index="", runs=None, strided=None, cus=None, copies=None,
+          spec=None):
     layer = compress_layer(W, chunk_size=chunk_size)
     _write(emu[1] / name, layer.encoded, W.reshape(-1).view(torch.int16).numpy(),
            layer.sign_mantissa.numpy())
-    _run(emu, name, "bf16", index, runs, strided, cus, copies)
+    _run(emu, name, "bf16", index, runs, strided, cus, copies, spec)
 
 
-def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None, cus=None):
+def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None, cus=None, spec=None):
     W = workloads.bf16_normal((rows, cols), seed, 0.02, outlier_frac=1e-3)
     layer = compress_layer(W, chunk_size=chunk_size)
     g = np.random.default_rng(seed + 1)
@@ -119,7 +123,7 @@ def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None, c
     want.numpy().tofile(os.path.join(d, "expect_y.bin"))
     with open(os.path.join(d, "gemv.txt"), "w") as f:
         f.write("%d %d %d\n" % (rows, cols, batch))
-    _run(emu, name, "gemv", index, runs, cus=cus)
+    _run(emu, name, "gemv", index, runs, cus=cus, spec=spec)
 
 
 @pytest.mark.parametrize("batch", [1, 4])
@@ -317,3 +321,140 @@ def test_gemv_with_index_ignored_chunk_by_chunk(emu):
 def test_foreign_index_ignored_chunk_by_chunk(emu):
     W = workloads.bf16_normal((40, 5000), 6, 0.02, outlier_frac=1e-3)
     _bf16(emu, "ix_foreign_items", W, 4096, index="index-foreign", runs="0")
+
+
+# Speculative segment runs (no index): tensors whose chunks hold 1024 symbols
+# or more decode in rounds of 512 segments across chunk boundaries over a
+# contiguous chunk range per workgroup. Small CU counts give each workgroup
+# many rounds (and, on a full grid, workgroups b and b + grid/2 split a CU's
+# share), so rounds start inside chunks, carry codeword ranks and partial
+# vector groups, and switch table sets; "0" decodes the same inputs chunk by
+# chunk.
+
+@pytest.mark.parametrize("spec", ["1", "0"])
+def test_spec_runs_bf16_1024_chunks_many_rounds(emu, spec):
+    W = workloads.bf16_normal((96, 8192), 21, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "sp1024_%s" % spec, W, 1024, cus=2, spec=spec)
+
+
+def test_spec_runs_bf16_64k_chunks_across_chunk_boundaries(emu):
+    # 6 chunks of 65536 on a 2-CU grid: rounds of a workgroup cross from one
+    # large chunk into the next.
+    W = workloads.bf16_normal((24, 16384), 22, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "sp64k", W, 65536, cus=2)
+
+
+def test_spec_runs_several_tensors_in_one_launch(emu):
+    W = workloads.bf16_normal((48, 8192), 23, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "sp_multi", W, 2048, cus=2, copies=3)
+
+
+def test_spec_runs_u8_ragged_last_chunk(emu):
+    rng = np.random.default_rng(24)
+    _u8(emu, "sp_ragged", rng.integers(90, 135, 2048 * 150 + 700), 2048, cus=2)
+
+
+def test_spec_runs_u8_one_bit_codes(emu):
+    # Two symbols: 1-bit codes, 80-bit segments, 13 segments a 1024-symbol chunk.
+    rng = np.random.default_rng(25)
+    _u8(emu, "sp_onebit", rng.integers(0, 2, 1024 * 90 + 33), 1024, cus=2)
+
+
+def test_spec_runs_every_guess_wrong(emu):
+    # 3-bit fixed-length codes: every speculative start is wrong, the result
+    # rests on the re-decodes from the predecessors' ends.
+    rng = np.random.default_rng(26)
+    _u8(emu, "sp_guess1024", rng.integers(0, 8, 1024 * 40), 1024, cus=2)
+    _u8(emu, "sp_guess64k", rng.integers(0, 8, 65536 + 30000), 65536, cus=2)
+
+
+def test_spec_runs_escape_blocks_beyond_the_lds_share(emu):
+    _u8(emu, "sp_escapes", many_escape_windows(seed=27, n=60000), 4096, cus=2)
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_spec_runs_gemv(emu, batch):
+    _gemv(emu, "sp_gemv1024_b%d" % batch, 128, 2048, 1024, batch, 28, cus=2)
+    _gemv(emu, "sp_gemv32k_b%d" % batch, 70, 1000, 32768, batch, 29, cus=2)
+
+
+def test_spec_runs_sliced_stream(emu):
+    # Whole-chunk decode of chunks [3, 40) of a stream: the slice's own
+    # n_symbols, and 8 slack bytes past its last chunk.
+    from afterimage_amd.runtime.compressed_store import _slice_encoded
+    rng = np.random.default_rng(30)
+    exps = rng.integers(100, 130, 1024 * 48)
+    enc = encode_chunked(torch.as_tensor(exps), chunk_size=1024)
+    sub = _slice_encoded(enc, 3, 40)
+    _write(emu[1] / "sp_slice", sub, exps[3 * 1024: 40 * 1024].astype(np.uint8))
+    _run(emu, "sp_slice", "u8", cus=2)
+
+
+class _Enc:
+    """A ChunkedEncoded's fields, for encodings edited by hand."""
+
+    def __init__(self, enc, **kw):
+        for k in ("packed", "chunk_offsets", "chunk_nbytes", "sym_lut", "len_lut", "max_bits",
+                  "chunk_size", "n_symbols"):
+            setattr(self, k, kw.get(k, getattr(enc, k)))
+
+    @property
+    def n_chunks(self):
+        return len(self.chunk_offsets)
+
+
+def _malformed(emu, name, enc):
+    # On a 2-CU grid (workgroups of several chunks fall back to the exact
+    # path when one of their chunks is short) and one chunk per workgroup
+    # (the chunks that hold their output count decode speculatively).
+    import oracle
+    want = oracle.decode_chunks(enc)[: int(enc.n_symbols)]
+    _write(emu[1] / name, enc, want.astype(np.uint8))
+    _run(emu, name, "u8", cus=2)
+    _run(emu, name, "u8")
+    _run(emu, name, "u8", cus=2, spec="0")
+
+
+def test_spec_runs_truncated_chunks_take_the_exact_path(emu):
+    # Chunks cut short (the bounded reader reads zeros past their end): a
+    # chunk in the middle (the chunks are then not back to back) and the last
+    # chunk (its codewords run out before its output count).
+    rng = np.random.default_rng(31)
+    enc = encode_chunked(torch.as_tensor(rng.integers(100, 140, 1024 * 60)), chunk_size=1024)
+    nb = np.array(enc.chunk_nbytes, np.int32)
+    nb[17] -= 40
+    _malformed(emu, "sp_trunc_mid", _Enc(enc, chunk_nbytes=nb))
+    nb = np.array(enc.chunk_nbytes, np.int32)
+    nb[-1] -= 60
+    _malformed(emu, "sp_trunc_last", _Enc(enc, chunk_nbytes=nb))
+
+
+def test_spec_runs_last_codeword_cut_by_the_chunk_end(emu):
+    # Each chunk loses its last byte but the chunks stay back to back (the
+    # stream is re-packed): codewords that run past a chunk's end read zeros
+    # there, not the next chunk's bits (about half the chunks still hold
+    # their output count and decode speculatively, the last window cleared
+    # past the chunk end; without that 18 bytes differ).
+    rng = np.random.default_rng(32)
+    enc = encode_chunked(torch.as_tensor(rng.integers(100, 140, 1024 * 40)), chunk_size=1024)
+    packed = np.asarray(enc.packed, np.uint8)
+    offs = np.asarray(enc.chunk_offsets, np.int64)
+    nb = np.asarray(enc.chunk_nbytes, np.int64) - 1
+    parts = [packed[o: o + n] for o, n in zip(offs, nb)]
+    new_off = np.concatenate([[0], np.cumsum(nb)[:-1]]).astype(np.int32)
+    new_packed = np.concatenate(parts + [np.zeros(8, np.uint8)])
+    _malformed(emu, "sp_cut", _Enc(enc, packed=new_packed, chunk_offsets=new_off,
+                                   chunk_nbytes=nb.astype(np.int32)))
+
+
+def test_spec_runs_chunks_out_of_order_and_empty(emu):
+    rng = np.random.default_rng(33)
+    enc = encode_chunked(torch.as_tensor(rng.integers(100, 140, 1024 * 30)), chunk_size=1024)
+    offs = np.array(enc.chunk_offsets, np.int32)
+    nb = np.array(enc.chunk_nbytes, np.int32)
+    offs[[5, 6]] = offs[[6, 5]]
+    nb[[5, 6]] = nb[[6, 5]]
+    _malformed(emu, "sp_order", _Enc(enc, chunk_offsets=offs, chunk_nbytes=nb))
+    nb = np.array(enc.chunk_nbytes, np.int32)
+    nb[9] = 0
+    _malformed(emu, "sp_empty", _Enc(enc, chunk_nbytes=nb))
