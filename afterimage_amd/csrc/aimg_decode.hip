@@ -2038,13 +2038,16 @@ __device__ void run_piece(RunLds& lds, const Tables& tb, bool global_esc, const 
         const uint32_t cbase = lds.cbase[b][jj];
         const uint32_t coff = lds.coff[b][jj];
         const uint32_t crend = lds.crend[b][jj];
-        const uint32_t B0 = 8 * P.A0;
-        const uint32_t at = 8 * coff + (g - cbase) * S;  // bit of the packed buffer
-        const uint32_t cend = 8 * coff + crend;
-        const uint32_t lo = at - B0;
-        const uint32_t hi = (at + S < cend ? at + S : cend) - B0;
+        // Compared within the chunk (chunk bits), then moved to tile bits by
+        // the chunk's byte offset from the round's first byte: absolute bit
+        // numbers of the packed buffer would pass 2^32 in buffers of 512 MiB.
+        const uint32_t seg_lo = (g - cbase) * S;
+        const uint32_t seg_hi = seg_lo + S < crend ? seg_lo + S : crend;
+        const uint32_t rel = 8u * (coff - P.A0);  // tile bit of the chunk's bit 0 (mod 2^32)
+        const uint32_t lo = rel + seg_lo;
+        const uint32_t hi = rel + seg_hi;
         __builtin_amdgcn_s_setprio(0);
-        if (active && at < cend) {
+        if (active && seg_lo < crend) {
             uint8_t* dst = stage + lead + excl;
             if (global_esc) {
                 decode_placed<true>(below, tb, lo + (ent & 15u), hi, dst);
@@ -2287,6 +2290,7 @@ struct __attribute__((aligned(16))) SpecLds {
     // to its end, the stage byte after the round's symbols.
     uint32_t last[4];
     uint32_t bad;  // a chunk of the round does not hold its symbols
+    uint32_t dummy[64];  // a word per lane for compaction writes that have no place
     uint32_t tile[kRunTileWords];
     __attribute__((aligned(16))) uint8_t stage[kSpecStageBytes];
 };
@@ -2303,6 +2307,18 @@ __device__ __forceinline__ uint32_t wave_scan_max(uint32_t v) {
     x = umax(x, dpp<0x142, 0xA>(x));
     x = umax(x, dpp<0x143, 0xC>(x));
     return x;
+}
+
+// OR of v over the wave, in every lane (every lane active).
+__device__ __forceinline__ uint32_t wave_or(uint32_t v) {
+    uint32_t x = v;
+    x |= dpp<0x111>(x);
+    x |= dpp<0x112>(x);
+    x |= dpp<0x114>(x);
+    x |= dpp<0x118>(x);
+    x |= dpp<0x142, 0xA>(x);
+    x |= dpp<0x143, 0xC>(x);
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 63));
 }
 
 // One lookup's symbols into an interleaved slot (`lane` points at the lane's
@@ -2372,21 +2388,26 @@ __device__ __forceinline__ void spec_tab_issue(SpecTabFetch& F, const DevTensor&
     F.cn = __builtin_amdgcn_raw_buffer_load_b32(buffer_of(T.nbytes, lim), at, 0, 0);
 }
 
+// (All fields 32-bit: a copy of a struct with padding bytes became a copy
+// through scratch memory, whose loads wait for every vector memory access.)
 struct SpecTab {
     uint32_t n_tab;  // chunks of the table (those below the piece's end)
     int32_t end;     // segments of the table counted from the round's first
-    bool bad;        // chunks not back to back, empty, or too large
+    uint32_t bad;    // 1: chunks not back to back, empty, or too large
     uint32_t off0;   // byte offset of the table's first chunk
 };
 
 // The fetched chunks into table set `set` (written by one wave; every wave
 // computes the same result). k0: the round's first segment in chunk c0;
 // first_off: where chunk c0 must start (the previous table's view of it).
+// *jj: the table chunk of the calling thread's segment (thread 64 w + lane),
+// found in registers: the chunks that start before the wave's first segment,
+// and a mask of those that start inside the wave.
 __device__ __forceinline__ SpecTab spec_tab_commit(const SpecTabFetch& F, const DevTensor& T,
                                                    SpecLds& lds, uint32_t set, uint32_t c0,
                                                    uint32_t cb, uint32_t k0, uint32_t first_off,
                                                    bool check_first, uint32_t S, uint32_t lane,
-                                                   bool writer) {
+                                                   uint32_t w, uint32_t* jj) {
     consume(F.co);
     consume(F.cn);
     const uint32_t c = c0 + lane;
@@ -2411,8 +2432,18 @@ __device__ __forceinline__ SpecTab spec_tab_commit(const SpecTabFetch& F, const 
         static_cast<int>(offv + nbv), static_cast<int>(n_tab > 0 ? n_tab - 1 : 0)));
     const bool any_bad = __ballot(bad) != 0;
     const uint32_t off0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(offv), 0));
-    if (writer) {
-        lds.cseg[set][lane] = static_cast<int32_t>(incl - nseg) - static_cast<int32_t>(k0);
+    const int32_t first = static_cast<int32_t>(incl - nseg) - static_cast<int32_t>(k0);
+    const int32_t rel = first - static_cast<int32_t>(64 * w);
+    const uint32_t before = static_cast<uint32_t>(__builtin_popcountll(__ballot(valid && rel < 0)));
+    const bool inside = valid && rel >= 0 && rel < 64;
+    const uint64_t bit = inside ? uint64_t{1} << rel : 0u;
+    const uint64_t heads = static_cast<uint64_t>(wave_or(static_cast<uint32_t>(bit))) |
+                           static_cast<uint64_t>(wave_or(static_cast<uint32_t>(bit >> 32))) << 32;
+    const uint64_t upto = lane == 63 ? ~uint64_t{0} : (uint64_t{2} << lane) - 1;
+    const uint32_t cnt = before + static_cast<uint32_t>(__builtin_popcountll(heads & upto));
+    *jj = cnt > 0 ? cnt - 1 : 0u;
+    if (w == 0) {
+        lds.cseg[set][lane] = first;
         lds.coff[set][lane] = valid ? offv : end_off;
         lds.cbits[set][lane] = 8 * nbv;
         if (lane == 0) {
@@ -2420,7 +2451,8 @@ __device__ __forceinline__ SpecTab spec_tab_commit(const SpecTabFetch& F, const 
             lds.coff[set][kSpecChunks] = end_off;
         }
     }
-    return {n_tab, static_cast<int32_t>(total) - static_cast<int32_t>(k0), any_bad, uniform(off0)};
+    return {n_tab, static_cast<int32_t>(total) - static_cast<int32_t>(k0), any_bad ? 1u : 0u,
+            uniform(off0)};
 }
 
 __device__ __forceinline__ void spec_tile_issue(uint32_t (&raw)[kTileBatch], const DevTensor& T,
@@ -2451,17 +2483,6 @@ __device__ __forceinline__ void spec_tile_commit(const uint32_t (&raw)[kTileBatc
     }
 }
 
-// The chunk of the table set that holds segment g of the round: the last of
-// the n_tab chunks whose first segment is at or before g.
-__device__ __forceinline__ uint32_t spec_chunk_of(const SpecLds& lds, uint32_t set, uint32_t n_tab,
-                                                  uint32_t g) {
-    uint32_t j = 0;
-#pragma unroll
-    for (uint32_t step = kSpecChunks / 2; step >= 1; step >>= 1)
-        if (j + step < n_tab && lds.cseg[set][j + step] <= static_cast<int32_t>(g)) j += step;
-    return j;
-}
-
 // Chunks [ca, cb) of tensor T (all of them below n_jobs).
 template <int kMode, int kGroup>
 __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, const LaunchArgs& args,
@@ -2479,23 +2500,20 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
         load_table(table, tid, lds.wsyms, lds.wmeta, lds.len, lds.esc);
     }
     uint32_t b = 0;
-    SpecTab tab = spec_tab_commit(TF, T, lds, b, ca, cb, 0u, 0u, false, S, lane, w == 0);
+    uint32_t jj = 0;
+    SpecTab tab = spec_tab_commit(TF, T, lds, b, ca, cb, 0u, 0u, false, S, lane, w, &jj);
     uint32_t c0 = ca;     // chunk of the round's first segment
     uint32_t p0 = 0;      // chunk bit where its first codeword starts (k0 > 0)
     uint32_t rank0 = 0;   // codewords of chunk c0 before the round
     uint32_t lead = 0;    // carried symbols at the front of the stage
     int64_t a0 = static_cast<int64_t>(ca) * cs;  // element of stage byte 0
     uint32_t A0 = tab.off0;  // packed byte of the round's first segment
-    int64_t fall_from = tab.bad ? a0 : -1;  // the first element the exact fallback writes
+    int64_t fall_from = tab.bad != 0u ? a0 : -1;  // the first element the exact fallback writes
     uint32_t raw[kTileBatch];
     if (fall_from < 0) spec_tile_issue(raw, T, A0, tid);
     if (tid == 0) lds.bad = 0u;
     __syncthreads();  // table set 0 is written
-    uint32_t jj = 0;
-    if (fall_from < 0) {
-        spec_tile_commit(raw, T, A0, tid, lds.tile);
-        jj = spec_chunk_of(lds, b, tab.n_tab, tid);
-    }
+    if (fall_from < 0) spec_tile_commit(raw, T, A0, tid, lds.tile);
     __syncthreads();  // the first round's words are in the tile
 
     TileRef below = (TileRef)(lds.tile + kRunTileWords - 2);
@@ -2527,6 +2545,10 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
         SmBatch<kMode> smb;
         sm_issue<kMode, kGroup>(smb, T, a0, tid, kThreads, static_cast<uint32_t>(piece_end));
 
+        // Chunk c0's output count and the stage's first place in it.
+        const uint32_t lim0 = static_cast<uint32_t>(
+            T.n_symbols - static_cast<int64_t>(c0) * cs < cs ? T.n_symbols - static_cast<int64_t>(c0) * cs : cs);
+        const uint32_t base0 = rank0 < lim0 ? rank0 : lim0;
         // This thread's segment: segment kseg of chunk c0 + jj.
         const bool active = tid < ns;
         const int32_t kseg = static_cast<int32_t>(tid) - lds.cseg[b][jj];
@@ -2610,20 +2632,19 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
         const uint32_t xw = incl - cnt;
         const uint32_t rank = hm != 0u ? xw - (hm - 1u) : carry + xw;
         // Stage place: chunk jj's element r is stage byte
-        // lead + jj cs + r - min(rank0, lim of chunk c0).
-        const int64_t lim64 = T.n_symbols - static_cast<int64_t>(c0 + jj) * cs;
-        const uint32_t lim = static_cast<uint32_t>(lim64 < cs ? lim64 : cs);
-        const int64_t lim0_64 = T.n_symbols - static_cast<int64_t>(c0) * cs;
-        const uint32_t lim0 = static_cast<uint32_t>(lim0_64 < cs ? lim0_64 : cs);
-        const uint32_t base0 = rank0 < lim0 ? rank0 : lim0;
+        // lead + jj cs + r - min(rank0, lim of chunk c0). (32-bit: elements
+        // below 2^31, chunk_size below 2^24 and jj below 64.)
+        const uint32_t cs32 = static_cast<uint32_t>(cs);
+        const uint32_t n32 = static_cast<uint32_t>(T.n_symbols);
+        const uint32_t left = n32 - (c0 + jj) * cs32;
+        const uint32_t lim = left < cs32 ? left : cs32;
         const uint32_t kept = rank < lim ? (cnt < lim - rank ? cnt : lim - rank) : 0u;
-        const int64_t pos64 = static_cast<int64_t>(lead) + static_cast<int64_t>(jj) * cs +
-                              (rank < lim ? rank : lim) - base0;
+        const uint32_t pos = lead + jj * cs32 + (rank < lim ? rank : lim) - base0;
         const bool at_end = hi_c == cbits;  // the chunk's last segment
-        const bool broken = active && ((at_end && static_cast<uint64_t>(rank) + cnt < lim) || pos64 < 0 ||
-                                       pos64 + kept > kSpecDense);
+        const bool broken = active && ((at_end && rank + cnt < lim) || pos > kSpecDense ||
+                                       kept > kSpecDense - pos);
         if (broken) lds.bad = 1u;
-        const uint32_t dpos = broken ? 0u : static_cast<uint32_t>(pos64);
+        const uint32_t dpos = broken ? 0u : pos;
         if (active && tid == ns - 1) {
             lds.last[0] = e - rel;
             lds.last[1] = rank + cnt;
@@ -2646,9 +2667,10 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
             slot[(nbody + 1 < kSlotRows ? nbody + 1 : kSlotRows - 1) * 64], slot[nbody * 64], hb);
         // Every thread is past its decode: the next round's words and table.
         SpecTab tabn = tab;
+        uint32_t jjn = 0;
         if (more) {
             spec_tile_commit(raw, T, A0n, tid, lds.tile);
-            tabn = spec_tab_commit(TF, T, lds, b ^ 1u, c0n, cb, k0n, offn, true, S, lane, w == 0);
+            tabn = spec_tab_commit(TF, T, lds, b ^ 1u, c0n, cb, k0n, offn, true, S, lane, w, &jjn);
         }
         __syncthreads();  // B: slots read; the next table and words written
         const bool bad_round = lds.bad != 0u;
@@ -2662,15 +2684,21 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
             uint8_t* dst = stage + dpos;
             if (hb & 1u) dst[0] = static_cast<uint8_t>(rw[0]);
             if (hb >= 2) *reinterpret_cast<uint16_t*>(dst + hb - 2) = static_cast<uint16_t>(rw[0] >> (8 * (hb - 2)));
-            uint32_t* body = reinterpret_cast<uint32_t*>(dst + hb);
+            // Body words, branch-free: in descending order, each to its place
+            // clamped to the last word, so the words past the run land on the
+            // last word and its own value, written last, overwrites them (a
+            // thread's LDS writes are done in order); with no body words they
+            // go to a dummy word of the lane's own.
+            uint32_t* const body = nbody != 0 ? reinterpret_cast<uint32_t*>(dst + hb) : lds.dummy + lane;
+            const uint32_t lastw = nbody != 0 ? nbody - 1 : 0u;
 #pragma unroll
-            for (uint32_t j = 0; j + 1 < kSlotRows; ++j)
-                if (j < nbody) body[j] = __builtin_amdgcn_alignbyte(rw[j + 1], rw[j], hb);
+            for (int32_t j = static_cast<int32_t>(kSlotRows) - 2; j >= 0; --j)
+                body[static_cast<uint32_t>(j) < lastw ? static_cast<uint32_t>(j) : lastw] =
+                    __builtin_amdgcn_alignbyte(rw[j + 1], rw[j], hb);
             uint8_t* tl = dst + hb + 4 * nbody;
             if (ntail >= 2) *reinterpret_cast<uint16_t*>(tl) = static_cast<uint16_t>(tv);
             if (ntail & 1u) tl[ntail - 1] = static_cast<uint8_t>(tv >> (8 * (ntail - 1)));
         }
-        const uint32_t jjn = more ? spec_chunk_of(lds, b ^ 1u, tabn.n_tab, tid) : 0u;
         __syncthreads();  // C: the round's symbols are in place
         if (bad_round) {
             fall_from = a0;
@@ -2701,7 +2729,7 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
         a0 += static_cast<int64_t>(nfull) * kGroup;
         lead = rem;
         if (!more) break;
-        if (tabn.bad) {
+        if (tabn.bad != 0u) {
             fall_from = a0;
             break;
         }
@@ -2930,8 +2958,10 @@ int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny, Batch* r
     // chunk kernel's (kModeIndex) and is the one other user.
     const bool to_run = run != nullptr && has_index && t.chunk_size >= kRunMinChunk &&
                         t.packed_nbytes >= 4 && vec_layout;
-    // (The speculative runs keep byte offsets within a round below 2^32.)
+    // (The speculative runs keep byte offsets within a round below 2^32,
+    // and chunk sizes below 2^24 keep their stage arithmetic in 32 bits.)
     const bool to_spec = !to_run && spec != nullptr && t.chunk_size >= kRunMinChunk &&
+                         t.chunk_size <= (1 << 24) &&
                          t.packed_nbytes >= 4 && t.packed_nbytes < (int64_t{1} << 32) - (int64_t{1} << 20) &&
                          vec_layout;
     const bool keep_index = has_index && (to_run || kMode == kModeIndex);

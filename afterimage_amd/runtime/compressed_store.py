@@ -194,9 +194,13 @@ def decompress_layer_gpu(layer: CompressedLayer, device: str = "cuda",
     written in place slice by slice. With ``reuse_decode_tables`` the tables
     are prepared once for the whole call; otherwise once per slice (both go
     through the content-keyed table cache). Work is ordered on the current
-    stream of ``device``; nothing here synchronises. On a CPU device the
-    library's CPU decoder writes the output directly (no slices are needed to
-    bound memory there) and the call returns when it is done.
+    stream of ``device``. As in the reference, the call synchronises the
+    device before it returns unless ``reuse_decode_tables`` is set
+    (compressed_store.py:181-183 passes ``synchronize=tables is None`` to
+    decode_gpu_v2, gpu_decode_v2.py:115-116), so a caller timing it with a
+    host clock sees the decode. On a CPU device the library's CPU decoder
+    writes the output directly (no slices are needed to bound memory there)
+    and the call returns when it is done.
     """
     enc = layer.encoded
     n = enc.n_symbols
@@ -213,14 +217,16 @@ def decompress_layer_gpu(layer: CompressedLayer, device: str = "cuda",
     if n <= max_slice_elems:
         _decode_range_into(layer, 0, enc.n_chunks, out, n,
                            dev, tables if tables is not None else _tables_for(enc, dev))
-        return out.reshape(layer.shape)
-    chunks_per_slice = max(1, max_slice_elems // enc.chunk_size)
-    for c0 in range(0, enc.n_chunks, chunks_per_slice):
-        c1 = min(c0 + chunks_per_slice, enc.n_chunks)
-        s0 = c0 * enc.chunk_size
-        s1 = min(c1 * enc.chunk_size, n)
-        _decode_range_into(layer, c0, c1, out[s0:s1], s1 - s0, dev,
-                           tables if tables is not None else _tables_for(enc, dev))
+    else:
+        chunks_per_slice = max(1, max_slice_elems // enc.chunk_size)
+        for c0 in range(0, enc.n_chunks, chunks_per_slice):
+            c1 = min(c0 + chunks_per_slice, enc.n_chunks)
+            s0 = c0 * enc.chunk_size
+            s1 = min(c1 * enc.chunk_size, n)
+            _decode_range_into(layer, c0, c1, out[s0:s1], s1 - s0, dev,
+                               tables if tables is not None else _tables_for(enc, dev))
+    if not reuse_decode_tables:
+        torch.cuda.synchronize(dev)
     return out.reshape(layer.shape)
 
 
@@ -228,7 +234,9 @@ def decompress_rows_gpu(layer: CompressedLayer, row_start: int, row_end: int,
                         device: str = "cuda") -> torch.Tensor:
     """Rows [row_start, row_end) of a 2-D compressed tensor
     (compressed_store.py:254-303): the covering chunk range is decoded and
-    the exact element range returned as a (rows, cols) view."""
+    the exact element range returned as a (rows, cols) view. On the GPU the
+    call synchronises the device after the decode, as the reference's does
+    (its _decode_exponent runs decode_gpu_v2 with synchronize=True)."""
     if len(layer.shape) != 2:
         raise ValueError("decompress_rows_gpu needs a 2D tensor, got shape %r"
                          % (layer.shape,))
@@ -251,6 +259,7 @@ def decompress_rows_gpu(layer: CompressedLayer, row_start: int, row_end: int,
         _decode_cpu_into(layer, c0, c1, flat, avail)
     else:
         _decode_range_into(layer, c0, c1, flat, avail, dev, _tables_for(enc, dev))
+        torch.cuda.synchronize(dev)
     return flat[e0 - base:e1 - base].reshape(row_end - row_start, cols)
 
 
@@ -287,7 +296,7 @@ def decompress_matvec_gpu(layer: CompressedLayer, x: torch.Tensor,
 
 def decompress_linear_gpu(layer: CompressedLayer, x: torch.Tensor, slice_rows: int = 8192,
                           device: str | torch.device = "cuda",
-                          fused: bool | None = None) -> torch.Tensor:
+                          fused: bool = False) -> torch.Tensor:
     """x @ W.T for the layer's 2-D bf16 weight W [rows, cols], as the
     reference's chunked lm_head computes it (streaming_engine.py:2307-2332):
     x [..., cols] times W a block of slice_rows rows at a time, each block
@@ -296,16 +305,19 @@ def decompress_linear_gpu(layer: CompressedLayer, x: torch.Tensor, slice_rows: i
     dimension. x must be bf16, the weight's dtype (F.linear refuses mixed
     dtypes). Returns [..., rows] in bf16.
 
-    The blocked path gives the reference's own result: the same weights, bit
-    for bit, in the same F.linear calls. Its blocks reuse one staging buffer.
+    The blocked path (the default) gives the reference's own result: the
+    same weights, bit for bit, in the same F.linear calls. Its blocks reuse
+    one staging buffer. slice_rows <= 0 takes all rows as one block (the
+    reference installs no chunked head then).
 
-    fused: True multiplies inside the decode kernel (decompress_matvec_gpu;
-    fp32 sums, rounded once to bf16) without decoding any block to memory,
-    for at most 4 rows of x (speculative-verify widths and single tokens);
-    None (default) takes it whenever x has at most 4 rows, False never.
-    Neither path is bit-identical to one unblocked F.linear: the reference
-    marks its blocked head lossy for that reason (its
-    tests/test_chunked_lm_head_gpu.py:1-27)."""
+    fused=True multiplies inside the decode kernel (decompress_matvec_gpu;
+    fp32 sums added with atomics in no fixed order, rounded once to bf16)
+    without decoding any block to memory, for at most 4 rows of x
+    (speculative-verify widths and single tokens). It is neither bit-identical
+    to the blocked path nor reproducible from call to call; it is held to
+    rel 1e-2 / abs 1e-3 of the fp32 product. Neither path is bit-identical to
+    one unblocked F.linear: the reference marks its blocked head lossy for
+    that reason (its tests/test_chunked_lm_head_gpu.py:1-27)."""
     dev = _gpu_device(device)
     if len(layer.shape) != 2:
         raise ValueError("decompress_linear_gpu needs a 2-D layer, got shape %s" % (layer.shape,))
@@ -324,8 +336,6 @@ def decompress_linear_gpu(layer: CompressedLayer, x: torch.Tensor, slice_rows: i
         return x.new_zeros(lead + (0,))
     t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, dev,
                                   tables=_tables_for(layer.encoded, dev))
-    if fused is None:
-        fused = 1 <= tokens <= GEMV_MAX_BATCH
     if fused:
         xb = x.reshape(tokens, cols).contiguous()
         y = decode_gemv(t, xb, rows, cols).to(torch.bfloat16)

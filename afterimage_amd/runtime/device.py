@@ -65,6 +65,20 @@ class DecodeTables(tuple):
     def __len__(self) -> int:
         return 2
 
+    # A tuple built from () would compare and hash by that empty content:
+    # tables are equal when they hold the same codebook on the same device.
+    def __eq__(self, other) -> bool:
+        if not isinstance(other, DecodeTables):
+            return False
+        return (self.key, self.max_bits, str(self.blob.device)) == \
+            (other.key, other.max_bits, str(other.blob.device))
+
+    def __ne__(self, other) -> bool:
+        return not self.__eq__(other)
+
+    def __hash__(self) -> int:
+        return hash((self.key, self.max_bits, str(self.blob.device)))
+
     def __iter__(self):
         return iter(self._flat())
 
@@ -541,8 +555,9 @@ def decode_gemv(t: DeviceTensor, x: torch.Tensor, rows: int, cols: int,
 def row_blocks(rows: int, cols: int, chunk_size: int, n_chunks: int, slice_rows: int):
     """The blocks of a blocked x @ W.T: (r0, r1, c0, c1) for each block of
     slice_rows rows (the last one shorter), with [c0, c1) the chunks that
-    hold its elements [r0 * cols, r1 * cols)."""
-    step = max(1, int(slice_rows))
+    hold its elements [r0 * cols, r1 * cols). slice_rows <= 0: one block of
+    all rows (no row blocking, as the reference's lm_head_slice_rows = 0)."""
+    step = int(slice_rows) if int(slice_rows) > 0 else max(1, int(rows))
     out = []
     for r0 in range(0, rows, step):
         r1 = min(r0 + step, rows)

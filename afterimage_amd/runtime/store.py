@@ -303,13 +303,23 @@ class StoreReader:
                                shape=tuple(meta["shape"]))
 
     def raw(self, key: str, verify: bool = False) -> torch.Tensor:
-        """A raw tensor in its stored dtype (bf16 values come back from their
-        float32 copies exactly)."""
+        """A raw tensor in its stored dtype, read as the reference's engine
+        reads it (streaming_engine.py:1078-1105): an int16 blob of a bf16
+        tensor holds its bit patterns (force_raw_storage and row-gather
+        writes, streaming_engine.py:193, :237) and is reinterpreted; a float32
+        blob of a bf16 tensor (the small-tensor rule) is cast back, which is
+        exact. A row-gather tensor is never loaded whole."""
         meta = self.tensors[key]
         if meta.get("compressed"):
             raise ValueError("tensor %r is compressed" % key)
+        if meta.get("row_gather"):
+            raise RuntimeError("%s is stored row-gather-only and should never be loaded whole"
+                               % key)
         t = torch.from_numpy(self.read(meta["blobs"]["raw"], verify=verify))
-        dtype = getattr(torch, str(meta["dtype"]).replace("torch.", ""), None)
+        dt = str(meta.get("dtype", "bfloat16")).replace("torch.", "")
+        if t.dtype == torch.int16 and "bfloat16" in dt:
+            return t.view(torch.bfloat16)
+        dtype = getattr(torch, dt, None)
         return t.to(dtype) if isinstance(dtype, torch.dtype) else t
 
     def host_block(self, keys: list[str], pin: bool = True, verify: bool = False):

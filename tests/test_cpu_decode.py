@@ -174,6 +174,20 @@ def test_table_cache_hits_by_identity_then_by_content():
     assert t4.key != t1.key
 
 
+def test_decode_tables_compare_and_hash_by_codebook():
+    # DecodeTables unpacks like a 2-tuple but must not compare or hash as the
+    # empty tuple it is built from: different codebooks differ.
+    a = case("dirichlet_4")["encoded"]
+    b = case("dirichlet_5")["encoded"]
+    ta = devmod._TableCache().get(a.sym_lut, a.len_lut, a.max_bits, "cpu")
+    ta2 = devmod._TableCache().get(a.sym_lut.copy(), a.len_lut.copy(), a.max_bits, "cpu")
+    tb = devmod._TableCache().get(b.sym_lut, b.len_lut, b.max_bits, "cpu")
+    assert ta is not ta2 and ta == ta2 and hash(ta) == hash(ta2)
+    assert ta != tb and not (ta == tb)
+    assert len({ta, ta2, tb}) == 2
+    assert ta != () and () != ta
+
+
 def test_table_cache_is_bounded_by_bytes():
     cache = devmod._TableCache(capacity_bytes=3 * 29000)
     names = ["dirichlet_%d" % k for k in range(6)]

@@ -75,7 +75,7 @@ def test_fused_head_for_up_to_four_rows_of_x(tokens):
     W = workloads.bf16_normal((2000, 1536), 4 + tokens, 0.02, outlier_frac=1e-3)
     layer = compress_layer(W, chunk_size=1024)
     x = _x((1, tokens, 1536), tokens)
-    y = decompress_linear_gpu(layer, x)  # fused by default at <= 4 rows of x
+    y = decompress_linear_gpu(layer, x, fused=True)
     assert y.shape == (1, tokens, 2000) and y.dtype == torch.bfloat16
     ref = torch.matmul(x.float().reshape(tokens, 1536),
                        W.cuda().float().t().contiguous()).reshape(1, tokens, 2000)

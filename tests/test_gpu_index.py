@@ -293,3 +293,45 @@ def test_chunks_not_back_to_back_make_the_index_unusable():
     assert not t.index_usable
     out = decode_bf16([t])[0]
     assert torch.equal(out.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
+
+
+def test_packed_buffer_past_512_mib_with_and_without_the_index():
+    # 95 copies of a 1024x17408 layer's chunks (each chunk is its own
+    # stream, so the copies form a valid tensor): 1.69e9 weights, about 550 MB
+    # of packed bits, so bit positions in the packed buffer pass 2^32. The
+    # decoders keep positions within a chunk or a round; with absolute bit
+    # numbers in 32 bits, segments past the wrap would be dropped.
+    import types
+    W, layer = workloads.single_layer(seed=9, rows=1024, cols=17408, chunk_size=65536)
+    enc = layer.encoded
+    k = 95
+    nb = np.asarray(enc.chunk_nbytes, np.int64)
+    used = int(nb.sum())
+    offs = np.asarray(enc.chunk_offsets, np.int64)
+    packed = np.concatenate([np.tile(np.asarray(enc.packed, np.uint8)[:used], k),
+                             np.zeros(8, np.uint8)])
+    big = types.SimpleNamespace(
+        packed=packed,
+        chunk_offsets=np.concatenate([offs + j * used for j in range(k)]).astype(np.int32),
+        chunk_nbytes=np.tile(nb, k).astype(np.int32), sym_lut=enc.sym_lut, len_lut=enc.len_lut,
+        max_bits=enc.max_bits, chunk_size=enc.chunk_size, n_symbols=k * enc.n_symbols,
+        shape=(k * enc.n_symbols,))
+    assert 8 * used * k > 1 << 32 and big.n_symbols < 1 << 31
+    sm = np.tile(layer.sign_mantissa.reshape(-1).numpy(), k)
+    t = DeviceTensor.from_encoded(big, sm, DEV)
+    del packed, sm
+    want = W.reshape(-1).to(DEV).view(torch.int16)
+    n_small = enc.n_symbols
+
+    def check(out):
+        o = out.view(torch.int16)
+        for j in range(k):
+            assert torch.equal(o[j * n_small:(j + 1) * n_small], want), "copy %d" % j
+
+    out = decode_bf16([t])[0]
+    check(out)
+    t.build_index()
+    assert t.index is not None
+    out.zero_()
+    decode_bf16([t], [out])
+    check(out)

@@ -134,6 +134,27 @@ def test_decompress_rows_matches_full_decode():
     assert decompress_rows_gpu(layer, 5, 5, device="cuda").shape == (0, 64)
 
 
+def test_calls_return_after_the_decode_as_the_reference_does():
+    # The reference synchronises when tables are not reused
+    # (compressed_store.py:181-183, gpu_decode_v2.py:115-116): an engine that
+    # times decompress_layer_gpu with a host clock sees the whole decode. On a
+    # stream kept busy beforehand, the call's return means every launch on
+    # the stream is done; with reuse_decode_tables it need not be.
+    W, layer = workloads.single_layer(seed=5, rows=1024, cols=17408, chunk_size=65536)
+    dev = torch.device("cuda")
+    junk = torch.empty(64 << 20, dtype=torch.float32, device=dev)
+    for _ in range(20):
+        junk.mul_(1.0001)  # about 20 ms of queued work before the call
+    out = decompress_layer_gpu(layer, device="cuda")
+    assert torch.cuda.current_stream(dev).query(), "decompress_layer_gpu returned before its work"
+    rows = decompress_rows_gpu(layer, 10, 700, device="cuda")
+    assert torch.cuda.current_stream(dev).query(), "decompress_rows_gpu returned before its work"
+    again = decompress_layer_gpu(layer, device="cuda", reuse_decode_tables=True)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(out.view(torch.int16), W.to(dev).view(torch.int16))
+    assert torch.equal(again, out) and torch.equal(rows, out[10:700])
+
+
 def test_unaligned_output_view_uses_elementwise_stores():
     torch.manual_seed(5)
     W = (torch.randn(64, 96) * 0.02).to(torch.bfloat16)

@@ -26,6 +26,14 @@ def test_row_blocks_cover_the_rows_and_their_chunks(rows, cols, chunk, step):
     assert row_blocks(0, cols, chunk, 0, step) == []
 
 
+@pytest.mark.parametrize("step", [0, -5])
+def test_row_blocks_without_slicing_are_one_block(step):
+    # lm_head_slice_rows = 0 means no chunked head: the whole tensor at once,
+    # not 1-row blocks.
+    assert row_blocks(151936, 5120, 1024, 759680, step) == [(0, 151936, 0, 759680)]
+    assert row_blocks(7, 3, 4, 6, step) == [(0, 7, 0, 6)]
+
+
 def _cpu_tensor(layer):
     enc = layer.encoded
     return DeviceTensor(packed=torch.from_numpy(enc.packed.copy()),

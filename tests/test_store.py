@@ -274,3 +274,29 @@ def test_direct_reader_reads_what_the_buffered_one_does(tmp_path):
                 size = an * (4 if f.startswith("chunk") else 1)
                 assert (a0, an) == (b0, bn) and np.array_equal(ba[a0:a0 + size], bb[b0:b0 + size])
         assert torch.equal(_bits(decompress_layer_gpu(b, device="cpu")), _bits(W))
+
+
+def test_raw_bf16_bit_patterns_written_as_int16_read_back_as_bf16(tmp_path):
+    # The reference writes force_raw_storage bf16 tensors and row-gather
+    # embeddings as int16 bit patterns with dtype "bfloat16"
+    # (streaming_engine.py:193, :237, :372-374) and reads them back by
+    # reinterpreting the bytes (streaming_engine.py:1084-1095); a numeric
+    # cast would turn the pattern 16256 (bf16 1.0) into 16256.0.
+    W = torch.tensor([[1.0, -2.5, 3.0e-3], [0.0, 65280.0, -1.0e-30]], dtype=torch.bfloat16)
+    bits = W.view(torch.int16).numpy()
+    with StoreWriter(tmp_path) as sw:
+        sw._entry("forced", {"orig_bytes": W.numel() * 2, "comp_bytes": W.numel() * 2,
+                             "shape": list(W.shape), "compressed": False,
+                             "dtype": "torch.bfloat16"}, {"raw": bits})
+        sw._entry("embed", {"orig_bytes": W.numel() * 2, "comp_bytes": W.numel() * 2,
+                            "shape": list(W.shape), "compressed": False, "row_gather": True,
+                            "hidden_size": 3, "dtype": "bfloat16"}, {"raw": bits})
+        sw.add_tensor("norm", torch.tensor([1.0, 0.5], dtype=torch.bfloat16))
+    with StoreReader(tmp_path) as rd:
+        got = rd.raw("forced", verify=True)
+        assert got.dtype == torch.bfloat16 and torch.equal(got.view(torch.int16), W.view(torch.int16))
+        assert float(got[0, 0]) == 1.0
+        with pytest.raises(RuntimeError, match="row-gather-only"):
+            rd.raw("embed")
+        norm = rd.raw("norm")  # float32 copy cast back
+        assert norm.dtype == torch.bfloat16 and norm.tolist() == [1.0, 0.5]
