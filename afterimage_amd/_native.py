@@ -73,6 +73,9 @@ _SIGNATURES = [
     ("aimg_decode_gemv_bf16", ctypes.c_int,
      [ctypes.POINTER(AimgTensor), ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
       ctypes.c_void_p, ctypes.c_void_p]),
+    ("aimg_decode_gemm_bf16", ctypes.c_int,
+     [ctypes.POINTER(AimgTensor), ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+      ctypes.c_void_p, ctypes.c_void_p]),
     ("aimg_recombine_bf16", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]),
     ("aimg_cpu_decode_bf16", ctypes.c_int, [ctypes.POINTER(AimgTensor), ctypes.c_int, ctypes.c_int]),

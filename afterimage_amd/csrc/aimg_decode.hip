@@ -67,6 +67,7 @@ constexpr uint32_t kOverlapBits = 32;
 // segments.
 constexpr uint32_t kSlotCap = kSegCodewords;
 constexpr uint32_t kSlotWords = kSlotCap / 4;  // compaction reads these and one more
+constexpr uint32_t kSlotRows = kSlotWords + 1;  // a slot's words: kSlotCap symbols and the word after
 constexpr uint32_t kSlotBytes = 92;
 static_assert(kSlotCap % 4 == 0 && kSlotBytes >= kSlotCap + 4, "slot room for the word after the cap");
 static_assert(kSlotBytes % 4 == 0 && (kSlotBytes / 4) % 2 == 1, "slot stride: an odd number of words");
@@ -84,6 +85,9 @@ constexpr uint32_t kTileBatch = kMaxSegBits / 32 + 1;
 // kSlotCap symbols per thread, plus a carried partial group.
 constexpr uint32_t kStoreBatch = (kSlotCap * kMinTpc + 15 + 8 * kMinTpc - 1) / (8 * kMinTpc);
 static_assert(kStoreBatch * 8 * kMinTpc >= kSlotCap * kMinTpc + 15, "one store batch covers a round");
+// Interleaved slots of a whole-workgroup chunk (word j of lane l of wave w at
+// row j, column l of the wave's block), then a dummy word per lane.
+constexpr uint32_t kWholeSlotBytes = kWaves * kSlotRows * 64 * 4;
 constexpr uint32_t kStagePadded =
     (kStageBytes + 16 > kStoreBatch * kThreads * 8 ? kStageBytes + 16 : kStoreBatch * kThreads * 8);
 // Of those, the groups whose sign/mantissa bytes are requested while the round
@@ -125,19 +129,22 @@ enum Mode : int {
     kModeGemv = 2,  // y += W x with W decoded on the fly and never written
     kModeGemv1 = 3, // kModeGemv for one x vector (batch 1)
     kModeIndex = 4, // the segment index: each segment's first boundary and codewords
+    kModeGemm = 5,  // Y += X W^T for up to 16 rows of X, W decoded on the fly (MFMA)
 };
 // Modes that combine the exponents with sign/mantissa bytes.
 constexpr bool needs_sm(int mode) { return mode != kModeU8 && mode != kModeIndex; }
 // Job::ib of a chunk decoded without the index.
 constexpr uint32_t kNoIndex = 0xFFFFFFFFu;
 constexpr int kGemvMaxBatch = 4;
+// Rows of x (tokens) of the fused decode -> GEMM: one MFMA tile's 16.
+constexpr int kGemmMaxRows = 16;
 // Steps ahead of use that x is requested with up to kGemvMaxBatch x vectors
 // (with one, 3). Measured on the 5120x17408 layer at batch 4: 2 steps
 // ahead 7% slower than 1, 3 steps 39% slower.
 constexpr uint32_t kGemvXAhead = 1;
 
 struct GemvArgs {
-    const uint16_t* x;  // bf16 [batch][cols]
+    const uint16_t* x;  // bf16 [batch][cols] (GEMM: [rows of x][cols])
     float* y;           // fp32 [batch][rows], accumulated
     uint32_t rows;
     uint32_t cols;
@@ -490,6 +497,61 @@ __device__ __forceinline__ void decode_placed(TileRef below, const Tables& tb, u
         lds_or(reinterpret_cast<uint32_t*>((q - (reinterpret_cast<uintptr_t>(q) & 3u)) + 4), spill);
 }
 
+// One lookup's symbols into an interleaved slot (`lane` points at the lane's
+// word 0; word j is lane[64 j]) at byte q, as slot_put does it.
+__device__ __forceinline__ void slot_put_il(uint32_t* lane, uint32_t q, uint32_t syms) {
+    const uint32_t b = q & 3u;
+    const uint64_t v = static_cast<uint64_t>(syms) << (8 * b);
+    uint32_t* w = lane + (q >> 2) * 64;
+    lds_or(w, static_cast<uint32_t>(v));
+    w[64] = static_cast<uint32_t>(v >> 32);
+}
+
+// decode_run into an interleaved slot. cend: the bit where the segment's
+// chunk ends, when the tile holds the next chunk's bits after it (speculative
+// runs; the chunk kernel's tile is zero past its chunk and passes
+// 0xFFFFFFFF). The bounded reader reads zeros there, and only the last window
+// can meet them (every earlier codeword ends before x <= cend), so that
+// window is looked up again with the bits from cend on cleared when it
+// reaches past cend.
+template <bool kGlobalEsc>
+__device__ __forceinline__ Adv decode_run_il(TileRef below, const Tables& tb, uint32_t p,
+                                             uint32_t x, uint32_t cend, uint32_t* lane) {
+    lane[0] = 0u;
+    if (p >= x) return {p, 0u};
+    uint32_t q = 0;
+    const Reader rd = reader_at(below, p);
+    Step s = lookup<true>(below, tb, rd.p, rd.sh, rd.pair);
+    uint32_t syms, adv, c;
+    take<kGlobalEsc>(tb, s, &syms, &adv, &c);
+    uint32_t pn = s.p + adv;
+    while (pn < x) {
+        Step t = lookup<false>(below, tb, pn, pn - s.m, s.next);
+        slot_put_il(lane, q, syms);
+        q += c;
+        t.syms = tb.syms[t.idx];
+        s = t;
+        take<kGlobalEsc>(tb, s, &syms, &adv, &c);
+        pn = s.p + adv;
+    }
+    if (cend - s.p < 16u) {
+        const uint32_t w = s.w & ~(0xFFFFFFFFu >> (cend - s.p));
+        const uint32_t idx = w >> (32 - kWinBits);
+        const uint32_t meta = tb.meta[idx];
+        syms = tb.syms[idx];
+        adv = meta & 31u;
+        c = meta >> 5;
+        if (adv == 0) {
+            syms = escape<kGlobalEsc>(tb, syms, w, &adv);
+            c = 1;
+        }
+    }
+    uint32_t kept;  // 1..4
+    const uint32_t e = cut_window(tb, s.p, s.p + adv, syms, c, x, &kept);
+    slot_put_il(lane, q, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
+    return {e, q + kept};
+}
+
 // Where to load the 4 bytes from packed-buffer byte A (A below the buffer
 // size): A itself, or the last whole word of the buffer (`last` = size - 4)
 // when A is within 3 bytes of its end; the word is then shifted right by
@@ -784,7 +846,7 @@ __device__ __forceinline__ void store_one(const DevTensor& T, const GemvArgs& G,
         static_cast<uint8_t*>(T.out)[el] = static_cast<uint8_t>(e);
     } else if (kMode == kModeBf16) {
         static_cast<uint16_t*>(T.out)[el] = bf16_one(T.sm[el], e);
-    } else if (kMode == kModeGemv || kMode == kModeGemv1) {
+    } else if (kMode == kModeGemv || kMode == kModeGemv1 || kMode == kModeGemm) {
         const float w = bf16_to_f32(bf16_one(T.sm[el], e));
         const uint32_t row = static_cast<uint32_t>(el / G.cols);
         const uint32_t col = static_cast<uint32_t>(el - static_cast<int64_t>(row) * G.cols);
@@ -1018,6 +1080,164 @@ __device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch],
     if (acc_row != 0xFFFFFFFFu) gemv_flush_lanes<kB>(G, nb, acc, acc_row);
 }
 
+// ---------------------------------------------------------------------------
+// Fused decode -> GEMM (kModeGemm, whole-workgroup rounds): Y[t][r] +=
+// sum_c X[t][c] W[r][c] for t < G.batch <= 16, on v_mfma_f32_16x16x32_bf16.
+// One MFMA takes a 16 x 32 tile of X (A: lane l holds X[l & 15][8 (l >> 4)
+// .. + 7]) and the 32 x 16 tile of W^T over the same 32 columns and 16 rows
+// of W (B: lane l holds W[row l & 15][the same 8 columns]) and adds to a 16 x
+// 16 tile of Y^T (D: lane l holds Y[4 (l >> 4) + k][row l & 15], k < 4).
+// A round's weights are in natural order, a row of W at a time, while the
+// B operand wants 16 rows at the same columns: each piece of 4 store steps
+// (2048 groups) is written to LDS as bf16 (with one padding group per row,
+// so that the 16 rows a read meets fall in different banks), and the waves
+// take the 32-column slices of each 16-row tile of W the piece touches,
+// X from global memory (L2) each time. Every wave keeps its partial D of the
+// current 16-row tile (rows 16 tile ..) in registers across pieces and
+// rounds; when the tile changes, the waves' partials are summed in LDS and
+// added to Y with one atomic per (row, x row).
+// ---------------------------------------------------------------------------
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kGemmPieceSteps = 4;                        // store steps a piece holds
+constexpr uint32_t kGemmPieceGroups = kGemmPieceSteps * kThreads;
+// Padding groups of a piece: one per row it touches, for rows of 64 groups
+// or more (a row of fewer takes none: the reads then meet bank conflicts).
+constexpr uint32_t kGemmPadMinGroups = 64;
+constexpr uint32_t kGemmPieceBytes = 16 * (kGemmPieceGroups + kGemmPieceGroups / kGemmPadMinGroups + 2);
+// The cross-wave sum of the partial tiles, after the piece in the stage.
+constexpr uint32_t kGemmRedOffset = (kGemmPieceBytes + 255) / 256 * 256;
+constexpr uint32_t kGemmRedBytes = kWaves * 64 * 16;
+constexpr uint32_t kNoTile = 0xFFFFFFFFu;
+constexpr uint32_t kGemmUnroll = 4;  // slices whose loads go out together
+
+struct GemmAcc {
+    f32x4_t d;      // this wave's partial sums of 16-row tile `tile`
+    uint32_t tile;  // kNoTile: none
+};
+
+__device__ __forceinline__ void gemm_acc_init(GemmAcc& A) {
+    A.d = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    A.tile = kNoTile;
+}
+
+// The waves' partial sums of the current tile to Y; every thread calls it
+// (it holds barriers). `stage`: at least kGemmRedOffset + kGemmRedBytes bytes
+// that no thread reads meanwhile.
+__device__ __forceinline__ void gemm_flush(GemmAcc& A, const GemvArgs& G, uint8_t* stage) {
+    if (A.tile == kNoTile) return;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u, w = tid >> 6;
+    f32x4_t* const red = reinterpret_cast<f32x4_t*>(stage + kGemmRedOffset);
+    red[w * 64 + lane] = A.d;
+    __syncthreads();
+    if (tid < 256) {
+        // Entry k of lane l2 of every wave: Y[4 (l2 >> 4) + k][16 tile + (l2 & 15)].
+        const uint32_t l2 = tid >> 2, k = tid & 3u;
+        const float* const f = reinterpret_cast<const float*>(red) + tid;
+        float sum = 0.0f;
+#pragma unroll
+        for (uint32_t v = 0; v < static_cast<uint32_t>(kWaves); ++v) sum += f[v * 256];
+        const uint32_t t = 4 * (l2 >> 4) + k;
+        const uint32_t row = 16 * A.tile + (l2 & 15u);
+        // Rows no weight of this workgroup met sum to exactly zero.
+        if (t < static_cast<uint32_t>(G.batch) && row < G.rows && sum != 0.0f)
+            atomicAdd(G.y + static_cast<int64_t>(t) * G.rows + row, sum);
+    }
+    __syncthreads();  // the sums are read before the area is written again
+    gemm_acc_init(A);
+}
+
+// One round's groups [0, nfull) (W groups a0 / 8 ...), their sign/mantissa
+// bytes in sm (group k * kThreads + tid at k), exponents in the stage. The
+// stage is overwritten but for the bytes past the round's groups, which the
+// caller carries into the next round: those are put back.
+__device__ __forceinline__ void gemm_round(const uint2 (&sm)[kStoreBatch], const GemvArgs& G,
+                                           uint8_t* stage, uint32_t a0, uint32_t nfull, uint32_t tid,
+                                           GemmAcc& A) {
+    const uint32_t cols = G.cols;
+    const uint32_t cg = cols / 8;  // groups a row
+    const uint32_t lane = tid & 63u, w = tid >> 6;
+    const uint32_t nb = static_cast<uint32_t>(G.batch);
+    uint2 ev[kStoreBatch];
+#pragma unroll
+    for (uint32_t k = 0; k < kStoreBatch; ++k)
+        ev[k] = *reinterpret_cast<const uint2*>(stage + (k * kThreads + tid) * 8);
+    const uint2 keep0 = reinterpret_cast<const uint2*>(stage + nfull * 8)[0];
+    const uint2 keep1 = reinterpret_cast<const uint2*>(stage + nfull * 8)[1];
+    __syncthreads();  // every exponent is read before the first piece is written
+    const uint32_t pad = cg >= kGemmPadMinGroups ? 1u : 0u;
+    const uint32_t g0 = a0 / 8;
+    const uint32_t ns = (cg + 3) / 4;  // 32-column slices a row
+    const __amdgpu_buffer_rsrc_t xr = buffer_of(G.x, nb * cols * 2u);
+    const uint32_t q = lane >> 4, n = lane & 15u;
+#pragma unroll
+    for (uint32_t p = 0; p < (kStoreBatch + kGemmPieceSteps - 1) / kGemmPieceSteps; ++p) {
+        const uint32_t vb = p * kGemmPieceGroups;
+        if (vb >= nfull) break;
+        const uint32_t ve = nfull - vb < kGemmPieceGroups ? nfull : vb + kGemmPieceGroups;
+        const uint32_t rb = (g0 + vb) / cg;      // the piece's first row
+        const uint32_t re = (g0 + ve - 1) / cg;  // and last
+        // The piece's weights to LDS, bf16, group v at v - vb plus the rows
+        // before its own.
+#pragma unroll
+        for (uint32_t kk = 0; kk < kGemmPieceSteps; ++kk) {
+            const uint32_t k = p * kGemmPieceSteps + kk;
+            if (k >= kStoreBatch) break;
+            const uint32_t v = k * kThreads + tid;
+            if (v < ve) {
+                uint4 wv;
+                wv.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, ev[k].x);
+                wv.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, ev[k].x);
+                wv.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, ev[k].y);
+                wv.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, ev[k].y);
+                const uint32_t row = (g0 + v) / cg;
+                *reinterpret_cast<uint4*>(stage + 16 * (v - vb + pad * (row - rb))) = wv;
+            }
+        }
+        __syncthreads();
+        for (uint32_t t = rb / 16; t <= re / 16; ++t) {
+            if (t != A.tile) {
+                gemm_flush(A, G, stage);
+                A.tile = t;
+            }
+            const uint32_t row = 16 * t + n;
+            // Slices s = w, w + kWaves, ... of this tile, kGemmUnroll at a time.
+            for (uint32_t s0 = w; s0 < ns; s0 += kGemmUnroll * kWaves) {
+                uint4 xa[kGemmUnroll], wb[kGemmUnroll];
+#pragma unroll
+                for (uint32_t u = 0; u < kGemmUnroll; ++u) {
+                    const uint32_t sl = s0 + u * kWaves;
+                    const uint32_t j = 4 * sl + q;  // the lane's column group
+                    const bool col_ok = sl < ns && j < cg;
+                    // X row n (zero past the batch: out of the buffer's range).
+                    const uint32_t xo = col_ok && n < nb ? n * cols * 2u + 16u * j : 0xFFFFFFF0u;
+                    const auto xv = __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0);
+                    xa[u] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+                    const uint32_t gv = row * cg + j;  // W group of this lane (rows * cols < 2^31)
+                    const bool ok = col_ok && gv >= g0 + vb && gv < g0 + ve;
+                    const uint32_t lo = ok ? 16u * (gv - g0 - vb + pad * (row - rb)) : 0u;
+                    const uint4 bv = *reinterpret_cast<const uint4*>(stage + lo);
+                    wb[u] = ok ? bv : make_uint4(0u, 0u, 0u, 0u);
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < kGemmUnroll; ++u)
+                    A.d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[u]),
+                                                                  __builtin_bit_cast(bf16x8_t, wb[u]),
+                                                                  A.d, 0, 0, 0);
+            }
+        }
+        __syncthreads();  // the piece is read before the next one (or the carry) is written
+    }
+    if (tid == 0) {
+        reinterpret_cast<uint2*>(stage + nfull * 8)[0] = keep0;
+        reinterpret_cast<uint2*>(stage + nfull * 8)[1] = keep1;
+    }
+    __syncthreads();
+}
+
 // Vector groups [0, nfull) of the staged round to output elements a0...;
 // thread i of a sub-group of tpc takes groups i, i + tpc, ... kWhole: the
 // sub-group is the whole workgroup, whose stage area is readable for every
@@ -1029,7 +1249,7 @@ template <int kMode, int kGroup, bool kWhole>
 __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTensor& T,
                                             const GemvArgs& G, const uint8_t* stage, int64_t a0,
                                             uint32_t nfull, uint32_t i, uint32_t tpc,
-                                            uint32_t skip = 0) {
+                                            uint32_t skip = 0, GemmAcc* gacc = nullptr) {
     if (kGroup == 1) {
         for (uint32_t v = i; v < nfull; v += tpc) store_one<kMode>(T, G, a0 + v, stage[v]);
         return;
@@ -1072,6 +1292,13 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
     } else {
 #pragma unroll
         for (uint32_t k = kSmAhead; k < kStoreBatch; ++k) sm[k] = make_uint2(0u, 0u);
+    }
+    if constexpr (kMode == kModeGemm) {
+        // Whole-workgroup rounds without skipped elements only (the
+        // speculative runs).
+        static_assert(kWhole && kGroup == 8, "the fused GEMM takes whole-workgroup rounds");
+        gemm_round(sm, G, const_cast<uint8_t*>(stage), static_cast<uint32_t>(a0), nfull, i, *gacc);
+        return;
     }
     // All staged exponents are read (from always valid offsets) before any
     // is combined, so the LDS reads overlap.
@@ -1244,6 +1471,12 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     uint32_t* const s_gpre = lds.gpre;
     uint32_t* const s_wbad = lds.wbad;
     uint32_t* const s_gval = lds.gval;
+    // Whole-workgroup chunks (the index build aside) take the fast path; its
+    // record of each wave's lane 0 (start, whether it is checked) reuses the
+    // sub-group prefix table, which that path does not need.
+    constexpr bool kWhole = kLg == kLgThreads && kMode != kModeIndex;
+    uint32_t* const s_f0 = lds.gpre;
+    uint32_t* const s_chk0 = lds.gpre + kWaves;
 
     const uint32_t tid = threadIdx.x;
     const uint8_t* loaded = nullptr;
@@ -1331,6 +1564,124 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             const bool active = seg_lo < RB;
             const uint32_t seg_hi = active ? (seg_lo + S < RB ? seg_lo + S : RB) : 0u;
             uint32_t f = 0, e = 0, cnt = 0;
+            // What the compaction hands to the store.
+            int64_t a0;
+            uint32_t want, avail, nfull, e_last;
+            if constexpr (kWhole) {
+                // A whole-workgroup chunk: slots interleaved by lane (no bank
+                // conflicts), one record barrier for the agreement check and
+                // the scan, and branch-free compaction writes.
+                const uint32_t lane = tid & 63u;
+                const uint32_t w = uniform(tid >> 6);
+                uint32_t* const slot_il =
+                    reinterpret_cast<uint32_t*>(stage + kLeadBytes) + w * kSlotRows * 64 + lane;
+                __builtin_amdgcn_s_setprio(0);
+                if (active) {
+                    Adv a;
+                    if (global_esc) {
+                        f = i == 0 ? p0 : advance<true>(below, tb, seg_lo - kOverlapBits, seg_lo);
+                        a = decode_run_il<true>(below, tb, f, seg_hi, 0xFFFFFFFFu, slot_il);
+                    } else {
+                        f = i == 0 ? p0 : advance<false>(below, tb, seg_lo - kOverlapBits, seg_lo);
+                        a = decode_run_il<false>(below, tb, f, seg_hi, 0xFFFFFFFFu, slot_il);
+                    }
+                    e = a.p;
+                    cnt = a.n;
+                }
+                __builtin_amdgcn_s_setprio(1);
+                // Each wave checks its lanes against the lane below and scans
+                // its counts; its last lane leaves the wave's count, end and
+                // disagreement, lane 0 its start, and after one barrier every
+                // wave checks the waves' first lanes and finds its prefix.
+                uint32_t incl;
+                const bool checked = active && i > 0;
+                for (;;) {
+                    const uint32_t ep0 = lane_below(e);
+                    incl = wave_scan_incl(cnt);
+                    const bool wbad = __ballot(checked && lane != 0 && f != ep0) != 0;
+                    if (lane == 63) {
+                        s_wsum[w] = incl;
+                        s_ewave[w] = e;
+                        s_wbad[w] = wbad ? 1u : 0u;
+                    }
+                    if (lane == 0) {
+                        s_f0[w] = f;
+                        s_chk0[w] = checked ? 1u : 0u;
+                    }
+                    __syncthreads();
+                    const uint32_t lw = lane & (kWaves - 1);
+                    const bool xbad = lw > 0 && s_chk0[lw] != 0u && s_f0[lw] != s_ewave[lw - 1];
+                    if (__ballot(lane < kWaves && (s_wbad[lw] != 0u || xbad)) == 0) break;
+                    // Rare: threads whose start disagrees with their
+                    // predecessor's end decode again from it (thread 0 is
+                    // always right, so pass k puts thread k right at the latest).
+                    const uint32_t ep = lane == 0 ? (w > 0 ? s_ewave[w - 1] : 0u) : ep0;
+                    const bool redo = checked && f != ep;
+                    __syncthreads();  // the records are read before they are written again
+                    if (redo) {
+                        f = ep;
+                        const Adv a = global_esc
+                                          ? decode_run_il<true>(below, tb, f, seg_hi, 0xFFFFFFFFu, slot_il)
+                                          : decode_run_il<false>(below, tb, f, seg_hi, 0xFFFFFFFFu, slot_il);
+                        e = a.p;
+                        cnt = a.n;
+                    }
+                }
+                uint32_t pre = 0, gtot = 0;
+#pragma unroll
+                for (uint32_t k = 0; k < kWaves; ++k) {
+                    const uint32_t v = s_wsum[k];
+                    pre += k < w ? v : 0u;
+                    gtot += v;
+                }
+                const uint32_t o = pre + incl - cnt;
+                const int64_t still = lim - ob;
+                want = g_active ? (gtot < still ? gtot : static_cast<uint32_t>(still)) : 0u;
+                avail = lead + want;
+                nfull = avail / kGroup;
+                a0 = chunk_base + ob - lead;
+                const uint32_t n_active = g_active ? (RB + S - 1) / S : 1u;
+                if (i == n_active - 1) s_glast[0] = e;
+                __builtin_amdgcn_s_setprio(2);
+                // Compaction: the slot into registers (the dense area overlaps
+                // the slots), a barrier, then the symbols to their place.
+                const uint32_t m = want > o ? (cnt < want - o ? cnt : want - o) : 0u;
+                const uint32_t dpos = lead + o;
+                const uint32_t head0 = (4u - (dpos & 3u)) & 3u;
+                const uint32_t hb = head0 < m ? head0 : m;
+                const uint32_t nbody = (m - hb) >> 2;
+                const uint32_t ntail = m - hb - 4 * nbody;
+                uint32_t rw[kSlotRows];
+                {
+                    const auto* sl = lds_ptr(slot_il);
+#pragma unroll
+                    for (uint32_t j = 0; j < kSlotRows; ++j) rw[j] = sl[j * 64];
+                }
+                const uint32_t tv = __builtin_amdgcn_alignbyte(
+                    slot_il[(nbody + 1 < kSlotRows ? nbody + 1 : kSlotRows - 1) * 64], slot_il[nbody * 64], hb);
+                __syncthreads();
+                e_last = s_glast[0];
+                uint8_t* dst = stage + dpos;
+                if (hb & 1u) dst[0] = static_cast<uint8_t>(rw[0]);
+                if (hb >= 2) *reinterpret_cast<uint16_t*>(dst + hb - 2) = static_cast<uint16_t>(rw[0] >> (8 * (hb - 2)));
+                // Body words in descending order to places clamped to the last
+                // one (its own value, written last, overwrites the others; a
+                // thread's LDS writes are done in order); none: a dummy word
+                // past the slots.
+                uint32_t* const body = nbody != 0 ? reinterpret_cast<uint32_t*>(dst + hb)
+                                                  : reinterpret_cast<uint32_t*>(stage + kLeadBytes + kWholeSlotBytes) + lane;
+                const uint32_t lastw = nbody != 0 ? nbody - 1 : 0u;
+#pragma unroll
+                for (int32_t j = static_cast<int32_t>(kSlotRows) - 2; j >= 0; --j)
+                    body[static_cast<uint32_t>(j) < lastw ? static_cast<uint32_t>(j) : lastw] =
+                        __builtin_amdgcn_alignbyte(rw[j + 1], rw[j], hb);
+                uint8_t* tl = dst + hb + 4 * nbody;
+                if (ntail >= 2) *reinterpret_cast<uint16_t*>(tl) = static_cast<uint16_t>(tv);
+                if (ntail & 1u) tl[ntail - 1] = static_cast<uint8_t>(tv >> (8 * (ntail - 1)));
+                // Every thread is past its decode, so the tile takes the next words.
+                fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
+                __syncthreads();
+            } else {
             __builtin_amdgcn_s_setprio(0);
             if (active) {
                 start_slot(slot);
@@ -1396,14 +1747,14 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             if (i == 0) s_gpre[g] = excl;
             if (tid == kThreads - 1) s_gpre[n_groups] = excl + cnt;
             __syncthreads();
-            const uint32_t e_last = s_glast[g];
+            e_last = s_glast[g];
             const uint32_t o = excl - s_gpre[g];
             const uint32_t gtot = s_gpre[g + 1] - s_gpre[g];
             const int64_t still = lim - ob;
-            const uint32_t want = g_active ? (gtot < still ? gtot : static_cast<uint32_t>(still)) : 0u;
-            const uint32_t avail = lead + want;
-            const uint32_t nfull = avail / kGroup;
-            const int64_t a0 = chunk_base + ob - lead;
+            want = g_active ? (gtot < still ? gtot : static_cast<uint32_t>(still)) : 0u;
+            avail = lead + want;
+            nfull = avail / kGroup;
+            a0 = chunk_base + ob - lead;
 
             __builtin_amdgcn_s_setprio(2);
             // Compaction. The dense area overlaps the slots, so every slot is
@@ -1442,6 +1793,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             // Every thread is past its decode, so the tile takes the next words.
             fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
             __syncthreads();
+            }
 
             store_round<kMode, kGroup, kLg == kLgThreads>(smb, T, args.gemv, stage, a0, nfull, i, tpc);
             ob += want;
@@ -2257,7 +2609,6 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void run_kernel(const Laun
 // ---------------------------------------------------------------------------
 
 constexpr uint32_t kSpecChunks = 64;            // chunks a round's table holds
-constexpr uint32_t kSlotRows = kSlotWords + 1;  // a slot's words: kSlotCap symbols and the word after
 constexpr uint32_t kSpecSlotBytes = kWaves * kSlotRows * 64 * 4;
 constexpr uint32_t kSpecStageBytes = kLeadBytes + kSpecSlotBytes;
 // Dense stage limit: a carried partial group and kSlotCap symbols a segment.
@@ -2265,8 +2616,12 @@ constexpr uint32_t kSpecDense = kLeadBytes + kThreads * kSlotCap;
 static_assert(kSpecStageBytes >= kSpecDense + 4, "a dense round fits the stage");
 static_assert(kSpecStageBytes >= kStoreBatch * kThreads * 8, "store batches read inside the stage");
 static_assert(kSpecStageBytes >= kStoreBatch * kThreads * 16 / 2, "u8 store batches too");
-// Chunks larger than this go to decode_kernel (their bit counts must fit 32 bits).
-constexpr int64_t kSpecMaxChunkBytes = int64_t{1} << 28;
+static_assert(kSpecStageBytes >= kGemmRedOffset + kGemmRedBytes, "a GEMM piece and its sums fit the stage");
+static_assert(kSpecStageBytes >= kSpecDense + 16, "the GEMM round keeps the carried bytes");
+// A chunk of this many bytes or more makes its table unusable (the exact
+// fallback decodes it): segment counts come from a multiply-high that is
+// exact below it, and its bit count fits 32 bits.
+constexpr int64_t kSpecMaxChunkBytes = int64_t{1} << 26;
 
 struct __attribute__((aligned(16))) SpecLds {
     uint8_t wmeta[kWinEntries];
@@ -2321,59 +2676,6 @@ __device__ __forceinline__ uint32_t wave_or(uint32_t v) {
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 63));
 }
 
-// One lookup's symbols into an interleaved slot (`lane` points at the lane's
-// word 0; word j is lane[64 j]) at byte q, as slot_put does it.
-__device__ __forceinline__ void slot_put_il(uint32_t* lane, uint32_t q, uint32_t syms) {
-    const uint32_t b = q & 3u;
-    const uint64_t v = static_cast<uint64_t>(syms) << (8 * b);
-    uint32_t* w = lane + (q >> 2) * 64;
-    lds_or(w, static_cast<uint32_t>(v));
-    w[64] = static_cast<uint32_t>(v >> 32);
-}
-
-// decode_run into an interleaved slot. cend: the bit where the segment's
-// chunk ends. The tile holds the next chunk's bits after it; the bounded
-// reader reads zeros there, and only the last window can meet them (every
-// earlier codeword ends before x <= cend), so that window is looked up again
-// with the bits from cend on cleared when it reaches past cend.
-template <bool kGlobalEsc>
-__device__ __forceinline__ Adv decode_run_il(TileRef below, const Tables& tb, uint32_t p,
-                                             uint32_t x, uint32_t cend, uint32_t* lane) {
-    lane[0] = 0u;
-    if (p >= x) return {p, 0u};
-    uint32_t q = 0;
-    const Reader rd = reader_at(below, p);
-    Step s = lookup<true>(below, tb, rd.p, rd.sh, rd.pair);
-    uint32_t syms, adv, c;
-    take<kGlobalEsc>(tb, s, &syms, &adv, &c);
-    uint32_t pn = s.p + adv;
-    while (pn < x) {
-        Step t = lookup<false>(below, tb, pn, pn - s.m, s.next);
-        slot_put_il(lane, q, syms);
-        q += c;
-        t.syms = tb.syms[t.idx];
-        s = t;
-        take<kGlobalEsc>(tb, s, &syms, &adv, &c);
-        pn = s.p + adv;
-    }
-    if (cend - s.p < 16u) {
-        const uint32_t w = s.w & ~(0xFFFFFFFFu >> (cend - s.p));
-        const uint32_t idx = w >> (32 - kWinBits);
-        const uint32_t meta = tb.meta[idx];
-        syms = tb.syms[idx];
-        adv = meta & 31u;
-        c = meta >> 5;
-        if (adv == 0) {
-            syms = escape<kGlobalEsc>(tb, syms, w, &adv);
-            c = 1;
-        }
-    }
-    uint32_t kept;  // 1..4
-    const uint32_t e = cut_window(tb, s.p, s.p + adv, syms, c, x, &kept);
-    slot_put_il(lane, q, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
-    return {e, q + kept};
-}
-
 // One chunk per lane (chunk c0 + lane) of a round's table, in flight.
 struct SpecTabFetch {
     uint32_t co, cn;
@@ -2392,10 +2694,21 @@ __device__ __forceinline__ void spec_tab_issue(SpecTabFetch& F, const DevTensor&
 // through scratch memory, whose loads wait for every vector memory access.)
 struct SpecTab {
     uint32_t n_tab;  // chunks of the table (those below the piece's end)
-    int32_t end;     // segments of the table counted from the round's first
+    uint32_t ns;     // segments of the round (at most 512: those of the table's chunks)
     uint32_t bad;    // 1: chunks not back to back, empty, or too large
     uint32_t off0;   // byte offset of the table's first chunk
+    // The next round: its first segment is segment ns of this one, in table
+    // chunk `done` (n_tab: the chunk after the table), at segment k0n of it,
+    // whose bytes start at offn.
+    uint32_t done, k0n, offn;
 };
+
+// ceil(a / d) for a < kSpecMaxChunkBytes and d <= 21 (segment bytes), with
+// m = ceil(2^32 / d): a multiply-high is exact there (a (m d - 2^32) < 2^32).
+__device__ __forceinline__ uint32_t div_ceil_seg(uint32_t a, uint32_t d, uint32_t m) {
+    const uint32_t q = __umulhi(a, m);
+    return q + (q * d < a ? 1u : 0u);
+}
 
 // The fetched chunks into table set `set` (written by one wave; every wave
 // computes the same result). k0: the round's first segment in chunk c0;
@@ -2406,8 +2719,8 @@ struct SpecTab {
 __device__ __forceinline__ SpecTab spec_tab_commit(const SpecTabFetch& F, const DevTensor& T,
                                                    SpecLds& lds, uint32_t set, uint32_t c0,
                                                    uint32_t cb, uint32_t k0, uint32_t first_off,
-                                                   bool check_first, uint32_t S, uint32_t lane,
-                                                   uint32_t w, uint32_t* jj) {
+                                                   bool check_first, uint32_t S, uint32_t smagic,
+                                                   uint32_t lane, uint32_t w, uint32_t* jj) {
     consume(F.co);
     consume(F.cn);
     const uint32_t c = c0 + lane;
@@ -2418,7 +2731,7 @@ __device__ __forceinline__ SpecTab spec_tab_commit(const SpecTabFetch& F, const 
     const bool huge = nb >= kSpecMaxChunkBytes;
     const uint32_t nbv = valid && !huge ? static_cast<uint32_t>(nb) : 0u;
     const uint32_t offv = static_cast<uint32_t>(off);
-    const uint32_t nseg = (8 * nbv + S - 1) / S;
+    const uint32_t nseg = div_ceil_seg(nbv, S / 8, smagic);
     const int64_t lim = T.n_symbols - static_cast<int64_t>(c) * T.chunk_size;
     const uint32_t incl = wave_scan_incl(nseg);
     const uint32_t prev_end = lane_below(offv + nbv);
@@ -2433,6 +2746,16 @@ __device__ __forceinline__ SpecTab spec_tab_commit(const SpecTabFetch& F, const 
     const bool any_bad = __ballot(bad) != 0;
     const uint32_t off0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(offv), 0));
     const int32_t first = static_cast<int32_t>(incl - nseg) - static_cast<int32_t>(k0);
+    const int32_t end = static_cast<int32_t>(total) - static_cast<int32_t>(k0);
+    const uint32_t ns = end <= 0 ? 0u : (end < static_cast<int32_t>(kThreads) ? static_cast<uint32_t>(end) : kThreads);
+    const uint32_t done = static_cast<uint32_t>(__builtin_popcountll(
+        __ballot(valid && static_cast<int32_t>(incl) - static_cast<int32_t>(k0) <= static_cast<int32_t>(ns))));
+    const uint32_t k0n = done < n_tab ? ns - static_cast<uint32_t>(__builtin_amdgcn_readlane(
+                                                 static_cast<int>(first), static_cast<int>(done)))
+                                      : 0u;
+    const uint32_t offn = done < n_tab ? static_cast<uint32_t>(__builtin_amdgcn_readlane(
+                                             static_cast<int>(offv), static_cast<int>(done)))
+                                       : end_off;
     const int32_t rel = first - static_cast<int32_t>(64 * w);
     const uint32_t before = static_cast<uint32_t>(__builtin_popcountll(__ballot(valid && rel < 0)));
     const bool inside = valid && rel >= 0 && rel < 64;
@@ -2451,8 +2774,8 @@ __device__ __forceinline__ SpecTab spec_tab_commit(const SpecTabFetch& F, const 
             lds.coff[set][kSpecChunks] = end_off;
         }
     }
-    return {n_tab, static_cast<int32_t>(total) - static_cast<int32_t>(k0), any_bad ? 1u : 0u,
-            uniform(off0)};
+    return {n_tab, uniform(ns), any_bad || ns == 0 ? 1u : 0u, uniform(off0), uniform(done),
+            uniform(k0n), uniform(offn)};
 }
 
 __device__ __forceinline__ void spec_tile_issue(uint32_t (&raw)[kTileBatch], const DevTensor& T,
@@ -2488,8 +2811,9 @@ template <int kMode, int kGroup>
 __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, const LaunchArgs& args,
                            const DevTensor& T, uint32_t ca, uint32_t cb, const uint8_t* table) {
     const uint32_t tid = threadIdx.x;
-    const uint32_t lane = tid & 63u, w = tid >> 6;
+    const uint32_t lane = tid & 63u, w = uniform(tid >> 6);
     const uint32_t S = segment_bits(tb.min_len);
+    const uint32_t smagic = static_cast<uint32_t>(((uint64_t{1} << 32) + S / 8 - 1) / (S / 8));
     const int64_t cs = T.chunk_size;
     // The piece's first table and words; the decode table (when it changes)
     // loads while they arrive.
@@ -2501,9 +2825,11 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
     }
     uint32_t b = 0;
     uint32_t jj = 0;
-    SpecTab tab = spec_tab_commit(TF, T, lds, b, ca, cb, 0u, 0u, false, S, lane, w, &jj);
+    SpecTab tab = spec_tab_commit(TF, T, lds, b, ca, cb, 0u, 0u, false, S, smagic, lane, w, &jj);
     uint32_t c0 = ca;     // chunk of the round's first segment
     uint32_t p0 = 0;      // chunk bit where its first codeword starts (k0 > 0)
+    GemmAcc gacc;         // fused GEMM: this wave's partial sums
+    gemm_acc_init(gacc);
     uint32_t rank0 = 0;   // codewords of chunk c0 before the round
     uint32_t lead = 0;    // carried symbols at the front of the stage
     int64_t a0 = static_cast<int64_t>(ca) * cs;  // element of stage byte 0
@@ -2523,19 +2849,12 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
     const int64_t piece_end = static_cast<int64_t>(cb) * cs < T.n_symbols ? static_cast<int64_t>(cb) * cs
                                                                          : T.n_symbols;
     while (fall_from < 0) {
-        const int32_t tab_end = tab.end;
-        const uint32_t ns = uniform(static_cast<uint32_t>(tab_end < static_cast<int32_t>(kThreads) ? tab_end
-                                                                                     : kThreads));
-        // The next round: its first segment is segment ns of this one.
-        const int32_t nx = lds.cseg[b][lane + 1];
-        const uint32_t done = static_cast<uint32_t>(
-            __builtin_popcountll(__ballot(lane < tab.n_tab && nx <= static_cast<int32_t>(ns))));
-        const uint32_t c0n = c0 + done;
+        const uint32_t ns = tab.ns;
+        // The next round (found when this round's table was committed).
+        const uint32_t c0n = c0 + tab.done;
         const bool more = c0n < cb;
-        const uint32_t k0n = done < tab.n_tab ? uniform(static_cast<uint32_t>(
-                                                    static_cast<int32_t>(ns) - lds.cseg[b][done]))
-                                              : 0u;
-        const uint32_t offn = uniform(lds.coff[b][done]);
+        const uint32_t k0n = tab.k0n;
+        const uint32_t offn = tab.offn;
         const uint32_t A0n = offn + k0n * (S / 8);
         __builtin_amdgcn_s_setprio(3);
         if (more) {
@@ -2670,7 +2989,8 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
         uint32_t jjn = 0;
         if (more) {
             spec_tile_commit(raw, T, A0n, tid, lds.tile);
-            tabn = spec_tab_commit(TF, T, lds, b ^ 1u, c0n, cb, k0n, offn, true, S, lane, w, &jjn);
+            tabn = spec_tab_commit(TF, T, lds, b ^ 1u, c0n, cb, k0n, offn, true, S, smagic, lane, w,
+                                   &jjn);
         }
         __syncthreads();  // B: slots read; the next table and words written
         const bool bad_round = lds.bad != 0u;
@@ -2710,7 +3030,7 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
         const uint32_t nfull = room < static_cast<int64_t>(nfull0) ? static_cast<uint32_t>(room > 0 ? room : 0)
                                                                   : nfull0;
         __builtin_amdgcn_s_setprio(2);
-        store_round<kMode, kGroup, true>(smb, T, args.gemv, stage, a0, nfull, tid, kThreads);
+        store_round<kMode, kGroup, true>(smb, T, args.gemv, stage, a0, nfull, tid, kThreads, 0, &gacc);
         // The partial vector group moves to the front.
         const uint32_t rem0 = avail - nfull * kGroup;
         const uint32_t rem = rem0 < static_cast<uint32_t>(kGroup) ? rem0 : kGroup - 1u;
@@ -2751,6 +3071,7 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
         // codeword (exact on any input).
         run_fallback<kMode>(tb, args, T, fall_from / cs, cb, fall_from);
     }
+    if constexpr (kMode == kModeGemm) gemm_flush(gacc, args.gemv, stage);
     __syncthreads();  // LDS is free for the next piece
 }
 
@@ -2927,9 +3248,11 @@ int launch_spec(Batch& B, hipStream_t s) {
 // is given; tensors without one that meet the same conditions go to `spec`,
 // the speculative segment-run kernel, when `spec` is given; the others decode
 // chunk by chunk.
+constexpr uint32_t kSpecMaxTpc = 128;
+
 template <int kMode>
 int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny, Batch* run = nullptr,
-               Batch* spec = nullptr) {
+               Batch* spec = nullptr, bool spec_all = false) {
     const std::string who = "tensor " + std::to_string(i) + ": ";
     if (t.chunk_size < 1) return fail(AIMG_ERR_INVALID_ARGUMENT, who + "chunk_size must be >= 1");
     if (t.n_chunks < 0 || t.n_symbols < 0 || t.packed_nbytes < 0)
@@ -2960,8 +3283,14 @@ int add_tensor(const aimg_tensor& t, int i, Batch& normal, Batch& tiny, Batch* r
                         t.packed_nbytes >= 4 && vec_layout;
     // (The speculative runs keep byte offsets within a round below 2^32,
     // and chunk sizes below 2^24 keep their stage arithmetic in 32 bits.)
+    // Unless forced, only chunks of 128 threads or fewer: a chunk of a whole
+    // workgroup (or half of one) decodes faster chunk by chunk, where no
+    // round crosses a chunk boundary (5120x17408 bf16 weights on MI355X,
+    // speculative runs against chunk by chunk: 64Ki-, 32Ki- and 16Ki-symbol
+    // chunks 6%, 13% and 5% slower; 8Ki and 4Ki 3% and 11% faster).
+    const bool spec_size = spec_all || threads_per_chunk(t.chunk_size) <= kSpecMaxTpc;
     const bool to_spec = !to_run && spec != nullptr && t.chunk_size >= kRunMinChunk &&
-                         t.chunk_size <= (1 << 24) &&
+                         t.chunk_size <= (1 << 24) && spec_size &&
                          t.packed_nbytes >= 4 && t.packed_nbytes < (int64_t{1} << 32) - (int64_t{1} << 20) &&
                          vec_layout;
     const bool keep_index = has_index && (to_run || kMode == kModeIndex);
@@ -3009,20 +3338,37 @@ int launch(const aimg_tensor* ts, int n, const GemvArgs& gemv, bool vec_ok, void
     normal.vec = vec_ok;
     // Tensors with an index and chunks of at least kRunMinChunk symbols
     // decode in segment runs; such tensors without an index in speculative
-    // segment runs; the others chunk by chunk. AIMG_SEGMENT_RUNS=0 ignores
-    // every index and AIMG_SPEC_RUNS=0 turns the speculative runs off (tests
-    // and benchmarks use them to check and time each path on the same inputs).
+    // segment runs when their chunks are small enough; the others chunk by
+    // chunk. AIMG_SEGMENT_RUNS=0 ignores every index, AIMG_SPEC_RUNS=0 turns
+    // the speculative runs off and AIMG_SPEC_RUNS=1 takes them for every
+    // chunk size they support (tests and benchmarks use these to check and
+    // time each path on the same inputs).
     const char* force = std::getenv("AIMG_SEGMENT_RUNS");
     const bool no_runs = force != nullptr && force[0] == '0';
     const char* force_spec = std::getenv("AIMG_SPEC_RUNS");
     const bool no_spec = force_spec != nullptr && force_spec[0] == '0';
+    const bool spec_all = force_spec != nullptr && force_spec[0] == '1';
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if constexpr (kMode == kModeGemm) {
+        // The fused GEMM runs in speculative segment runs only, whatever the
+        // chunk size (an index is not used).
+        for (int i = 0; i < n; ++i) {
+            const int rc = add_tensor<kMode>(ts[i], i, normal, tiny, nullptr, vec_ok ? &spec : nullptr, true);
+            if (rc != AIMG_OK) return rc;
+        }
+        if (normal.m != 0 || tiny.m != 0)
+            return fail(AIMG_ERR_UNSUPPORTED,
+                        "fused GEMM: needs chunk_size a multiple of 8 and >= " + std::to_string(kRunMinChunk) +
+                            ", at most 2^24, 8-byte aligned sign_mantissa, 4 or more packed bytes and below "
+                            "4 GiB - 1 MiB");
+        return launch_spec<kMode>(spec, s);
+    } else {
     Batch* const to_run = vec_ok && !no_runs ? &run : nullptr;
     Batch* const to_spec = vec_ok && !no_spec ? &spec : nullptr;
     for (int i = 0; i < n; ++i) {
-        const int rc = add_tensor<kMode>(ts[i], i, normal, tiny, to_run, to_spec);
+        const int rc = add_tensor<kMode>(ts[i], i, normal, tiny, to_run, to_spec, spec_all);
         if (rc != AIMG_OK) return rc;
     }
-    const hipStream_t s = static_cast<hipStream_t>(stream);
     int rc = launch_run<kMode>(run, s);
     if (rc != AIMG_OK) return rc;
     rc = launch_spec<kMode>(spec, s);
@@ -3030,6 +3376,7 @@ int launch(const aimg_tensor* ts, int n, const GemvArgs& gemv, bool vec_ok, void
     rc = launch_batch<kMode>(normal, s, false);
     if (rc != AIMG_OK) return rc;
     return launch_batch<kMode>(tiny, s, true);
+    }
 }
 
 // Recombine of already-decoded exponents: out[i] = bf16 bits of (sm[i], e[i]).
@@ -3196,4 +3543,23 @@ extern "C" int aimg_decode_gemv_bf16(const aimg_tensor* t, int64_t rows, int64_t
     const bool vec_ok = cols % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
     if (batch == 1) return aimg::launch<aimg::kModeGemv1>(t, 1, g, vec_ok, stream);
     return aimg::launch<aimg::kModeGemv>(t, 1, g, vec_ok, stream);
+}
+
+extern "C" int aimg_decode_gemm_bf16(const aimg_tensor* t, int64_t rows, int64_t cols,
+                                     const void* x, int n_x, float* y, void* stream) {
+    using aimg::fail;
+    if (t == nullptr) return fail(AIMG_ERR_INVALID_ARGUMENT, "tensor is null");
+    if (rows < 1 || cols < 1 || rows > INT32_MAX || cols > INT32_MAX ||
+        rows * cols != t->n_symbols)
+        return fail(AIMG_ERR_INVALID_ARGUMENT, "rows * cols must equal n_symbols (both >= 1)");
+    if (n_x < 1 || n_x > aimg::kGemmMaxRows)
+        return fail(AIMG_ERR_INVALID_ARGUMENT, "n_x must be in 1.." + std::to_string(aimg::kGemmMaxRows));
+    if (x == nullptr || y == nullptr) return fail(AIMG_ERR_INVALID_ARGUMENT, "null x or y");
+    if (cols % 8 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 ||
+        static_cast<int64_t>(n_x) * cols * 2 > int64_t{0xFFFFFFFF})
+        return fail(AIMG_ERR_UNSUPPORTED,
+                    "fused GEMM: needs cols % 8 == 0, a 16-byte aligned x and n_x * cols * 2 below 2^32");
+    const aimg::GemvArgs g{static_cast<const uint16_t*>(x), y, static_cast<uint32_t>(rows),
+                           static_cast<uint32_t>(cols), n_x, 0u, 0u};
+    return aimg::launch<aimg::kModeGemm>(t, 1, g, true, stream);
 }

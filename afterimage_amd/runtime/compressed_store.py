@@ -17,8 +17,8 @@ import dataclasses
 import numpy as np
 import torch
 
-from .device import (GEMV_MAX_BATCH, DeviceTensor, cpu_decode, decode_bf16, decode_gemv,
-                     decode_linear, recombine_bf16)
+from .device import (GEMM_MAX_ROWS, GEMV_MAX_BATCH, DeviceTensor, cpu_decode, decode_bf16,
+                     decode_gemm, decode_gemv, decode_linear, recombine_bf16)
 from .huffman_chunked import ChunkedEncoded, encode_chunked, lengths_from_counts, symbol_counts
 
 EXPONENT_SHIFT = 7
@@ -276,8 +276,10 @@ def decompress_matvec_gpu(layer: CompressedLayer, x: torch.Tensor,
                           device: str | torch.device = "cuda") -> torch.Tensor:
     """x @ W.T for the layer's 2-D bf16 weight W [rows, cols] without
     materialising W: the exponents are decoded and multiplied in one kernel
-    (fp32 accumulation, bf16 result). x: [cols] or [b, cols] with b <= 4
+    (fp32 accumulation, bf16 result). x: [cols] or [b, cols] with b <= 16
     (a speculative-verify width), any float dtype; it is rounded to bf16.
+    Up to 4 rows take the fused GEMV, 5 to 16 the fused GEMM on the matrix
+    cores (which needs cols % 8 == 0 and chunks of at least 1024 symbols).
     Returns [b, rows] (or [rows] for a 1-D x) in bf16. The reference forms
     the same product as decompress_rows_gpu (compressed_store.py:254-303)
     followed by a matmul (streaming_engine.py:2271-2335)."""
@@ -290,7 +292,8 @@ def decompress_matvec_gpu(layer: CompressedLayer, x: torch.Tensor,
     xb = xb.to(device=dev, dtype=torch.bfloat16).contiguous()
     t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, dev,
                                   tables=_tables_for(layer.encoded, dev))
-    y = decode_gemv(t, xb, rows, cols).to(torch.bfloat16)
+    fn = decode_gemv if int(xb.shape[0]) <= GEMV_MAX_BATCH else decode_gemm
+    y = fn(t, xb, rows, cols).to(torch.bfloat16)
     return y.reshape(rows) if squeeze else y
 
 
@@ -312,12 +315,18 @@ def decompress_linear_gpu(layer: CompressedLayer, x: torch.Tensor, slice_rows: i
 
     fused=True multiplies inside the decode kernel (decompress_matvec_gpu;
     fp32 sums added with atomics in no fixed order, rounded once to bf16)
-    without decoding any block to memory, for at most 4 rows of x
-    (speculative-verify widths and single tokens). It is neither bit-identical
-    to the blocked path nor reproducible from call to call; it is held to
-    rel 1e-2 / abs 1e-3 of the fp32 product. Neither path is bit-identical to
-    one unblocked F.linear: the reference marks its blocked head lossy for
-    that reason (its tests/test_chunked_lm_head_gpu.py:1-27)."""
+    without decoding any block to memory, for at most 16 rows of x (single
+    tokens and the speculative-verify widths: up to 4 rows on the fused GEMV,
+    5 to 16 on the fused GEMM, which needs cols % 8 == 0 and chunks of at
+    least 1024 symbols). It is neither bit-identical to the blocked path nor
+    reproducible from call to call; it is held to rel 1e-2 / abs 1e-3 of the
+    fp32 product. Neither path is bit-identical to one unblocked F.linear:
+    the reference marks its blocked head lossy for that reason (its
+    tests/test_chunked_lm_head_gpu.py:1-27).
+
+    The layer's arrays may be host arrays (copied to the GPU on each call,
+    as the reference reads them for each token) or tensors already on the
+    GPU (used in place)."""
     dev = _gpu_device(device)
     if len(layer.shape) != 2:
         raise ValueError("decompress_linear_gpu needs a 2-D layer, got shape %s" % (layer.shape,))
@@ -328,9 +337,9 @@ def decompress_linear_gpu(layer: CompressedLayer, x: torch.Tensor, slice_rows: i
         raise ValueError("x must be bf16, the weight's dtype; got %s" % x.dtype)
     lead = tuple(x.shape[:-1])
     tokens = int(np.prod(lead)) if lead else 1
-    if fused and not 1 <= tokens <= GEMV_MAX_BATCH:
+    if fused and not 1 <= tokens <= GEMM_MAX_ROWS:
         raise ValueError("the fused product takes 1..%d rows of x, got %d"
-                         % (GEMV_MAX_BATCH, tokens))
+                         % (GEMM_MAX_ROWS, tokens))
     x = x.to(dev)
     if rows == 0:
         return x.new_zeros(lead + (0,))
@@ -338,7 +347,8 @@ def decompress_linear_gpu(layer: CompressedLayer, x: torch.Tensor, slice_rows: i
                                   tables=_tables_for(layer.encoded, dev))
     if fused:
         xb = x.reshape(tokens, cols).contiguous()
-        y = decode_gemv(t, xb, rows, cols).to(torch.bfloat16)
+        fn = decode_gemv if tokens <= GEMV_MAX_BATCH else decode_gemm
+        y = fn(t, xb, rows, cols).to(torch.bfloat16)
         return y.reshape(lead + (rows,))
     return decode_linear(t, x, rows, cols, slice_rows)
 

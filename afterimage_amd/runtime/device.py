@@ -382,13 +382,21 @@ class DeviceTensor:
         if sign_mantissa is not None:
             sm = torch.as_tensor(sign_mantissa).reshape(-1).to(device=device, dtype=torch.uint8)
         return cls(
-            packed=torch.from_numpy(np.ascontiguousarray(enc.packed)).to(device),
-            chunk_offsets=torch.from_numpy(
-                np.ascontiguousarray(enc.chunk_offsets, dtype=np.int32)).to(device),
-            chunk_nbytes=torch.from_numpy(
-                np.ascontiguousarray(enc.chunk_nbytes, dtype=np.int32)).to(device),
+            packed=_on_device(enc.packed, torch.uint8, device),
+            chunk_offsets=_on_device(enc.chunk_offsets, torch.int32, device),
+            chunk_nbytes=_on_device(enc.chunk_nbytes, torch.int32, device),
             sign_mantissa=sm, tables=tables, chunk_size=int(enc.chunk_size),
             n_symbols=int(enc.n_symbols), shape=tuple(enc.shape))
+
+
+def _on_device(a, dtype: torch.dtype, device) -> torch.Tensor:
+    """A 1-D contiguous ``dtype`` tensor on ``device`` with a's values: a
+    tensor already there is used as it is (a layer kept resident in HBM is
+    not copied again), a host array or tensor is copied."""
+    if isinstance(a, torch.Tensor):
+        return a.reshape(-1).to(device=device, dtype=dtype).contiguous()
+    np_dtype = {torch.uint8: np.uint8, torch.int32: np.int32}[dtype]
+    return torch.from_numpy(np.ascontiguousarray(np.asarray(a).reshape(-1), dtype=np_dtype)).to(device)
 
 
 def build_indexes(tensors: list[DeviceTensor], keep_unusable: bool = False) -> None:
@@ -517,6 +525,7 @@ def decode_u8(tensors: list[DeviceTensor], n_out: list[int] | None = None,
 
 
 GEMV_MAX_BATCH = 4
+GEMM_MAX_ROWS = 16
 
 
 def decode_gemv(t: DeviceTensor, x: torch.Tensor, rows: int, cols: int,
@@ -526,14 +535,29 @@ def decode_gemv(t: DeviceTensor, x: torch.Tensor, rows: int, cols: int,
     GPU (b <= GEMV_MAX_BATCH); y: fp32 [b, rows], zeros when not given.
     Returns y. The fp32 sums are added with atomics, so their order (and
     the last bits of y) can vary between calls."""
+    return _fused(t, x, rows, cols, y, GEMV_MAX_BATCH, "aimg_decode_gemv_bf16")
+
+
+def decode_gemm(t: DeviceTensor, x: torch.Tensor, rows: int, cols: int,
+                y: torch.Tensor | None = None) -> torch.Tensor:
+    """decode_gemv for 1..GEMM_MAX_ROWS rows of x (speculative-verify
+    widths), on the matrix cores: bf16 products, fp32 sums, W decoded inside
+    the kernel and never written. Needs cols % 8 == 0 and chunks of 1024 to
+    2^24 symbols (a multiple of 8); other layers raise (the blocked
+    decode_linear serves them)."""
+    return _fused(t, x, rows, cols, y, GEMM_MAX_ROWS, "aimg_decode_gemm_bf16")
+
+
+def _fused(t: DeviceTensor, x: torch.Tensor, rows: int, cols: int, y: torch.Tensor | None,
+           max_b: int, entry: str) -> torch.Tensor:
     dev = x.device
     if dev.type != "cuda":
         raise RuntimeError("the decoder runs on the GPU only; got x on %s" % dev)
     if x.dim() != 2 or x.dtype != torch.bfloat16 or x.shape[1] != cols or not x.is_contiguous():
         raise ValueError("x must be a contiguous bf16 [batch, %d] tensor" % cols)
     b = int(x.shape[0])
-    if not 1 <= b <= GEMV_MAX_BATCH:
-        raise ValueError("batch must be in 1..%d, got %d" % (GEMV_MAX_BATCH, b))
+    if not 1 <= b <= max_b:
+        raise ValueError("batch must be in 1..%d, got %d" % (max_b, b))
     if rows * cols != t.n_symbols:
         raise ValueError("rows * cols = %d, the tensor has %d weights" % (rows * cols, t.n_symbols))
     if y is None:
@@ -547,7 +571,7 @@ def decode_gemv(t: DeviceTensor, x: torch.Tensor, rows: int, cols: int,
     d[0] = _descriptor(t, y, t.n_symbols)
     d[0].out = None
     with torch.cuda.device(dev):
-        _native.check(_native.lib().aimg_decode_gemv_bf16(
+        _native.check(getattr(_native.lib(), entry)(
             d, rows, cols, x.data_ptr(), b, y.data_ptr(), _stream_handle(dev)))
     return y
 

@@ -1,23 +1,26 @@
 """Decode throughput of the gfx950 BF16 weight decoder on one MI355X.
 
-Default workload (the headline): one 5120x17408 bf16 weight (N(0, 0.02) with
-0.1% N(0, 0.5) outliers, seed 2), compressed with a per-tensor
-canonical-Huffman exponent codebook in chunks of 65536 symbols (1360 chunks).
-Its compressed form (bitstreams, chunk offsets/lengths, sign/mantissa bytes,
-decode table, and the segment index built once when the layer became
-resident) is in HBM before timing starts. One step = one kernel launch that
-rebuilds the whole bf16 tensor in HBM. The same launch without the index is
-timed as well ("no_index"), and so are launches over three copies of the
-layer in turn ("cold_inputs"), whose inputs no longer fit in the GPU's
-last-level cache between launches. --workload block does the same for a whole
-14B-class decoder block (9 tensors, one codebook per role) in one launch.
-Prints one JSON line.
+Headline (value and roofline of the default run): one 5120x17408 bf16 weight
+(N(0, 0.02) with 0.1% N(0, 0.5) outliers, seed 2), compressed with a
+per-tensor canonical-Huffman exponent codebook in chunks of 65536 symbols
+(1360 chunks), its store-format arrays (bitstreams, chunk offsets/lengths,
+sign/mantissa bytes) and decode table in HBM before timing starts, and
+nothing else: no derived data. One step = one kernel launch that rebuilds the
+whole bf16 tensor in HBM, the decode decompress_layer_gpu and the streamed
+ring run. The same launches over three copies of the layer in turn
+("cold_inputs") read their inputs from HBM rather than the last-level cache.
+
+The default run ("suite") adds, as extra keys of the same line, each timed in
+this run: the layer at the reference store's default 1024-symbol chunks; the
+layer with a prebuilt segment index (the compressed-resident tier, with its
+build time); config 1 (1024x3072); config 3 (a 14B-class block in one
+launch); config 4 (40 streamed blocks through a 2-slot ring); config 5 (the
+fused decode->GEMV at batch 1 and 4, both chunk sizes). Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
-                    [--workload layer|block|gemv|ring|api|head|resync] [--chunk-size N]
-                    [--batch B] [--slice-rows R] [--no-index] [--no-cold]
-                    [--no-cpu-baseline]
-                    [--cpu-threads T]
+                    [--workload suite|layer|block|gemv|ring|api|head|resync]
+                    [--chunk-size N] [--batch B] [--slice-rows R] [--index] [--no-cold]
+                    [--no-cpu-baseline] [--cpu-threads T]
 """
 from __future__ import annotations
 
@@ -140,16 +143,26 @@ def _copy_calibration(mib: int, steps: int, warmup: int) -> int:
 
 
 def _bench_ring(args) -> int:
+    rec = _ring(args)
+    if rec is None:
+        return 1
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+def _ring(args, blocks=None) -> dict | None:
     """Streamed 14B-class blocks: two distinct compressed blocks in pinned host
     memory, cycled through `--layers` layers per step; H2D on a side stream,
-    decode on the compute stream, 2-slot ring under a 4 GiB device budget."""
+    decode on the compute stream, 2-slot ring under a 4 GiB device budget.
+    Returns the JSON record, or None when a decoded layer is not bit-exact."""
     from afterimage_amd import workloads
     from afterimage_amd.runtime.stream_ring import HostBlock, LayerRing
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     t0 = time.perf_counter()
-    blocks = [workloads.block_14b(seed=s) for s in (3, 4)]
+    if blocks is None:
+        blocks = [workloads.block_14b(seed=s) for s in (3, 4)]
     hbs = [HostBlock([l for _, _, l in blk]) for blk in blocks]
     _log("2 blocks built and pinned in %.1fs: %.1f MB compressed each"
          % (time.perf_counter() - t0, hbs[0].nbytes / 1e6))
@@ -164,7 +177,7 @@ def _bench_ring(args) -> int:
     torch.cuda.synchronize(dev)
     if not ok:
         print("streamed decode differs from the original weights", file=sys.stderr)
-        return 1
+        return None
     ring.timing = True
     walls = []
     dec_s = []
@@ -216,26 +229,39 @@ def _bench_ring(args) -> int:
         "roofline": None,
         "cpu_baseline": None,
     }
+    del ring, hbs, slot
+    return rec
+
+
+def _bench_gemv(args) -> int:
+    rec = _gemv(args)
+    if rec is None:
+        return 1
     print(json.dumps(rec), flush=True)
     return 0
 
 
-def _bench_gemv(args) -> int:
+def _gemv(args, W=None, layer=None) -> dict | None:
     """Fused decode->GEMV: y[b] = W x[b] for the 5120x17408 weight, W decoded
     in the kernel and never written. One step = zero y + one launch; the
-    roofline figures come from the launches alone, timed in a second loop."""
+    roofline figures come from the launches alone, timed in a second loop.
+    With --index the layer's segment index is built first (the
+    compressed-resident tier); without it the GEMV decodes speculatively, as
+    decompress_matvec_gpu does. Returns the JSON record, or None when y is
+    outside the tolerance."""
     from afterimage_amd import workloads
     from afterimage_amd.runtime.device import DeviceTensor, decode_gemv
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    W, layer = workloads.single_layer(seed=2, chunk_size=args.chunk_size)
+    if W is None:
+        W, layer = workloads.single_layer(seed=2, chunk_size=args.chunk_size)
     rows, cols = W.shape
     b = args.batch
     g = np.random.default_rng(23)
     x = torch.from_numpy(g.standard_normal((b, cols), dtype=np.float32)).to(torch.bfloat16).to(dev)
     t = DeviceTensor.from_encoded(layer.encoded, layer.sign_mantissa, dev)
-    if not args.no_index:
+    if getattr(args, "index", False):
         t.build_index()  # the resident layer's segment index, built once
     y = torch.zeros((b, rows), dtype=torch.float32, device=dev)
 
@@ -252,7 +278,7 @@ def _bench_gemv(args) -> int:
     if not ok:
         print("fused GEMV differs from decode-then-matmul beyond rel 1e-2 / abs 1e-3",
               file=sys.stderr)
-        return 1
+        return None
     stream = torch.cuda.current_stream(dev)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
@@ -328,8 +354,8 @@ def _bench_gemv(args) -> int:
                      "algorithmic_bytes_per_launch": algo_bytes},
         "cpu_baseline": None,
     }
-    print(json.dumps(rec), flush=True)
-    return 0
+    del t, ex, y
+    return rec
 
 
 def _bench_head(args) -> int:
@@ -592,9 +618,12 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=["layer", "block", "gemv", "ring", "api", "head", "resync"],
-                    default="layer",
-                    help="layer: one 5120x17408 weight (the headline); block: a whole "
+    ap.add_argument("--workload",
+                    choices=["suite", "layer", "block", "gemv", "ring", "api", "head", "resync"],
+                    default="suite",
+                    help="suite (default): the headline layer and every other configuration "
+                         "as extra keys of one line; layer: one 5120x17408 weight (the "
+                         "headline alone); block: a whole "
                          "14B-class decoder block in one launch; gemv: fused decode->GEMV "
                          "of the 5120x17408 weight with a [batch, 17408] activation; ring: 40 "
                          "streamed blocks from pinned host memory through a 2-slot ring; api: "
@@ -607,12 +636,13 @@ def main() -> int:
                     help="gemv: batch (1..4); head: tokens of x")
     ap.add_argument("--slice-rows", type=int, default=8192, help="head: rows per block")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-index", action="store_true",
-                    help="layer/block: time the decode without segment indexes only")
+    ap.add_argument("--index", action="store_true",
+                    help="layer/block/gemv: build each tensor's segment index before timing "
+                         "(the compressed-resident tier; the default decodes from the "
+                         "store-format arrays alone, as the drop-in API does)")
     ap.add_argument("--no-cold", action="store_true",
-                    help="layer: skip the cold-input launches (kernel traces of the timed loop)")
-    ap.add_argument("--index-only", action="store_true",
-                    help="layer/block: skip the launches without the index (for profiling)")
+                    help="suite/layer: skip the cold-input launches (kernel traces of the "
+                         "timed loop)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="CPU-baseline threads (0: OpenMP's count, i.e. every CPU given)")
     ap.add_argument("--chunk-size", type=int, default=None,
@@ -627,9 +657,6 @@ def main() -> int:
         print("bench.py measures one GPU only: this build has no multi-GPU decode path "
               "(chunks would shard by range with no exchange step). Run with --gpus 1.",
               file=sys.stderr)
-        return 2
-    if args.no_index and args.index_only:
-        print("--no-index and --index-only exclude each other", file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
@@ -650,133 +677,109 @@ def main() -> int:
     if args.workload == "resync":
         return _bench_resync(args)
 
-    from afterimage_amd import _native, workloads
+    if args.workload == "suite":
+        return _suite(args)
+    return _single(args)
+
+
+LAYER_WORKLOAD = ("bf16 5120x17408 weight decode, N(0,0.02) + 0.1%% N(0,0.5) outliers (seed 2), "
+                  "per-tensor Huffman exponent codebook, %d-symbol chunks (%d), inputs resident "
+                  "in HBM, one launch per step, %s")
+BLOCK_WORKLOAD = ("bf16 14B-class decoder block (q,o 5120x5120; k,v 1024x5120; gate,up 17408x5120; "
+                  "down 5120x17408; 2 RMSNorm 5120), N(0,0.02) weights, norms N(1,0.05) (seed %d), "
+                  "one exponent codebook per role, 65536-symbol chunks (%d), inputs resident in "
+                  "HBM, all 9 tensors in one launch per step, %s")
+NO_INDEX = "decoded from the store-format arrays alone (no derived data), as decompress_layer_gpu does"
+WITH_INDEX = ("each tensor's segment index (derived data, built once when the compressed tensor "
+              "becomes resident in HBM; a tier the reference does not have) prebuilt")
+
+
+def _decode(items, steps: int, warmup: int, index: bool = False, cold: bool = False) -> dict:
+    """aimg_decode_bf16 over the items' tensors, one launch per step, inputs
+    resident in HBM: launches timed with HIP events on the launch stream,
+    the loop by the host clock; bit-exactness checked against the original
+    weights before timing. index: build each tensor's segment index first
+    (its build time is reported). cold: also three copies decoded in turn,
+    so that the inputs come from HBM rather than the last-level cache."""
+    from afterimage_amd import _native
     from afterimage_amd.runtime.device import DeviceTensor, _descriptor
 
     dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    t0 = time.perf_counter()
-    if args.workload == "layer":
-        seed = 2
-        W, layer = workloads.single_layer(seed=seed, chunk_size=args.chunk_size)
-        items = [("layer", W, layer)]
-        config_key = "5120x17408/seed%d/chunk%d/outliers1e-3" % (seed, args.chunk_size)
-        description = ("bf16 5120x17408 weight decode, N(0,0.02) + 0.1%% N(0,0.5) outliers "
-                       "(seed 2), per-tensor Huffman exponent codebook, %d-symbol chunks "
-                       "(%d), inputs resident in HBM, one launch per step"
-                       % (args.chunk_size, layer.encoded.n_chunks))
-    else:
-        seed = 3
-        items = workloads.block_14b(seed=seed)
-        config_key = "block14b/seed%d/chunk65536/per-role" % seed
-        description = ("bf16 14B-class decoder block (q,o 5120x5120; k,v 1024x5120; gate,up "
-                       "17408x5120; down 5120x17408; 2 RMSNorm 5120), N(0,0.02) weights, "
-                       "norms N(1,0.05) (seed 3), one exponent codebook per role, "
-                       "65536-symbol chunks (5042), inputs resident in HBM, all 9 tensors "
-                       "in one launch per step")
     layers = [layer for _, _, layer in items]
-    _log("workload built in %.1fs: %d tensors, %d chunks, packed %.2f MB"
-         % (time.perf_counter() - t0, len(items), sum(l.encoded.n_chunks for l in layers),
-            sum(l.encoded.packed.nbytes for l in layers) / 1e6))
     dts = [DeviceTensor.from_encoded(l.encoded, l.sign_mantissa, dev) for l in layers]
     outs = [torch.empty(l.encoded.n_symbols, dtype=torch.bfloat16, device=dev) for l in layers]
     lib = _native.lib()
     stream = torch.cuda.current_stream(dev)
     handle = ctypes.c_void_p(stream.cuda_stream)
     decode = lib.aimg_decode_bf16
-    n_desc = len(dts)
-
-    def descriptors():
-        d = (_native.AimgTensor * len(dts))()
-        for j, (dt, o) in enumerate(zip(dts, outs)):
-            d[j] = _descriptor(dt, o, o.numel())
-        return d
-
-    def bit_exact() -> bool:
-        torch.cuda.synchronize(dev)
-        return all(torch.equal(o.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
-                   for (_, W, _), o in zip(items, outs))
-
-    def launches(d, k: int) -> float:
-        """Seconds per launch of k back-to-back launches, by HIP events."""
+    index_info = None
+    if index:
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize(dev)
         e0.record(stream)
-        for _ in range(k):
-            rc = decode(d, n_desc, handle)
+        for dt in dts:
+            dt.build_index()
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        ix_bytes = sum(dt.index.numel() for dt in dts if dt.index is not None)
+        comp = sum(dt.packed.numel() + dt.sign_mantissa.numel() for dt in dts)
+        index_info = {"build_us": round(e0.elapsed_time(e1) * 1e3, 1), "bytes": ix_bytes,
+                      "bytes_read_per_launch": sum(dt.index_bytes_read for dt in dts),
+                      "frac_of_compressed": round(ix_bytes / comp, 4)}
+
+    def descriptors(ts, os_):
+        d = (_native.AimgTensor * len(ts))()
+        for j, (dt, o) in enumerate(zip(ts, os_)):
+            d[j] = _descriptor(dt, o, o.numel())
+        return d
+
+    def exact(os_) -> bool:
+        torch.cuda.synchronize(dev)
+        return all(torch.equal(o.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
+                   for (_, W, _), o in zip(items, os_))
+
+    def launches(d, k: int) -> float:
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(dev)
+        e0.record(stream)
+        for j in range(k):
+            rc = decode(d[j % len(d)], len(dts), handle)
             if rc:
                 _native.check(rc)
         e1.record(stream)
         torch.cuda.synchronize(dev)
         return e0.elapsed_time(e1) / 1e3 / k
 
-    # Without segment indexes first (the path any caller gets), then, unless
-    # --no-index, build each tensor's index once (a resident layer's load
-    # step) and time the decode that uses it.
-    no_index_s = None
-    if not args.index_only:
-        plain = descriptors()
-        launches(plain, max(1, args.warmup))
-        if not bit_exact():
-            print("decoded output (no index) differs from the original weights", file=sys.stderr)
-            return 1
-        no_index_s = launches(plain, min(args.steps, 100))
-    index_info = None
-    if not args.no_index:
-        for o in outs:
-            o.fill_(0)
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for dt in dts:
-            dt.build_index()
-        e1.record(stream)
-        torch.cuda.synchronize(dev)
-        ix_bytes = sum(dt.index.numel() for dt in dts)
-        comp = sum(dt.packed.numel() + dt.sign_mantissa.numel() for dt in dts)
-        index_info = {
-            "build_us": round(e0.elapsed_time(e1) * 1e3, 1),
-            "bytes": ix_bytes,
-            "bytes_read_per_launch": sum(dt.index_bytes_read for dt in dts),
-            "frac_of_compressed": round(ix_bytes / comp, 4),
-        }
-    desc = descriptors()
-
-    def step():
-        rc = decode(desc, n_desc, handle)
-        if rc:
-            _native.check(rc)
-
-    for _ in range(args.warmup):
-        step()
-    # Bit-exactness of the benchmarked outputs (outside the timed region).
-    ok = bit_exact()
+    desc = descriptors(dts, outs)
+    launches([desc], max(1, warmup))
+    ok = exact(outs)
     if not ok:
-        print("decoded output differs from the original weights", file=sys.stderr)
-        return 1
-    _log("warmup done, output bit-exact (index %s)" % ("on" if index_info else "off"))
-
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
+        raise RuntimeError("decoded output differs from the original weights")
     torch.cuda.synchronize(dev)
     t_start = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(args.steps):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize(dev)
+    kernel_s = launches([desc], steps)
     wall = time.perf_counter() - t_start
-    kernel_s = ev0.elapsed_time(ev1) / 1e3 / args.steps
-    _log("timed %d steps: wall %.3f ms/step, events %.1f us/launch"
-         % (args.steps, wall * 1e3 / args.steps, kernel_s * 1e6))
-
-    # The loop above decodes one layer over and over, so part of its inputs
-    # (118 MB for the 5120x17408 layer) stays in the GPU's 256 MB last-level
-    # cache between launches. Decoding three copies of the layer in turn
-    # (354 MB of inputs) reads them from HBM, as a streamed model would.
-    cold = None
-    if args.workload == "layer" and not args.no_cold:
+    n = sum(l.encoded.n_symbols for l in layers)
+    n_chunks = sum(l.encoded.n_chunks for l in layers)
+    chunk_bytes = sum(int(l.encoded.chunk_nbytes.astype(np.int64).sum()) for l in layers)
+    n_tables = len({dt.tables.key for dt in dts})
+    # bitstreams + chunk offsets and lengths + sign/mantissa + window tables
+    # + bf16 write (+ the segment index read, when there is one)
+    algo = chunk_bytes + 8 * n_chunks + n + (5 * 4096 + 256) * n_tables + 2 * n
+    if index_info:
+        algo += index_info["bytes_read_per_launch"]
+    res = {"kernel_us": round(kernel_s * 1e6, 2), "wall_s": wall, "steps": steps,
+           "decompressed_gbs": round(2 * n / kernel_s / 1e9, 1),
+           "achieved_gbs": round(algo / kernel_s / 1e9, 1),
+           "frac": round(algo / kernel_s / 1e9 / HBM_PEAK_GBS, 4),
+           "algorithmic_bytes_per_launch": algo, "n_weights": n, "n_chunks": n_chunks,
+           "n_tensors": len(items), "decode_tables": n_tables,
+           "packed_exponent_bytes": chunk_bytes,
+           "bits_per_exponent": round(8 * chunk_bytes / n, 4), "bit_exact": ok,
+           "segment_index": index_info}
+    if cold:
         import dataclasses
 
         copies = [(dts, outs)]
@@ -786,99 +789,181 @@ def main() -> int:
                 chunk_nbytes=dt.chunk_nbytes.clone(), sign_mantissa=dt.sign_mantissa.clone(),
                 index=None if dt.index is None else dt.index.clone()) for dt in dts]
             copies.append((c_dts, [torch.empty_like(o) for o in outs]))
-        c_desc = []
-        for c_dts, c_outs in copies:
-            d = (_native.AimgTensor * len(c_dts))()
-            for j, (dt, o) in enumerate(zip(c_dts, c_outs)):
-                d[j] = _descriptor(dt, o, o.numel())
-            c_desc.append(d)
-        k_cold = 3 * min(args.steps // 3, 40) or 3
-        for k in range(6):
-            _native.check(decode(c_desc[k % 3], n_desc, handle))
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize(dev)
-        e0.record(stream)
-        for k in range(k_cold):
-            rc = decode(c_desc[k % 3], n_desc, handle)
-            if rc:
-                _native.check(rc)
-        e1.record(stream)
-        torch.cuda.synchronize(dev)
-        cold_s = e0.elapsed_time(e1) / 1e3 / k_cold
-        cold_ok = all(torch.equal(o.view(torch.int16).cpu(), W.reshape(-1).view(torch.int16))
-                      for c_dts, c_outs in copies for (_, W, _), o in zip(items, c_outs))
-        cold = {"kernel_us": round(cold_s * 1e6, 2), "launches": k_cold, "bit_exact": cold_ok,
-                "inputs_bytes": 3 * sum(dt.packed.numel() + dt.sign_mantissa.numel()
-                                        for dt in dts)}
+        c_desc = [descriptors(c_dts, c_outs) for c_dts, c_outs in copies]
+        k_cold = 3 * max(1, min(steps // 3, 40))
+        launches(c_desc, 6)
+        cold_s = launches(c_desc, k_cold)
+        cold_ok = all(exact(c_outs) for _, c_outs in copies)
+        res["cold_inputs"] = {
+            "kernel_us": round(cold_s * 1e6, 2), "launches": k_cold, "bit_exact": cold_ok,
+            "decompressed_gbs": round(2 * n / cold_s / 1e9, 1),
+            "frac": round(algo / cold_s / 1e9 / HBM_PEAK_GBS, 4),
+            "inputs_bytes": 3 * sum(dt.packed.numel() + dt.sign_mantissa.numel() for dt in dts),
+            "what": "three copies decoded in turn (inputs read from HBM, not from the "
+                    "last-level cache)"}
         del copies, c_desc
+    del dts, outs
+    torch.cuda.empty_cache()
+    return res
 
-    n = sum(l.encoded.n_symbols for l in layers)
-    n_chunks = sum(l.encoded.n_chunks for l in layers)
-    chunk_bytes = sum(int(l.encoded.chunk_nbytes.astype(np.int64).sum()) for l in layers)
-    n_tables = len({dt.tables.key for dt in dts})
-    # bitstreams + offsets and lengths + sign/mantissa + window tables + bf16
-    # write (+ the segment index entries and chunk bases read)
-    algo_plain = chunk_bytes + 8 * n_chunks + n + (5 * 4096 + 256) * n_tables + 2 * n
-    algo_bytes = algo_plain + (index_info["bytes_read_per_launch"] if index_info else 0)
-    achieved = algo_bytes / kernel_s / 1e9
-    value = 2 * n * args.steps / wall / 1e9
-    if index_info:
-        config_key += "/index"
-    traffic = _traffic(config_key)
+
+def _record(args, res: dict, workload: str, config_key: str, layers, what: str) -> dict:
+    """The driver's JSON line for a decode measurement (value: decompressed
+    GB/s over the host-clocked loop)."""
+    n = res["n_weights"]
     rec = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": round(2 * n * res["steps"] / res["wall_s"] / 1e9, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": res["steps"],
         "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "ms_per_step": round(res["wall_s"] * 1e3 / res["steps"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {
-            "workload": description,
-            "config_key": config_key,
-            "n_tensors": len(items),
-            "n_weights": n,
-            "n_chunks": n_chunks,
-            "decode_tables": n_tables,
-            "packed_exponent_bytes": chunk_bytes,
-            "bits_per_exponent": round(8 * chunk_bytes / n, 4),
-            "bit_exact": ok,
-            "segment_index": index_info,
-        },
+        "config": {"workload": workload, "config_key": config_key,
+                   **{k: res[k] for k in ("n_tensors", "n_weights", "n_chunks", "decode_tables",
+                                          "packed_exponent_bytes", "bits_per_exponent",
+                                          "bit_exact", "segment_index")}},
         "roofline": {
             "bound": "hbm",
-            "achieved": round(achieved, 1),
+            "achieved": res["achieved_gbs"],
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "algorithmic_bytes_per_launch": algo_bytes,
-            "kernel_us": round(kernel_s * 1e6, 2),
+            "frac": res["frac"],
+            "traffic": _traffic(config_key),
+            "algorithmic_bytes_per_launch": res["algorithmic_bytes_per_launch"],
+            "kernel_us": res["kernel_us"],
         },
-        "cold_inputs": None if cold is None else dict(
-            cold, decompressed_gbs=round(2 * n / (cold["kernel_us"] / 1e6) / 1e9, 1),
-            frac=round(algo_bytes / (cold["kernel_us"] / 1e6) / 1e9 / HBM_PEAK_GBS, 4),
-            what="three copies of the layer decoded in turn (inputs read from HBM, not from "
-                 "the last-level cache)"),
-        "no_index": None if no_index_s is None else {
-            "kernel_us": round(no_index_s * 1e6, 2),
-            "decompressed_gbs": round(2 * n / no_index_s / 1e9, 1),
-            "achieved_gbs": round(algo_plain / no_index_s / 1e9, 1),
-            "frac": round(algo_plain / no_index_s / 1e9 / HBM_PEAK_GBS, 4),
-            "launches": min(args.steps, 100),
-        },
+        "cold_inputs": res.get("cold_inputs"),
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
         _log("timing the CPU baseline (~15 s)")
-        rec["cpu_baseline"] = _cpu_baseline(layers, args.cpu_threads,
-                                            "the whole " + args.workload)
+        rec["cpu_baseline"] = _cpu_baseline(layers, args.cpu_threads, what)
+    return rec
+
+
+def _single(args) -> int:
+    """--workload layer | block: one decode measurement, without the segment
+    index unless --index."""
+    from afterimage_amd import workloads
+
+    torch.cuda.set_device(0)
+    t0 = time.perf_counter()
+    tier = WITH_INDEX if args.index else NO_INDEX
+    if args.workload == "layer":
+        W, layer = workloads.single_layer(seed=2, chunk_size=args.chunk_size)
+        items = [("layer", W, layer)]
+        key = "5120x17408/seed2/chunk%d/outliers1e-3" % args.chunk_size
+        desc = LAYER_WORKLOAD % (args.chunk_size, layer.encoded.n_chunks, tier)
+    else:
+        items = workloads.block_14b(seed=3)
+        key = "block14b/seed3/chunk65536/per-role"
+        desc = BLOCK_WORKLOAD % (3, sum(l.encoded.n_chunks for _, _, l in items), tier)
+    if args.index:
+        key += "/index"
+    _log("workload built in %.1fs" % (time.perf_counter() - t0))
+    res = _decode(items, args.steps, args.warmup, index=args.index,
+                  cold=args.workload == "layer" and not args.no_cold)
+    rec = _record(args, res, desc, key, [l for _, _, l in items], "the whole " + args.workload)
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+def _suite(args) -> int:
+    """The default run: the headline (config 2, the 5120x17408 layer in
+    65536-symbol chunks decoded without an index, as decompress_layer_gpu and
+    the streamed ring decode it) as value and roofline, and the other
+    configurations as extra keys, each timed in this same run."""
+    import types
+
+    from afterimage_amd import workloads
+    from afterimage_amd.runtime.compressed_store import compress_layer
+
+    torch.cuda.set_device(0)
+    t0 = time.perf_counter()
+    W, layer = workloads.single_layer(seed=2, chunk_size=65536)
+    items = [("layer", W, layer)]
+    _log("layer built in %.1fs" % (time.perf_counter() - t0))
+    head = _decode(items, args.steps, args.warmup, cold=not args.no_cold)
+    key = "5120x17408/seed2/chunk65536/outliers1e-3"
+    rec = _record(args, head, LAYER_WORKLOAD % (65536, layer.encoded.n_chunks, NO_INDEX), key,
+                  [layer], "the whole layer")
+    _log("headline: %.2f us per launch, %.4f of HBM roofline" % (head["kernel_us"], head["frac"]))
+    short = min(args.steps, 100)
+    extra = {}
+
+    def brief(res: dict) -> dict:
+        out = {k: res[k] for k in ("kernel_us", "decompressed_gbs", "achieved_gbs", "frac",
+                                   "algorithmic_bytes_per_launch", "n_weights", "n_chunks",
+                                   "bit_exact")}
+        if res.get("cold_inputs"):
+            out["cold_inputs"] = {k: res["cold_inputs"][k]
+                                  for k in ("kernel_us", "decompressed_gbs", "frac", "bit_exact")}
+        if res.get("segment_index"):
+            out["segment_index"] = res["segment_index"]
+        return out
+
+    # The same layer at the reference store's default 1024-symbol chunks
+    # (afterimage compress, cli.py:1117 / config.py:361), no index.
+    l1024 = compress_layer(W, chunk_size=1024)
+    extra["chunk1024"] = dict(brief(_decode([("layer", W, l1024)], short, args.warmup, cold=True)),
+                              what="the same layer in 1024-symbol chunks, no index")
+    del l1024
+    # The compressed-resident tier: the layer's segment index built once,
+    # then decodes that use it (no reference counterpart).
+    ix = _decode(items, short, args.warmup, index=True)
+    extra["index_tier"] = dict(
+        brief(ix), what="the layer with its segment index prebuilt: derived data built once "
+                        "per resident compressed tensor, for a tier that keeps tensors "
+                        "compressed in HBM (the reference has none); build_us + kernel_us is "
+                        "the one-shot cost")
+    # Config 1: the 1024x3072 layer at 4096-symbol chunks.
+    Ws, small = workloads.small_layer(seed=1)
+    extra["config1_small_layer"] = dict(
+        brief(_decode([("small", Ws, small)], short, args.warmup)),
+        what="bf16 1024x3072, 4096-symbol chunks, one launch, no index (launch-bound)")
+    # Config 5: the fused decode->GEMV at batch 1 and 4, speculative decode
+    # (no index) as decompress_matvec_gpu runs it, at both chunk sizes.
+    gargs = types.SimpleNamespace(steps=short, warmup=args.warmup, index=False, chunk_size=65536)
+    for b in (1, 4):
+        gargs.batch = b
+        g = _gemv(gargs, W, layer)
+        extra["config5_gemv_b%d" % b] = None if g is None else dict(
+            g["roofline"], within_tolerance=g["config"]["within_tolerance"],
+            what="fused decode->GEMV, 5120x17408 x [%d, 17408], 65536-symbol chunks, no index; "
+                 "frac: the exponent-byte decode's time over the GEMV's" % b)
+    l1024 = compress_layer(W, chunk_size=1024)
+    for b in (1, 4):
+        gargs.batch = b
+        gargs.chunk_size = 1024
+        g = _gemv(gargs, W, l1024)
+        extra["config5_gemv_b%d_chunk1024" % b] = None if g is None else dict(
+            g["roofline"], within_tolerance=g["config"]["within_tolerance"],
+            what="the same at 1024-symbol chunks")
+    del l1024
+    # Config 3: a 14B-class block in one launch, no index.
+    t0 = time.perf_counter()
+    blk3 = workloads.block_14b(seed=3)
+    _log("block built in %.1fs" % (time.perf_counter() - t0))
+    extra["config3_block"] = dict(
+        brief(_decode(blk3, short, args.warmup)),
+        what="the 14B-class block (9 tensors, 5 codebooks, 65536-symbol chunks) in one launch, "
+             "no index")
+    # Config 4: 40 streamed blocks through a 2-slot ring under 4 GiB.
+    blk4 = workloads.block_14b(seed=4)
+    rargs = types.SimpleNamespace(layers=40, steps=3, warmup=2)
+    r = _ring(rargs, [blk3, blk4])
+    extra["config4_ring"] = None if r is None else {
+        "layers_per_s": r["value"], "ms_per_40_layers": r["ms_per_step"],
+        "decode_only_gbs": r["decode_only_gbs"], "h2d_pinned_gbs": r["h2d_pinned_gbs"],
+        "h2d_bound_layers_per_s": r["h2d_bound_layers_per_s"], "bit_exact": r["config"]["bit_exact"],
+        "what": r["config"]["workload"]}
+    rec["extra"] = extra
     print(json.dumps(rec), flush=True)
     return 0
 

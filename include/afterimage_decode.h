@@ -130,6 +130,22 @@ int aimg_decode_gemv_bf16(const aimg_tensor* t, int64_t rows, int64_t cols, cons
                           int batch, float* y, void* stream);
 
 /*
+ * Fused decode -> GEMM for 1..16 rows of x: y[t][r] += sum_c W[r][c] * x[t][c]
+ * in fp32 for t < n_x, W as in aimg_decode_gemv_bf16 (never written; t->out
+ * ignored), on the matrix cores (bf16 products, fp32 sums). x: bf16
+ * [n_x][cols], 16-byte aligned (device); y: float [n_x][rows] (device),
+ * zeroed by the caller and added to with atomics (the order of the fp32
+ * additions is not fixed). This is the chunked lm_head's speculative-verify
+ * forward (streaming_engine.py:2307-2332, called with step_k + 1 positions
+ * at :2554-2556: decompress_rows_gpu per row block, then F.linear) in one
+ * launch that writes no weights. Needs cols % 8 == 0, chunk_size a multiple
+ * of 8 in 1024 .. 2^24 and n_x * cols * 2 < 2^32; other shapes fail with
+ * AIMG_ERR_UNSUPPORTED (the caller then takes the blocked decode and GEMM).
+ */
+int aimg_decode_gemm_bf16(const aimg_tensor* t, int64_t rows, int64_t cols, const void* x,
+                          int n_x, float* y, void* stream);
+
+/*
  * out[i] = ((sm[i] & 0x80) << 8) | (exponent[i] << 7) | (sm[i] & 0x7F) for
  * i < n, on the GPU (all three pointers device memory; out is uint16 bf16
  * bits). Replaces recombine_exponent_and_sign_mantissa and _recombine

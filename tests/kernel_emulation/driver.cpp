@@ -90,9 +90,11 @@ int main(int argc, char** argv) {
             memcpy(t.index, hdr, sizeof hdr);
         }
     }
-    if (std::string(argv[2]) == "gemv") {
-        // y += W x for the rows x cols bf16 weight W, checked against
-        // expect_y.bin within rel 1e-2 / abs 1e-3 (the GPU tests' bar).
+    const bool gemm = std::string(argv[2]) == "gemm";
+    if (std::string(argv[2]) == "gemv" || gemm) {
+        // y += W x for the rows x cols bf16 weight W (gemm: on the matrix
+        // cores, up to 16 x vectors), checked against expect_y.bin within
+        // rel 1e-2 / abs 1e-3 (the GPU tests' bar).
         long long rows = 0, cols = 0, batch = 0;
         FILE* g = fopen((d + "/gemv.txt").c_str(), "r");
         if (!g || fscanf(g, "%lld %lld %lld", &rows, &cols, &batch) != 3) return 2;
@@ -102,8 +104,9 @@ int main(int argc, char** argv) {
         std::vector<uint8_t> yv(4 * batch * rows);
         float* y = exact<float>(yv);
         const void* x = exact<uint8_t>(xv);
-        const int rc = aimg_decode_gemv_bf16(&t, rows, cols, x, (int)batch, y, nullptr);
-        if (rc) { fprintf(stderr, "gemv rc=%d: %s\n", rc, aimg_last_error()); return 6; }
+        const int rc = gemm ? aimg_decode_gemm_bf16(&t, rows, cols, x, (int)batch, y, nullptr)
+                            : aimg_decode_gemv_bf16(&t, rows, cols, x, (int)batch, y, nullptr);
+        if (rc) { fprintf(stderr, "%s rc=%d: %s\n", argv[2], rc, aimg_last_error()); return 6; }
         const float* want = reinterpret_cast<const float*>(ey.data());
         size_t bad = 0;
         for (long long k = 0; k < batch * rows; ++k) {
@@ -111,8 +114,8 @@ int main(int argc, char** argv) {
             const double aw = want[k] < 0 ? -want[k] : want[k];
             bad += diff > 1e-3 + 1e-2 * aw;
         }
-        printf("%s gemv: %s (%zu of %lld outside tolerance)\n", d.c_str(), bad ? "MISMATCH" : "ok", bad,
-               batch * rows);
+        printf("%s %s: %s (%zu of %lld outside tolerance)\n", d.c_str(), argv[2], bad ? "MISMATCH" : "ok",
+               bad, batch * rows);
         return bad ? 1 : 0;
     }
     const char* ce = getenv("AIMG_EMU_COPIES");

@@ -60,8 +60,9 @@ struct Block {
     std::barrier<> bar;
     std::vector<std::barrier<>*> wave;
     std::vector<uint64_t> xbuf;
+    std::vector<uint64_t> mbuf;  // MFMA operands: 4 words a lane
     std::vector<int> flags;
-    explicit Block(unsigned n_) : n(n_), bar(n_), xbuf(n_), flags(n_) {
+    explicit Block(unsigned n_) : n(n_), bar(n_), xbuf(n_), mbuf(4 * n_), flags(n_) {
         for (unsigned w = 0; w * 64 < n; ++w)
             wave.push_back(new std::barrier<>(n - 64 * w < 64 ? n - 64 * w : 64));
     }
@@ -245,6 +246,7 @@ inline float atomicAdd(float* p, float v) {
     }
 }
 inline int __ffs(int x) { return __builtin_ffs(x); }
+inline uint32_t __umulhi(uint32_t a, uint32_t b) { return (uint32_t)(((uint64_t)a * b) >> 32); }
 inline void __builtin_amdgcn_s_setprio(int) {}  // wave issue priority: no effect here
 // v_dot2c_f32_bf16: c + a.lo b.lo + a.hi b.hi in fp32 (bf16 products are exact
 // in fp32).
@@ -256,6 +258,36 @@ inline float __builtin_amdgcn_fdot2_f32_bf16(emu_bf16x2 a, emu_bf16x2 b, float c
     return c + (__uint_as_float((uint32_t)x[0] << 16) * __uint_as_float((uint32_t)y[0] << 16) +
                 __uint_as_float((uint32_t)x[1] << 16) * __uint_as_float((uint32_t)y[1] << 16));
 }
+// v_mfma_f32_16x16x32_bf16 on a whole wave: A[i][k] is element k % 8 of
+// lane 16 (k / 8) + i, B[k][j] element k % 8 of lane 16 (k / 8) + j, and
+// lane 16 (i / 4) + j gets D[i][j] + C in element i % 4 (the layout the
+// hardware was checked to use). Products and sums in fp32, k in order.
+typedef __bf16 emu_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float emu_f32x4 __attribute__((ext_vector_type(4)));
+inline emu_f32x4 __builtin_amdgcn_mfma_f32_16x16x32_bf16(emu_bf16x8 a, emu_bf16x8 b, emu_f32x4 c, int, int,
+                                                         int) {
+    emu::Block& B = *emu::g_block;
+    const unsigned w = threadIdx.x >> 6, l = emu::lane();
+    B.wave[w]->arrive_and_wait();
+    std::memcpy(&B.mbuf[4 * threadIdx.x], &a, 16);
+    std::memcpy(&B.mbuf[4 * threadIdx.x + 2], &b, 16);
+    B.wave[w]->arrive_and_wait();
+    auto el = [&](unsigned ln, unsigned half, unsigned e) {
+        uint16_t v;
+        std::memcpy(&v, reinterpret_cast<const uint8_t*>(&B.mbuf[4 * (64 * w + ln) + 2 * half]) + 2 * e, 2);
+        return __uint_as_float((uint32_t)v << 16);
+    };
+    emu_f32x4 d;
+    for (unsigned r = 0; r < 4; ++r) {
+        const unsigned i = 4 * (l >> 4) + r, j = l & 15;
+        float s = c[r];
+        for (unsigned k = 0; k < 32; ++k) s += el(16 * (k / 8) + i, 0, k % 8) * el(16 * (k / 8) + j, 1, k % 8);
+        d[r] = s;
+    }
+    B.wave[w]->arrive_and_wait();
+    return d;
+}
+
 template <typename K, typename... A>
 inline void emu_launch(K kernel, dim3 g, dim3 b, A... args) {
     gridDim = {g.x, 1, 1};

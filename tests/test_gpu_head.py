@@ -129,7 +129,7 @@ def test_errors_and_empty_inputs():
     W = workloads.bf16_normal((40, 64), 2, 0.02)
     layer = compress_layer(W, chunk_size=128)
     with pytest.raises(ValueError):
-        decompress_linear_gpu(layer, _x((5, 64), 1), fused=True)   # more than 4 rows of x
+        decompress_linear_gpu(layer, _x((17, 64), 1), fused=True)  # more than 16 rows of x
     with pytest.raises(ValueError):
         decompress_linear_gpu(layer, _x((2, 63), 1))               # wrong width
     with pytest.raises(ValueError):

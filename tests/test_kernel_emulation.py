@@ -82,7 +82,9 @@ def _run(emu, name, mode, index="", runs=None, strided=None, cus=None, copies=No
     env.pop("AIMG_EMU_COPIES", None)
     env.pop("AIMG_SPEC_RUNS", None)
     if spec is not None:
-        env["AIMG_SPEC_RUNS"] = spec  # "0": tensors without an index decode chunk by chunk
+        # "0": tensors without an index decode chunk by chunk; "1": in
+        # speculative runs whatever their chunk size
+        env["AIMG_SPEC_RUNS"] = spec
     if cus is not None:
         env["AIMG_EMU_CUS"] = str(cus)  # a grid of 2 * cus workgroups
     if copies is not None:
@@ -92,7 +94,7 @@ def _run(emu, name, mode, index="", runs=None, strided=None, cus=None, copies=No
     if strided is not None:
         env["AIMG_RUN_STRIDED"] = strided
     args = [exe, str(d / name), mode] + ([index] if index else [])
-    r = subprocess.run(args, capture_output=True, text=True, env=env, timeout=600)
+    r = subprocess.run(args, capture_output=True, text=True, env=env, timeout=1800)
     assert r.returncode == 0 and ": ok" in r.stdout, (r.stdout + r.stderr)[-4000:]
 
 
@@ -111,7 +113,8 @@ def _bf16(emu, name, W, chunk_size, index="", runs=None, strided=None, cus=None,
     _run(emu, name, "bf16", index, runs, strided, cus, copies, spec)
 
 
-def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None, cus=None, spec=None):
+def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None, cus=None, spec=None,
+          mode="gemv"):
     W = workloads.bf16_normal((rows, cols), seed, 0.02, outlier_frac=1e-3)
     layer = compress_layer(W, chunk_size=chunk_size)
     g = np.random.default_rng(seed + 1)
@@ -123,7 +126,7 @@ def _gemv(emu, name, rows, cols, chunk_size, batch, seed, index="", runs=None, c
     want.numpy().tofile(os.path.join(d, "expect_y.bin"))
     with open(os.path.join(d, "gemv.txt"), "w") as f:
         f.write("%d %d %d\n" % (rows, cols, batch))
-    _run(emu, name, "gemv", index, runs, cus=cus, spec=spec)
+    _run(emu, name, mode, index, runs, cus=cus, spec=spec)
 
 
 @pytest.mark.parametrize("batch", [1, 4])
@@ -338,10 +341,11 @@ def test_spec_runs_bf16_1024_chunks_many_rounds(emu, spec):
 
 
 def test_spec_runs_bf16_64k_chunks_across_chunk_boundaries(emu):
-    # 6 chunks of 65536 on a 2-CU grid: rounds of a workgroup cross from one
-    # large chunk into the next.
+    # 6 chunks of 65536 on a 2-CU grid, forced into speculative runs (such
+    # chunks decode chunk by chunk unless forced): rounds of a workgroup
+    # cross from one large chunk into the next.
     W = workloads.bf16_normal((24, 16384), 22, 0.02, outlier_frac=1e-3)
-    _bf16(emu, "sp64k", W, 65536, cus=2)
+    _bf16(emu, "sp64k", W, 65536, cus=2, spec="1")
 
 
 def test_spec_runs_several_tensors_in_one_launch(emu):
@@ -365,7 +369,14 @@ def test_spec_runs_every_guess_wrong(emu):
     # rests on the re-decodes from the predecessors' ends.
     rng = np.random.default_rng(26)
     _u8(emu, "sp_guess1024", rng.integers(0, 8, 1024 * 40), 1024, cus=2)
-    _u8(emu, "sp_guess64k", rng.integers(0, 8, 65536 + 30000), 65536, cus=2)
+    _u8(emu, "sp_guess64k", rng.integers(0, 8, 65536 + 30000), 65536, cus=2, spec="1")
+
+
+def test_whole_workgroup_chunks_every_guess_wrong(emu):
+    # The same on the chunk-by-chunk path of chunks that take a whole
+    # workgroup (interleaved slots, one record barrier per check pass).
+    rng = np.random.default_rng(26)
+    _u8(emu, "ww_guess64k", rng.integers(0, 8, 65536 + 30000), 65536, cus=2)
 
 
 def test_spec_runs_escape_blocks_beyond_the_lds_share(emu):
@@ -375,7 +386,7 @@ def test_spec_runs_escape_blocks_beyond_the_lds_share(emu):
 @pytest.mark.parametrize("batch", [1, 4])
 def test_spec_runs_gemv(emu, batch):
     _gemv(emu, "sp_gemv1024_b%d" % batch, 128, 2048, 1024, batch, 28, cus=2)
-    _gemv(emu, "sp_gemv32k_b%d" % batch, 70, 1000, 32768, batch, 29, cus=2)
+    _gemv(emu, "sp_gemv32k_b%d" % batch, 70, 1000, 32768, batch, 29, cus=2, spec="1")
 
 
 def test_spec_runs_sliced_stream(emu):
@@ -458,3 +469,20 @@ def test_spec_runs_chunks_out_of_order_and_empty(emu):
     nb = np.array(enc.chunk_nbytes, np.int32)
     nb[9] = 0
     _malformed(emu, "sp_empty", _Enc(enc, chunk_nbytes=nb))
+
+
+# Fused decode -> GEMM on the matrix cores (speculative runs, pieces of a
+# round written to LDS as bf16, 16-row tiles summed across waves when the
+# tile changes): several x rows, rows of W longer and shorter than a piece's
+# padding threshold, a last 32-column slice cut short (cols % 32 != 0), tiles
+# that continue across rounds and workgroups (2 CUs), and 64Ki-symbol chunks.
+
+@pytest.mark.parametrize("rows,cols,chunk,n_x", [
+    (70, 1024, 1024, 5),
+    (40, 5120, 4096, 16),
+    (300, 200, 1024, 8),
+    (24, 16384, 65536, 3),
+])
+def test_fused_gemm(emu, rows, cols, chunk, n_x):
+    _gemv(emu, "gemm_%d_%d_%d_%d" % (rows, cols, chunk, n_x), rows, cols, chunk, n_x, 40 + n_x,
+          cus=2, mode="gemm")
