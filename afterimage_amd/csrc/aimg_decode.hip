@@ -129,8 +129,10 @@ enum Mode : int {
     kModeGemv = 2,  // y += W x with W decoded on the fly and never written
     kModeGemv1 = 3, // kModeGemv for one x vector (batch 1)
     kModeIndex = 4, // the segment index: each segment's first boundary and codewords
-    kModeGemm = 5,  // Y += X W^T for up to 16 rows of X, W decoded on the fly (MFMA)
+    kModeGemm = 5,      // Y += X W^T for up to 16 rows of X, W decoded on the fly (MFMA)
+    kModeGemmRows = 6,  // kModeGemm for rows of more than kGemmPieceMaxCols columns
 };
+constexpr bool is_gemm(int mode) { return mode == kModeGemm || mode == kModeGemmRows; }
 // Modes that combine the exponents with sign/mantissa bytes.
 constexpr bool needs_sm(int mode) { return mode != kModeU8 && mode != kModeIndex; }
 // Job::ib of a chunk decoded without the index.
@@ -846,7 +848,7 @@ __device__ __forceinline__ void store_one(const DevTensor& T, const GemvArgs& G,
         static_cast<uint8_t*>(T.out)[el] = static_cast<uint8_t>(e);
     } else if (kMode == kModeBf16) {
         static_cast<uint16_t*>(T.out)[el] = bf16_one(T.sm[el], e);
-    } else if (kMode == kModeGemv || kMode == kModeGemv1 || kMode == kModeGemm) {
+    } else if (kMode == kModeGemv || kMode == kModeGemv1 || is_gemm(kMode)) {
         const float w = bf16_to_f32(bf16_one(T.sm[el], e));
         const uint32_t row = static_cast<uint32_t>(el / G.cols);
         const uint32_t col = static_cast<uint32_t>(el - static_cast<int64_t>(row) * G.cols);
@@ -860,7 +862,7 @@ __device__ __forceinline__ void store_one(const DevTensor& T, const GemvArgs& G,
 // (groups k * tpc + i of the round), requested ahead of use.
 template <int kMode>
 struct SmBatch {
-    uint2 v[needs_sm(kMode) ? kSmAhead : 1];
+    uint2 v[needs_sm(kMode) && kMode != kModeGemmRows ? kSmAhead : 1];
 };
 
 // Buffer loads (zero past the tensor's last byte), so the batch needs no
@@ -870,7 +872,8 @@ template <int kMode, int kGroup>
 // without reading memory).
 __device__ __forceinline__ void sm_issue(SmBatch<kMode>& B, const DevTensor& T, int64_t a0,
                                          uint32_t i, uint32_t tpc, uint32_t limit = 0xFFFFFFFFu) {
-    if (!needs_sm(kMode) || kGroup == 1) return;
+    // (kModeGemmRows reads them where its matrix tiles want them.)
+    if (!needs_sm(kMode) || kMode == kModeGemmRows || kGroup == 1) return;
     const uint32_t n = static_cast<uint32_t>(T.n_symbols);
     const __amdgpu_buffer_rsrc_t rs = buffer_of(T.sm, n < limit ? n : limit);
     const uint32_t v0 = static_cast<uint32_t>(a0) + i * kGroup;
@@ -1081,57 +1084,85 @@ __device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch],
 }
 
 // ---------------------------------------------------------------------------
-// Fused decode -> GEMM (kModeGemm, whole-workgroup rounds): Y[t][r] +=
-// sum_c X[t][c] W[r][c] for t < G.batch <= 16, on v_mfma_f32_16x16x32_bf16.
-// One MFMA takes a 16 x 32 tile of X (A: lane l holds X[l & 15][8 (l >> 4)
-// .. + 7]) and the 32 x 16 tile of W^T over the same 32 columns and 16 rows
-// of W (B: lane l holds W[row l & 15][the same 8 columns]) and adds to a 16 x
-// 16 tile of Y^T (D: lane l holds Y[4 (l >> 4) + k][row l & 15], k < 4).
-// A round's weights are in natural order, a row of W at a time, while the
-// B operand wants 16 rows at the same columns: each piece of 4 store steps
-// (2048 groups) is written to LDS as bf16 (with one padding group per row,
-// so that the 16 rows a read meets fall in different banks), and the waves
-// take the 32-column slices of each 16-row tile of W the piece touches,
-// X from global memory (L2) each time. Every wave keeps its partial D of the
-// current 16-row tile (rows 16 tile ..) in registers across pieces and
-// rounds; when the tile changes, the waves' partials are summed in LDS and
-// added to Y with one atomic per (row, x row).
+// Fused decode -> GEMM (kModeGemm, kModeGemmRows; whole-workgroup rounds):
+// Y[t][r] += sum_c X[t][c] W[r][c] for t < G.batch <= 16, on
+// v_mfma_f32_16x16x32_bf16. One MFMA takes a 16 x 32 tile of X (A: lane l
+// holds X[l & 15][8 (l >> 4) .. + 7]) and the 32 x 16 tile of W^T over the
+// same 32 columns and 16 rows of W (B: lane l holds W[row l & 15][the same 8
+// columns]) and adds to a 16 x 16 tile of Y^T (D: lane l holds Y[4 (l >> 4)
+// + k][row l & 15], k < 4). A round's weights are in natural order, a row of
+// W after another, while the B operand wants 16 rows at the same columns;
+// the waves take the 32-column slices of each 16-row tile of W the round
+// touches, X from L2, and X is read once per slice for the rows of the tile
+// the pass holds. Two ways to get there:
+// - kModeGemm (rows of up to 8192 columns): each piece of 4 store steps
+//   (2048 groups) is written to LDS as bf16 (sign/mantissa bytes requested
+//   during the decode, one padding group per row so that the 16 rows a read
+//   meets fall in different banks), then read as B operands: a pass per
+//   piece, which holds 2 to 16 rows of W.
+// - kModeGemmRows (longer rows, of which a piece holds one or two): one pass
+//   per round, each lane reading its group's exponents from the stage and
+//   their sign/mantissa bytes from memory (on the 5120x17408 layer, 8 rows of
+//   x: 258 us against 379 us in pieces; on the 151936x5120 lm_head, 1157 us
+//   against 990 us).
+// Every wave keeps its partial D of the current 16-row tile in registers
+// across passes and rounds; the waves' partials of a complete tile are summed
+// in LDS and added to Y with one atomic per (row, x row).
 // ---------------------------------------------------------------------------
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kGemmPieceSteps = 4;                        // store steps a piece holds
+constexpr uint32_t kNoTile = 0xFFFFFFFFu;
+constexpr uint32_t kGemmUnroll = 4;  // slices whose loads go out together
+// Rows of more columns than this take kModeGemmRows.
+constexpr int64_t kGemmPieceMaxCols = 8192;
+constexpr uint32_t kGemmPieceSteps = 4;  // store steps a piece holds
 constexpr uint32_t kGemmPieceGroups = kGemmPieceSteps * kThreads;
 // Padding groups of a piece: one per row it touches, for rows of 64 groups
 // or more (a row of fewer takes none: the reads then meet bank conflicts).
 constexpr uint32_t kGemmPadMinGroups = 64;
 constexpr uint32_t kGemmPieceBytes = 16 * (kGemmPieceGroups + kGemmPieceGroups / kGemmPadMinGroups + 2);
-// The cross-wave sum of the partial tiles, after the piece in the stage.
+// The cross-wave sum of the partial tiles, after a piece in the stage.
 constexpr uint32_t kGemmRedOffset = (kGemmPieceBytes + 255) / 256 * 256;
 constexpr uint32_t kGemmRedBytes = kWaves * 64 * 16;
-constexpr uint32_t kNoTile = 0xFFFFFFFFu;
-constexpr uint32_t kGemmUnroll = 4;  // slices whose loads go out together
 
 struct GemmAcc {
-    f32x4_t d;      // this wave's partial sums of 16-row tile `tile`
-    uint32_t tile;  // kNoTile: none
+    f32x4_t d;       // this wave's partial sums of 16-row tile `tile`
+    f32x4_t dp;      // those of tile `ptile`, complete, not yet added to Y
+    uint32_t tile;   // kNoTile: none
+    uint32_t ptile;  // kNoTile: none
 };
 
 __device__ __forceinline__ void gemm_acc_init(GemmAcc& A) {
     A.d = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    A.dp = A.d;
     A.tile = kNoTile;
+    A.ptile = kNoTile;
 }
 
-// The waves' partial sums of the current tile to Y; every thread calls it
-// (it holds barriers). `stage`: at least kGemmRedOffset + kGemmRedBytes bytes
-// that no thread reads meanwhile.
-__device__ __forceinline__ void gemm_flush(GemmAcc& A, const GemvArgs& G, uint8_t* stage) {
-    if (A.tile == kNoTile) return;
+// Partial sums d of tile `tile`, this wave's alone, to Y (one atomic per
+// entry; rows no weight of the wave met hold exactly zero and are skipped).
+__device__ __forceinline__ void gemm_add_wave(const f32x4_t& d, uint32_t tile, const GemvArgs& G) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row = 16 * tile + (lane & 15u);
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+        const uint32_t t = 4 * (lane >> 4) + k;
+        if (t < static_cast<uint32_t>(G.batch) && row < G.rows && d[k] != 0.0f)
+            atomicAdd(G.y + static_cast<int64_t>(t) * G.rows + row, d[k]);
+    }
+}
+
+// The waves' partial sums d of tile `tile`, summed in LDS, to Y; every
+// thread calls it (it holds barriers), with the stage's kGemmRedBytes bytes
+// from kGemmRedOffset free.
+__device__ __forceinline__ void gemm_add_block(const f32x4_t& d, uint32_t tile, const GemvArgs& G,
+                                               uint8_t* stage) {
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, w = tid >> 6;
     f32x4_t* const red = reinterpret_cast<f32x4_t*>(stage + kGemmRedOffset);
-    red[w * 64 + lane] = A.d;
+    red[w * 64 + lane] = d;
     __syncthreads();
     if (tid < 256) {
         // Entry k of lane l2 of every wave: Y[4 (l2 >> 4) + k][16 tile + (l2 & 15)].
@@ -1141,22 +1172,29 @@ __device__ __forceinline__ void gemm_flush(GemmAcc& A, const GemvArgs& G, uint8_
 #pragma unroll
         for (uint32_t v = 0; v < static_cast<uint32_t>(kWaves); ++v) sum += f[v * 256];
         const uint32_t t = 4 * (l2 >> 4) + k;
-        const uint32_t row = 16 * A.tile + (l2 & 15u);
-        // Rows no weight of this workgroup met sum to exactly zero.
+        const uint32_t row = 16 * tile + (l2 & 15u);
         if (t < static_cast<uint32_t>(G.batch) && row < G.rows && sum != 0.0f)
             atomicAdd(G.y + static_cast<int64_t>(t) * G.rows + row, sum);
     }
     __syncthreads();  // the sums are read before the area is written again
+}
+
+// The tile the wave's partial sums belong to, when the workgroup's elements
+// end (every thread calls it).
+__device__ __forceinline__ void gemm_finish(GemmAcc& A, const GemvArgs& G, uint8_t* stage) {
+    if (A.ptile != kNoTile) gemm_add_block(A.dp, A.ptile, G, stage);
+    if (A.tile != kNoTile) gemm_add_block(A.d, A.tile, G, stage);
     gemm_acc_init(A);
 }
 
-// One round's groups [0, nfull) (W groups a0 / 8 ...), their sign/mantissa
-// bytes in sm (group k * kThreads + tid at k), exponents in the stage. The
-// stage is overwritten but for the bytes past the round's groups, which the
-// caller carries into the next round: those are put back.
-__device__ __forceinline__ void gemm_round(const uint2 (&sm)[kStoreBatch], const GemvArgs& G,
-                                           uint8_t* stage, uint32_t a0, uint32_t nfull, uint32_t tid,
-                                           GemmAcc& A) {
+// kModeGemm: one round's groups [0, nfull) (W groups a0 / 8 ...), their
+// sign/mantissa bytes in sm (group k * kThreads + tid at k), exponents in the
+// stage, written to LDS as bf16 a piece of kGemmPieceSteps store steps at a
+// time. The stage is overwritten but for the bytes past the round's groups,
+// which the caller carries into the next round: those are put back.
+__device__ __forceinline__ void gemm_round_pieces(const uint2 (&sm)[kStoreBatch], const GemvArgs& G,
+                                                  uint8_t* stage, uint32_t a0, uint32_t nfull,
+                                                  uint32_t tid, GemmAcc& A) {
     const uint32_t cols = G.cols;
     const uint32_t cg = cols / 8;  // groups a row
     const uint32_t lane = tid & 63u, w = tid >> 6;
@@ -1200,7 +1238,8 @@ __device__ __forceinline__ void gemm_round(const uint2 (&sm)[kStoreBatch], const
         __syncthreads();
         for (uint32_t t = rb / 16; t <= re / 16; ++t) {
             if (t != A.tile) {
-                gemm_flush(A, G, stage);
+                if (A.tile != kNoTile) gemm_add_block(A.d, A.tile, G, stage);
+                A.d = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
                 A.tile = t;
             }
             const uint32_t row = 16 * t + n;
@@ -1238,6 +1277,102 @@ __device__ __forceinline__ void gemm_round(const uint2 (&sm)[kStoreBatch], const
     __syncthreads();
 }
 
+// kModeGemmRows: one round's groups [0, nfull) (W groups a0 / 8 ...),
+// exponents in the stage, read where the B operand wants them, with their
+// sign/mantissa bytes from memory: X is read once per slice of the round
+// (pieces would read it once per piece, and a piece of long rows holds one
+// or two). Bytes past the round's groups (the partial group carried into the
+// next round) are kept.
+__device__ __forceinline__ void gemm_round_rows(const DevTensor& T, const GemvArgs& G, uint8_t* stage,
+                                                uint32_t a0, uint32_t nfull, uint32_t tid, GemmAcc& A) {
+    const uint32_t cols = G.cols;
+    const uint32_t cg = cols / 8;  // groups a row
+    const uint32_t lane = tid & 63u, w = tid >> 6;
+    const uint32_t nb = static_cast<uint32_t>(G.batch);
+    const uint32_t q = lane >> 4, n = lane & 15u;
+    const uint32_t g0 = a0 / 8, ge = g0 + nfull;
+    const uint32_t ns = (cg + 3) / 4;  // 32-column slices a row
+    const __amdgpu_buffer_rsrc_t xr = buffer_of(G.x, nb * cols * 2u);
+    const __amdgpu_buffer_rsrc_t sr = buffer_of(T.sm, static_cast<uint32_t>(T.n_symbols));
+    if (nfull != 0) {
+        const uint32_t t_lo = g0 / cg / 16, t_hi = (ge - 1) / cg / 16;
+        for (uint32_t t = t_lo; t <= t_hi; ++t) {
+            if (t != A.tile) {
+                if (A.tile != kNoTile) {
+                    // The wave's tile is complete: it waits for the block sum
+                    // at the round's end (one waiting already: added now).
+                    if (A.ptile != kNoTile) gemm_add_wave(A.dp, A.ptile, G);
+                    A.dp = A.d;
+                    A.ptile = A.tile;
+                }
+                A.d = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                A.tile = t;
+            }
+            const uint32_t row = 16 * t + n;
+            // Slices s = w, w + kWaves, ... of this tile, kGemmUnroll at a
+            // time; the loads of the next kGemmUnroll go out before this
+            // step's products (X and the sign/mantissa bytes come from L2).
+            auto issue = [&](uint32_t s0, uint4 (&xa)[kGemmUnroll], uint2 (&sm)[kGemmUnroll],
+                             uint2 (&ex)[kGemmUnroll]) {
+#pragma unroll
+                for (uint32_t u = 0; u < kGemmUnroll; ++u) {
+                    const uint32_t sl = s0 + u * kWaves;
+                    const uint32_t j = 4 * sl + q;  // the lane's column group
+                    const bool col_ok = sl < ns && j < cg;
+                    // X row n (zero past the batch or the row: out of the buffer's range).
+                    const uint32_t xo = col_ok && n < nb ? n * cols * 2u + 16u * j : 0xFFFFFFF0u;
+                    const auto xv = __builtin_amdgcn_raw_buffer_load_b128(xr, xo, 0, 0);
+                    xa[u] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+                    const uint32_t gv = row * cg + j;  // W group of this lane (rows * cols < 2^31)
+                    const bool ok = col_ok && gv >= g0 && gv < ge;
+                    const auto sv = __builtin_amdgcn_raw_buffer_load_b64(sr, ok ? 8u * gv : 0xFFFFFFF8u, 0, 0);
+                    sm[u] = make_uint2(sv[0], sv[1]);
+                    const uint2 e = *reinterpret_cast<const uint2*>(stage + (ok ? 8u * (gv - g0) : 0u));
+                    ex[u] = ok ? e : make_uint2(0u, 0u);
+                }
+            };
+            for (uint32_t s0 = w; s0 < ns; s0 += kGemmUnroll * kWaves) {
+                uint4 xa[kGemmUnroll];
+                uint2 sm[kGemmUnroll], ex[kGemmUnroll];
+                issue(s0, xa, sm, ex);
+#pragma unroll
+                for (uint32_t u = 0; u < kGemmUnroll; ++u) {
+                    uint4 wb;
+                    wb.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[u].x, ex[u].x);
+                    wb.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[u].x, ex[u].x);
+                    wb.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[u].y, ex[u].y);
+                    wb.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[u].y, ex[u].y);
+                    A.d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[u]),
+                                                                  __builtin_bit_cast(bf16x8_t, wb),
+                                                                  A.d, 0, 0, 0);
+                }
+            }
+        }
+    }
+    // Complete tiles to Y, summed over the waves in the stage once every
+    // wave is done with it: the one waiting, and the current one when the
+    // next round (which starts at group ge) begins past it.
+    const bool done_cur = A.tile != kNoTile && ge / cg >= 16 * (A.tile + 1);
+    if (A.ptile == kNoTile && !done_cur) return;
+    const uint2 keep0 = reinterpret_cast<const uint2*>(stage + nfull * 8)[0];
+    const uint2 keep1 = reinterpret_cast<const uint2*>(stage + nfull * 8)[1];
+    __syncthreads();
+    if (A.ptile != kNoTile) {
+        gemm_add_block(A.dp, A.ptile, G, stage);
+        A.ptile = kNoTile;
+    }
+    if (done_cur) {
+        gemm_add_block(A.d, A.tile, G, stage);
+        A.d = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        A.tile = kNoTile;
+    }
+    if (tid == 0) {
+        reinterpret_cast<uint2*>(stage + nfull * 8)[0] = keep0;
+        reinterpret_cast<uint2*>(stage + nfull * 8)[1] = keep1;
+    }
+    __syncthreads();
+}
+
 // Vector groups [0, nfull) of the staged round to output elements a0...;
 // thread i of a sub-group of tpc takes groups i, i + tpc, ... kWhole: the
 // sub-group is the whole workgroup, whose stage area is readable for every
@@ -1250,6 +1385,13 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
                                             const GemvArgs& G, const uint8_t* stage, int64_t a0,
                                             uint32_t nfull, uint32_t i, uint32_t tpc,
                                             uint32_t skip = 0, GemmAcc* gacc = nullptr) {
+    if constexpr (kMode == kModeGemmRows) {
+        // Whole-workgroup rounds without skipped elements only (the
+        // speculative runs).
+        static_assert(kWhole && kGroup == 8, "the fused GEMM takes whole-workgroup rounds");
+        gemm_round_rows(T, G, const_cast<uint8_t*>(stage), static_cast<uint32_t>(a0), nfull, i, *gacc);
+        return;
+    }
     if (kGroup == 1) {
         for (uint32_t v = i; v < nfull; v += tpc) store_one<kMode>(T, G, a0 + v, stage[v]);
         return;
@@ -1294,10 +1436,8 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
         for (uint32_t k = kSmAhead; k < kStoreBatch; ++k) sm[k] = make_uint2(0u, 0u);
     }
     if constexpr (kMode == kModeGemm) {
-        // Whole-workgroup rounds without skipped elements only (the
-        // speculative runs).
         static_assert(kWhole && kGroup == 8, "the fused GEMM takes whole-workgroup rounds");
-        gemm_round(sm, G, const_cast<uint8_t*>(stage), static_cast<uint32_t>(a0), nfull, i, *gacc);
+        gemm_round_pieces(sm, G, const_cast<uint8_t*>(stage), static_cast<uint32_t>(a0), nfull, i, *gacc);
         return;
     }
     // All staged exponents are read (from always valid offsets) before any
@@ -3071,7 +3211,7 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
         // codeword (exact on any input).
         run_fallback<kMode>(tb, args, T, fall_from / cs, cb, fall_from);
     }
-    if constexpr (kMode == kModeGemm) gemm_flush(gacc, args.gemv, stage);
+    if constexpr (is_gemm(kMode)) gemm_finish(gacc, args.gemv, stage);
     __syncthreads();  // LDS is free for the next piece
 }
 
@@ -3349,7 +3489,7 @@ int launch(const aimg_tensor* ts, int n, const GemvArgs& gemv, bool vec_ok, void
     const bool no_spec = force_spec != nullptr && force_spec[0] == '0';
     const bool spec_all = force_spec != nullptr && force_spec[0] == '1';
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if constexpr (kMode == kModeGemm) {
+    if constexpr (is_gemm(kMode)) {
         // The fused GEMM runs in speculative segment runs only, whatever the
         // chunk size (an index is not used).
         for (int i = 0; i < n; ++i) {
@@ -3561,5 +3701,6 @@ extern "C" int aimg_decode_gemm_bf16(const aimg_tensor* t, int64_t rows, int64_t
                     "fused GEMM: needs cols % 8 == 0, a 16-byte aligned x and n_x * cols * 2 below 2^32");
     const aimg::GemvArgs g{static_cast<const uint16_t*>(x), y, static_cast<uint32_t>(rows),
                            static_cast<uint32_t>(cols), n_x, 0u, 0u};
+    if (cols > aimg::kGemmPieceMaxCols) return aimg::launch<aimg::kModeGemmRows>(t, 1, g, true, stream);
     return aimg::launch<aimg::kModeGemm>(t, 1, g, true, stream);
 }

@@ -13,9 +13,11 @@ ring run. The same launches over three copies of the layer in turn
 The default run ("suite") adds, as extra keys of the same line, each timed in
 this run: the layer at the reference store's default 1024-symbol chunks; the
 layer with a prebuilt segment index (the compressed-resident tier, with its
-build time); config 1 (1024x3072); config 3 (a 14B-class block in one
-launch); config 4 (40 streamed blocks through a 2-slot ring); config 5 (the
-fused decode->GEMV at batch 1 and 4, both chunk sizes). Prints one JSON line.
+build time); a small 1024x3072 layer; a 14B-class block in one launch; 40
+streamed blocks through a 2-slot ring; the fused decode->GEMV at batch 1 and
+4 and the fused decode->GEMM at 8 and 16 rows of x, at both chunk sizes; and
+the 151936x5120 lm_head at 8 tokens, blocked against fused. Prints one JSON
+line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
                     [--workload suite|layer|block|gemv|ring|api|head|resync]
@@ -243,14 +245,16 @@ def _bench_gemv(args) -> int:
 
 def _gemv(args, W=None, layer=None) -> dict | None:
     """Fused decode->GEMV: y[b] = W x[b] for the 5120x17408 weight, W decoded
-    in the kernel and never written. One step = zero y + one launch; the
+    in the kernel and never written (batch 1..4; 5..16 rows of x take the
+    fused GEMM on the matrix cores). One step = zero y + one launch; the
     roofline figures come from the launches alone, timed in a second loop.
     With --index the layer's segment index is built first (the
-    compressed-resident tier); without it the GEMV decodes speculatively, as
-    decompress_matvec_gpu does. Returns the JSON record, or None when y is
-    outside the tolerance."""
+    compressed-resident tier; the GEMM ignores it); without it the product
+    decodes speculatively, as decompress_matvec_gpu does. Returns the JSON
+    record, or None when y is outside the tolerance."""
     from afterimage_amd import workloads
-    from afterimage_amd.runtime.device import DeviceTensor, decode_gemv
+    from afterimage_amd.runtime.device import GEMV_MAX_BATCH, DeviceTensor, decode_gemm
+    from afterimage_amd.runtime.device import decode_gemv as _gemv_call
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -264,6 +268,8 @@ def _gemv(args, W=None, layer=None) -> dict | None:
     if getattr(args, "index", False):
         t.build_index()  # the resident layer's segment index, built once
     y = torch.zeros((b, rows), dtype=torch.float32, device=dev)
+    decode_gemv = _gemv_call if b <= GEMV_MAX_BATCH else decode_gemm
+    kind = "GEMV" if b <= GEMV_MAX_BATCH else "GEMM"
 
     def step():
         y.zero_()
@@ -276,7 +282,7 @@ def _gemv(args, W=None, layer=None) -> dict | None:
     yb = y.to(torch.bfloat16).float()
     ok = bool(((yb - ref).abs() <= 1e-3 + 1e-2 * ref.abs()).all())
     if not ok:
-        print("fused GEMV differs from decode-then-matmul beyond rel 1e-2 / abs 1e-3",
+        print("fused %s differs from decode-then-matmul beyond rel 1e-2 / abs 1e-3" % kind,
               file=sys.stderr)
         return None
     stream = torch.cuda.current_stream(dev)
@@ -323,7 +329,7 @@ def _gemv(args, W=None, layer=None) -> dict | None:
     algo_bytes = (chunk_bytes + 8 * enc.n_chunks + n + (5 * 4096 + 256) + 2 * b * cols
                   + 8 * b * rows + t.index_bytes_read)
     rec = {
-        "metric": "fused decode->GEMV weight GB/s (bf16 bytes consumed per second)",
+        "metric": "fused decode->%s weight GB/s (bf16 bytes consumed per second)" % kind,
         "value": round(2 * n * args.steps / wall / 1e9, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -335,9 +341,9 @@ def _gemv(args, W=None, layer=None) -> dict | None:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "fused decode->GEMV, 5120x17408 bf16 weight (seed 2, 0.1%% "
+        "config": {"workload": "fused decode->%s, 5120x17408 bf16 weight (seed 2, 0.1%% "
                                "outliers, %d-symbol chunks) x bf16 activation [%d, 17408] N(0,1) "
-                               "(seed 23), fp32 accumulate -> bf16" % (enc.chunk_size, b),
+                               "(seed 23), fp32 accumulate -> bf16" % (kind, enc.chunk_size, b),
                    "batch": b, "within_tolerance": ok, "tolerance": "rel 1e-2, abs 1e-3",
                    "flops_per_step": 2 * n * b, "chunk_size": enc.chunk_size,
                    "segment_index": t.index is not None},
@@ -359,21 +365,34 @@ def _gemv(args, W=None, layer=None) -> dict | None:
 
 
 def _bench_head(args) -> int:
+    rec = _head(args)
+    if rec is None:
+        return 1
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+def _head(args) -> dict | None:
     """The output projection of a 14B-class model (lm_head 151936x5120 bf16,
     resident compressed in HBM at the reference store's default 1024-symbol
     chunks) applied to x [1, tokens, 5120]. One step = one blocked forward
     as the reference's chunked head computes it: 8192-row blocks, each
-    decoded (through a segment index of its own) into one staging buffer and
-    multiplied by the GEMM library, outputs concatenated. Also timed: the
-    whole head decoded at once (through its segment index) then one
-    F.linear, the fused decode->GEMV for at most 4 tokens, and F.linear on
-    the already-decoded weight alone."""
+    decoded into one staging buffer and multiplied by the GEMM library,
+    outputs concatenated (no index unless --index). Also timed: the fused
+    product that decodes no weight to memory (GEMV up to 4 tokens, GEMM on
+    the matrix cores for 5..16), both as its kernel alone and as the API
+    call decompress_linear_gpu(fused=True) on the resident layer; the whole
+    head decoded at once then one F.linear; and F.linear on the decoded
+    weight alone. Returns the record, or None when a check fails."""
     import torch.nn.functional as F
 
     from afterimage_amd import workloads
-    from afterimage_amd.runtime.compressed_store import compress_layer
-    from afterimage_amd.runtime.device import (GEMV_MAX_BATCH, DeviceTensor, decode_bf16,
-                                               decode_gemv, decode_linear, row_blocks)
+    from afterimage_amd.runtime.compressed_store import (CompressedLayer, compress_layer,
+                                                         decompress_linear_gpu)
+    from afterimage_amd.runtime.device import (GEMM_MAX_ROWS, GEMV_MAX_BATCH, DeviceTensor,
+                                               decode_bf16, decode_gemm, decode_gemv,
+                                               decode_linear, row_blocks)
+    from afterimage_amd.runtime.huffman_chunked import ChunkedEncoded
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -385,7 +404,16 @@ def _bench_head(args) -> int:
          % (time.perf_counter() - t0, layer.encoded.n_chunks, layer.encoded.packed.nbytes / 1e6))
     enc = layer.encoded
     n = enc.n_symbols
-    t = DeviceTensor.from_encoded(enc, layer.sign_mantissa, dev).build_index()
+    t = DeviceTensor.from_encoded(enc, layer.sign_mantissa, dev)
+    if args.index:
+        t.build_index()
+    # The same layer with its arrays resident on the GPU, for the API call.
+    resident = CompressedLayer(
+        sign_mantissa=t.sign_mantissa, shape=layer.shape,
+        encoded=ChunkedEncoded(packed=t.packed, chunk_offsets=t.chunk_offsets,
+                               chunk_nbytes=t.chunk_nbytes, sym_lut=enc.sym_lut,
+                               len_lut=enc.len_lut, max_bits=enc.max_bits,
+                               chunk_size=enc.chunk_size, n_symbols=n, shape=enc.shape))
     g = np.random.default_rng(29)
     x = torch.from_numpy(g.standard_normal((1, tokens, cols), dtype=np.float32)) \
         .to(torch.bfloat16).to(dev)
@@ -394,7 +422,8 @@ def _bench_head(args) -> int:
     staging = torch.empty(need, dtype=torch.bfloat16, device=dev)
     whole = torch.empty(n, dtype=torch.bfloat16, device=dev)
     y_fused = torch.zeros((tokens, rows), dtype=torch.float32, device=dev)
-    fused_ok = tokens <= GEMV_MAX_BATCH
+    fused_ok = tokens <= GEMM_MAX_ROWS
+    fused_fn = decode_gemv if tokens <= GEMV_MAX_BATCH else decode_gemm
 
     def blocked():
         return decode_linear(t, x, rows, cols, slice_rows, staging=staging)
@@ -405,7 +434,10 @@ def _bench_head(args) -> int:
 
     def fused():
         y_fused.zero_()
-        decode_gemv(t, x.reshape(tokens, cols), rows, cols, y_fused)
+        fused_fn(t, x.reshape(tokens, cols), rows, cols, y_fused)
+
+    def api():
+        return decompress_linear_gpu(resident, x, fused=True)
 
     # Parity before timing: the decoded head is the original bit for bit,
     # and the blocked forward is the reference's blocked F.linear calls on
@@ -425,14 +457,16 @@ def _bench_head(args) -> int:
     del ref, buf, flat
     if not bit_exact:
         print("decoded head differs from the original weights", file=sys.stderr)
-        return 1
+        return None
     fused_within = None
     if fused_ok:
         fused()
         yf = torch.matmul(x.reshape(tokens, cols).float(), Wd.float().t().contiguous())
         yb = y_fused.to(torch.bfloat16).float()
-        fused_within = bool(((yb - yf).abs() <= 1e-3 + 1e-2 * yf.abs()).all())
-        del yf, yb
+        ya = api().reshape(tokens, rows).float()
+        fused_within = bool(((yb - yf).abs() <= 1e-3 + 1e-2 * yf.abs()).all()) and \
+            bool(((ya - yf).abs() <= 1e-3 + 1e-2 * yf.abs()).all())
+        del yf, yb, ya
     del Wd
     stream = torch.cuda.current_stream(dev)
 
@@ -456,7 +490,8 @@ def _bench_head(args) -> int:
     decode_s = timed(lambda: decode_bf16([t], [whole]))
     gemm_s = timed(lambda: F.linear(x, whole.view(rows, cols)))
     fused_s = timed(fused) if fused_ok else None
-    rec = {
+    api_s = timed(api) if fused_ok else None
+    return {
         "metric": "blocked lm_head forward: decompressed BF16 GB/s (decode + GEMM per block)",
         "value": round(2 * n / blocked_s / 1e9, 2),
         "unit": "GB/s",
@@ -472,25 +507,29 @@ def _bench_head(args) -> int:
         "data": "synthetic",
         "config": {"workload": "lm_head 151936x5120 bf16 (seed 5, 0.1%% outliers, %d-symbol "
                                "chunks) resident compressed, x [1, %d, 5120] bf16 N(0,1) "
-                               "(seed 29), %d-row blocks" % (enc.chunk_size, tokens, slice_rows),
+                               "(seed 29), %d-row blocks, %s"
+                               % (enc.chunk_size, tokens, slice_rows,
+                                  WITH_INDEX if args.index else NO_INDEX),
                    "tokens": tokens, "slice_rows": slice_rows, "chunk_size": enc.chunk_size,
                    "blocks": len(blocks), "staging_bytes": 2 * need,
+                   "segment_index": t.index is not None,
                    "weights_bit_exact": bit_exact,
                    "blocked_equals_reference_forward": same_as_reference,
                    "fused_within_tolerance": fused_within,
+                   "fused_kind": ("GEMV" if tokens <= GEMV_MAX_BATCH else "GEMM (MFMA)")
+                   if fused_ok else None,
                    "tolerance": "fused: rel 1e-2, abs 1e-3 against the fp32 product"},
         "paths_us": {
             "blocked_decode_and_gemm": round(blocked_s * 1e6, 1),
             "whole_decode_then_gemm": round(unblocked_s * 1e6, 1),
             "whole_decode_alone": round(decode_s * 1e6, 1),
             "gemm_alone_on_decoded_weight": round(gemm_s * 1e6, 1),
-            "fused_decode_gemv": None if fused_s is None else round(fused_s * 1e6, 1),
+            "fused_kernel": None if fused_s is None else round(fused_s * 1e6, 1),
+            "fused_api_decompress_linear_gpu": None if api_s is None else round(api_s * 1e6, 1),
         },
         "roofline": None,
         "cpu_baseline": None,
     }
-    print(json.dumps(rec), flush=True)
-    return 0
 
 
 def _bench_resync(args) -> int:
@@ -633,7 +672,7 @@ def main() -> int:
                          "with and without the index")
     ap.add_argument("--layers", type=int, default=40, help="ring: layers streamed per step")
     ap.add_argument("--batch", type=int, default=1,
-                    help="gemv: batch (1..4); head: tokens of x")
+                    help="gemv: rows of x (1..4: fused GEMV; 5..16: fused GEMM); head: tokens of x")
     ap.add_argument("--slice-rows", type=int, default=8192, help="head: rows per block")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--index", action="store_true",
@@ -875,7 +914,7 @@ def _single(args) -> int:
 
 
 def _suite(args) -> int:
-    """The default run: the headline (config 2, the 5120x17408 layer in
+    """The default run: the headline (the 5120x17408 layer in
     65536-symbol chunks decoded without an index, as decompress_layer_gpu and
     the streamed ring decode it) as value and roofline, and the other
     configurations as extra keys, each timed in this same run."""
@@ -922,43 +961,66 @@ def _suite(args) -> int:
                         "per resident compressed tensor, for a tier that keeps tensors "
                         "compressed in HBM (the reference has none); build_us + kernel_us is "
                         "the one-shot cost")
-    # Config 1: the 1024x3072 layer at 4096-symbol chunks.
+    # A small layer: 1024x3072 at 4096-symbol chunks.
     Ws, small = workloads.small_layer(seed=1)
-    extra["config1_small_layer"] = dict(
+    extra["small_layer_1024x3072"] = dict(
         brief(_decode([("small", Ws, small)], short, args.warmup)),
         what="bf16 1024x3072, 4096-symbol chunks, one launch, no index (launch-bound)")
-    # Config 5: the fused decode->GEMV at batch 1 and 4, speculative decode
+    # The fused decode->GEMV at batch 1 and 4, speculative decode
     # (no index) as decompress_matvec_gpu runs it, at both chunk sizes.
     gargs = types.SimpleNamespace(steps=short, warmup=args.warmup, index=False, chunk_size=65536)
     for b in (1, 4):
         gargs.batch = b
         g = _gemv(gargs, W, layer)
-        extra["config5_gemv_b%d" % b] = None if g is None else dict(
+        extra["gemv_b%d" % b] = None if g is None else dict(
             g["roofline"], within_tolerance=g["config"]["within_tolerance"],
             what="fused decode->GEMV, 5120x17408 x [%d, 17408], 65536-symbol chunks, no index; "
                  "frac: the exponent-byte decode's time over the GEMV's" % b)
-    l1024 = compress_layer(W, chunk_size=1024)
-    for b in (1, 4):
+    # The fused decode->GEMM (matrix cores) at speculative-verify widths.
+    for b in (8, 16):
         gargs.batch = b
-        gargs.chunk_size = 1024
-        g = _gemv(gargs, W, l1024)
-        extra["config5_gemv_b%d_chunk1024" % b] = None if g is None else dict(
+        g = _gemv(gargs, W, layer)
+        extra["gemm_t%d" % b] = None if g is None else dict(
             g["roofline"], within_tolerance=g["config"]["within_tolerance"],
-            what="the same at 1024-symbol chunks")
+            what="fused decode->GEMM, 5120x17408 x [%d, 17408], 65536-symbol chunks, no index; "
+                 "frac: the exponent-byte decode's time over the GEMM's" % b)
+    l1024 = compress_layer(W, chunk_size=1024)
+    gargs.chunk_size = 1024
+    for b in (1, 4, 8):
+        gargs.batch = b
+        g = _gemv(gargs, W, l1024)
+        extra[("gemv_b%d_chunk1024" if b <= 4 else "gemm_t%d_chunk1024") % b] = \
+            None if g is None else dict(g["roofline"],
+                                        within_tolerance=g["config"]["within_tolerance"],
+                                        what="the same at 1024-symbol chunks")
     del l1024
-    # Config 3: a 14B-class block in one launch, no index.
+    # The chunked lm_head at 8 tokens (a speculative-verify width), no index:
+    # the reference's blocked forward against the fused GEMM.
+    hargs = types.SimpleNamespace(slice_rows=8192, batch=8, chunk_size=1024, index=False,
+                                  steps=5, warmup=2)
+    h = _head(hargs)
+    extra["head_t8"] = None if h is None else dict(
+        paths_us=h["paths_us"], weights_bit_exact=h["config"]["weights_bit_exact"],
+        blocked_equals_reference_forward=h["config"]["blocked_equals_reference_forward"],
+        fused_within_tolerance=h["config"]["fused_within_tolerance"],
+        what="lm_head 151936x5120 bf16, 1024-symbol chunks, resident compressed, no index, "
+             "x [1, 8, 5120]: blocked decode + F.linear per 8192 rows (the reference's chunked "
+             "head) against the fused decode->GEMM (kernel alone, and through "
+             "decompress_linear_gpu(fused=True))")
+    torch.cuda.empty_cache()
+    # A 14B-class block in one launch, no index.
     t0 = time.perf_counter()
     blk3 = workloads.block_14b(seed=3)
     _log("block built in %.1fs" % (time.perf_counter() - t0))
-    extra["config3_block"] = dict(
+    extra["block_14b"] = dict(
         brief(_decode(blk3, short, args.warmup)),
         what="the 14B-class block (9 tensors, 5 codebooks, 65536-symbol chunks) in one launch, "
              "no index")
-    # Config 4: 40 streamed blocks through a 2-slot ring under 4 GiB.
+    # 40 streamed blocks through a 2-slot ring under 4 GiB.
     blk4 = workloads.block_14b(seed=4)
     rargs = types.SimpleNamespace(layers=40, steps=3, warmup=2)
     r = _ring(rargs, [blk3, blk4])
-    extra["config4_ring"] = None if r is None else {
+    extra["ring_40_blocks"] = None if r is None else {
         "layers_per_s": r["value"], "ms_per_40_layers": r["ms_per_step"],
         "decode_only_gbs": r["decode_only_gbs"], "h2d_pinned_gbs": r["h2d_pinned_gbs"],
         "h2d_bound_layers_per_s": r["h2d_bound_layers_per_s"], "bit_exact": r["config"]["bit_exact"],

@@ -61,7 +61,7 @@ def store_two_full_blocks(tmp_path_factory):
 
 
 def test_streamed_full_blocks_from_the_store_under_4gb(store_two_full_blocks):
-    """Config 4 at its real shapes: full 14B-class blocks read from the store
+    """The streamed ring at its real shapes: full 14B-class blocks read from the store
     straight into pinned buffers (CRC-32 checked), then streamed through a
     2-slot ring under a 4 GiB device budget for 6 layers; every tensor of
     every layer bit-exact against the seeded originals."""

@@ -260,7 +260,7 @@ def test_recombine_kernel_on_every_byte_pair_and_offsets():
 
 
 @pytest.mark.parametrize("misalign", [1, 3])
-def test_decode_from_store_views_config1(misalign):
+def test_decode_from_store_views_small_layer(misalign):
     """Config-1 layer from non-owning unaligned views, as read_many returns
     them (afterimage/runtime/binstore.py:115-133)."""
     from tests.store_views import store_views
