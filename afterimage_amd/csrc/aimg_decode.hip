@@ -1653,7 +1653,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(table + kEscOffset);
         const bool global_esc = hdr->n_esc_blocks > static_cast<uint32_t>(kLdsEscBlocks);
         __syncthreads();  // the previous item is done with LDS; its tile writes are visible
-        if (table != loaded) {
+        const bool reload = table != loaded;
+        if (reload) {
             loaded = table;
             load_table(table, tid, s_wsyms, s_wmeta, s_len, s_esc);
         }
@@ -1668,11 +1669,17 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         uint8_t* stage = s_stage + g * region;
         uint8_t* slot = stage + kLeadBytes + i_item * kSlotBytes;
 
-        if (i_item == 0) s_gval[g] = cur.nr;
-        __syncthreads();
+        // Rounds of the item: the most any of its chunks needs (a whole-workgroup
+        // chunk's own, without a barrier unless the table was just loaded).
         uint32_t NR = 0;
-        for (uint32_t k = 0; k < n_groups; ++k) NR = NR > s_gval[k] ? NR : s_gval[k];
-        NR = uniform(NR);
+        if (kLg == kLgThreads && !reload) {
+            NR = uniform(cur.nr);
+        } else {
+            if (i_item == 0) s_gval[g] = cur.nr;
+            __syncthreads();
+            for (uint32_t k = 0; k < n_groups; ++k) NR = NR > s_gval[k] ? NR : s_gval[k];
+            NR = uniform(NR);
+        }
 
         int64_t ob = 0;     // chunk-local symbols placed so far
         uint32_t lead = 0;  // placed symbols still staged at the front of the region
