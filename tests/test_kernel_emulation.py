@@ -199,6 +199,14 @@ def test_bf16_whole_workgroup_chunks(emu):
     _bf16(emu, "bf16_whole", W, 65536)
 
 
+def test_bf16_whole_workgroup_chunks_several_per_workgroup(emu):
+    # Seven 65536-symbol chunks on a 1-CU grid (2 workgroups): each workgroup
+    # goes from item to item, its next item's job prepared during the
+    # current one; a 1024-symbol tensor in the same launch (two tables).
+    W = workloads.bf16_normal((27, 16384), 13, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "bf16_whole_items", W, 65536, cus=1, spec="0")
+
+
 @full
 def test_bf16_two_round_64k_chunks_with_outliers(emu):
     W = workloads.bf16_normal((64, 17408), 2, 0.02, outlier_frac=1e-3)
