@@ -36,6 +36,7 @@
 // (LDS for the first 48 blocks, global memory beyond).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <cstdlib>
 #include <mutex>
@@ -163,6 +164,16 @@ struct LaunchArgs {
     // runs: a full grid, whose workgroups b and b + grid / 2 split a CU's share.
     int32_t strided;
     GemvArgs gemv;  // kModeGemv only (one tensor)
+    // Chunk by chunk, whole-workgroup chunks: the last n_split chunks (from
+    // chunk item split_first on) are split in two halves of their rounds.
+    // Items 0 .. n_split - 1 are their first halves, the grid's first items;
+    // then come the other chunks, then the second halves. Split chunk k hands
+    // over through record k of `handoff`, tagged with `tag`. n_split 0: no
+    // chunk is split.
+    int64_t split_first;
+    int64_t n_split;
+    uint64_t* handoff;
+    uint32_t tag;
 };
 
 // Read-only launch data that every thread of a workgroup reads at the same
@@ -597,6 +608,18 @@ struct Job {
     uint32_t lim;  // output symbols of the chunk
     uint32_t nr;   // rounds
     uint32_t ib;   // index build: the chunk's first segment, or kNoIndex
+    uint32_t r0;   // the item's rounds: r0 .. r1 - 1 of the chunk's
+    uint32_t r1;
+    int32_t half;  // kWholeChunk, or which half of a split chunk (LaunchArgs)
+    uint32_t slot; // a split chunk's handoff record
+};
+
+// Job::half.
+enum Half : int32_t {
+    kWholeChunk = 0,
+    kFirstHalf = 1,   // rounds 0 .. nr/2 - 1; hands its state over at the end
+    kSecondHalf = 2,  // rounds nr/2 .. nr - 1; takes the state over first
+    kNoHalf = 3,      // second half of a chunk of fewer than 2 rounds: nothing
 };
 
 // Index build: whether the plan step gave tensor T's index its chunk bases
@@ -612,8 +635,24 @@ __device__ __forceinline__ bool index_build_ready(const DevTensor& T) {
 // kLg > 0: every tensor of the launch has 1 << kLg threads per chunk.
 template <int kMode, uint32_t kLg>
 __device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, uint32_t tid) {
-    Job J{-1, 0u, kMaxSegBits, 0, 0u, 0u, 0u, 0u, kNoIndex};
+    Job J{-1, 0u, kMaxSegBits, 0, 0u, 0u, 0u, 0u, kNoIndex, 0u, 0u, kWholeChunk, 0u};
     if (item >= args.total_items) return J;
+    // Split chunk k (chunk item split_first + k): its first half is item k,
+    // its second half item split_first + n_split + k; the chunk items before
+    // split_first are items n_split .. split_first + n_split - 1.
+    if (args.n_split > 0) {
+        if (item < args.n_split) {
+            J.half = kFirstHalf;
+            J.slot = static_cast<uint32_t>(item);
+            item += args.split_first;
+        } else if (item < args.split_first + args.n_split) {
+            item -= args.n_split;
+        } else {
+            J.half = kSecondHalf;
+            J.slot = static_cast<uint32_t>(item - args.split_first - args.n_split);
+            item = args.split_first + J.slot;
+        }
+    }
     int d = 0;
     while (d + 1 < args.n_tensors && item >= args.t[d + 1].item_begin) ++d;
     const DevTensor& T = args.t[d];
@@ -660,6 +699,23 @@ __device__ __forceinline__ Job make_job(const LaunchArgs& args, int64_t item, ui
         J.lim = static_cast<uint32_t>(lim);
         const int64_t round_bits = static_cast<int64_t>(J.S) << J.lg;
         J.nr = static_cast<uint32_t>((static_cast<int64_t>(nb) * 8 + round_bits - 1) / round_bits);
+    }
+    J.r1 = J.nr;
+    if (J.half != kWholeChunk) {
+        // A chunk of fewer than 2 rounds is not split: its first half takes it whole.
+        const uint32_t h = J.nr / 2;
+        if (h == 0) {
+            if (J.half == kFirstHalf) {
+                J.half = kWholeChunk;
+            } else {
+                J.half = kNoHalf;
+                J.r0 = J.nr;
+            }
+        } else if (J.half == kFirstHalf) {
+            J.r1 = h;
+        } else {
+            J.r0 = h;
+        }
     }
     return J;
 }
@@ -1587,11 +1643,97 @@ struct __attribute__((aligned(16))) Lds {
     uint32_t gval[kMaxGroups];
     uint32_t ewave[kWaves];      // segment end of each wave's last lane
     uint32_t glast[kMaxGroups];  // segment end of each sub-group's last active thread
+    uint32_t hand[8];            // a split chunk's handoff as its second half took it
     uint32_t tile[kTileWords];
     // Past the slots: the word read or zero-ORed past the last slot, and the
     // groups an unclamped store batch of a whole-workgroup chunk reads.
     __attribute__((aligned(16))) uint8_t stage[kStagePadded];
 };
+
+// Handoff records of split chunks (LaunchArgs::split_first): kHandoffWords
+// 64-bit words each, every word the launch's tag above a 32-bit value. Word 0
+// is the record's state: 0 empty; p0 (where the second half's first round
+// starts) once the first half has written the record; kHandoffGaveUp once the
+// second half has stopped waiting for it. Words 1..6: the symbols placed so
+// far, the carried symbols, and their bytes. A record is empty again at the
+// end of a launch: the second half empties a record it reads, and a first
+// half that finds its second half gone empties it. Tags keep launches that
+// overlap on one GPU from reading each other's records (they then fall back
+// to whole chunks). Every access to a record is a device-scope atomic (it
+// bypasses the XCD's L2, whose contents other XCDs do not see), so no
+// fence has to write back or invalidate the L2 for it: the first half waits
+// for its word writes to complete before it publishes word 0, and the second
+// half reads the words only after it has seen word 0.
+constexpr uint32_t kHandoffWords = 8;
+constexpr uint32_t kHandoffSlots = 1024;
+constexpr uint32_t kHandoffGaveUp = 0xFFFFFFFFu;
+// Polls of a record (each an L2-bypassing load and a short sleep) before the
+// second half decodes its chunk whole. First halves are the grid's first
+// items and second halves its last, so the record is normally written long
+// before it is read.
+constexpr uint32_t kHandoffPolls = 64;
+
+// The first half's state at its end: thread 0 writes the record's words,
+// then publishes it in word 0 (release).
+__device__ __forceinline__ void give_handoff(const LaunchArgs& args, uint32_t slot, uint32_t p0,
+                                          uint32_t ob, uint32_t lead, const uint8_t* stage) {
+    uint64_t* const rec = args.handoff + static_cast<uint64_t>(slot) * kHandoffWords;
+    const uint64_t tg = static_cast<uint64_t>(args.tag) << 32;
+    uint32_t b[4] = {0u, 0u, 0u, 0u};
+    for (uint32_t k = 0; k < lead && k < 16u; ++k)
+        b[k >> 2] |= static_cast<uint32_t>(stage[k]) << (8 * (k & 3u));
+    __hip_atomic_store(rec + 1, tg | ob, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(rec + 2, tg | lead, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (uint32_t k = 0; k < 4; ++k)
+        __hip_atomic_store(rec + 3 + k, tg | b[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The words above are complete (device-scope writes) before word 0 is.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    uint64_t seen = 0;
+    if (!__hip_atomic_compare_exchange_strong(rec, &seen, tg | p0, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT) &&
+        seen == (tg | kHandoffGaveUp))
+        __hip_atomic_store(rec, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The second half's wait (thread 0): out[0] 1 when the record was taken,
+// then p0, the symbols placed, the carried symbols (< kGroup), their bytes.
+// A record whose values cannot come from its chunk is not taken.
+__device__ __forceinline__ void take_handoff(const LaunchArgs& args, uint32_t slot, uint32_t group,
+                                          uint32_t lim, uint32_t* out) {
+    uint64_t* const rec = args.handoff + static_cast<uint64_t>(slot) * kHandoffWords;
+    const uint64_t tg = static_cast<uint64_t>(args.tag) << 32;
+    uint64_t v = 0;
+    bool ok = false;
+    for (uint32_t k = 0; k < kHandoffPolls; ++k) {
+        v = __hip_atomic_load(rec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = (v >> 32) == args.tag && static_cast<uint32_t>(v) != kHandoffGaveUp;
+        if (ok) break;
+        __builtin_amdgcn_s_sleep(16);
+    }
+    if (!ok) {
+        uint64_t seen = 0;
+        if (!__hip_atomic_compare_exchange_strong(rec, &seen, tg | kHandoffGaveUp, __ATOMIC_RELAXED,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &&
+            (seen >> 32) == args.tag && static_cast<uint32_t>(seen) != kHandoffGaveUp) {
+            v = seen;
+            ok = true;
+        }
+    }
+    uint32_t w[6] = {0u, 0u, 0u, 0u, 0u, 0u};
+    if (ok) {
+        for (uint32_t k = 0; k < 6; ++k) {
+            const uint64_t x = __hip_atomic_load(rec + 1 + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = ok && (x >> 32) == args.tag;
+            w[k] = static_cast<uint32_t>(x);
+        }
+        __hip_atomic_store(rec, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // p0 lies within the longest codeword past its round's start.
+        ok = ok && static_cast<uint32_t>(v) < 64u && w[0] <= lim && w[1] < group && w[1] <= w[0];
+    }
+    out[0] = ok ? 1u : 0u;
+    out[1] = static_cast<uint32_t>(v);
+    for (uint32_t k = 0; k < 6; ++k) out[2 + k] = w[k];
+}
 
 // kLg > 0 fixes the threads per chunk at 1 << kLg for the whole launch, so
 // that sub-group geometry and the per-thread offsets derived from it are
@@ -1615,6 +1757,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     // record of each wave's lane 0 (start, whether it is checked) reuses the
     // sub-group prefix table, which that path does not need.
     constexpr bool kWhole = kLg == kLgThreads && kMode != kModeIndex;
+    // Whole-workgroup chunks of bf16 or exponent-byte launches may be split.
+    constexpr bool kSplit = kWhole && (kMode == kModeBf16 || kMode == kModeU8);
     uint32_t* const s_f0 = lds.gpre;
     uint32_t* const s_chk0 = lds.gpre + kWaves;
 
@@ -1631,10 +1775,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     // The first item's words and table load together.
     Job cur = make_job<kMode, kLg>(args, blockIdx.x, tid);
     Fetch F;
-    fetch_issue<kMode, kTiny>(F, args, cur, 0, tid);
+    fetch_issue<kMode, kTiny>(F, args, cur, cur.r0, tid);
     loaded = uniform(args.t[uniform(static_cast<uint32_t>(cur.d))].table);
     load_table(loaded, tid, s_wsyms, s_wmeta, s_len, s_esc);
-    fetch_commit<kTiny>(F, args, cur, 0, tid, s_tile);
+    fetch_commit<kTiny>(F, args, cur, cur.r0, tid, s_tile);
 
     for (int64_t item = blockIdx.x; item < args.total_items; item += gridDim.x) {
         const DevTensor& T = args.t[uniform(static_cast<uint32_t>(cur.d))];
@@ -1684,15 +1828,39 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
         int64_t ob = 0;     // chunk-local symbols placed so far
         uint32_t lead = 0;  // placed symbols still staged at the front of the region
         uint32_t p0 = 0;    // true start of the next round, relative to its first bit
-        for (uint32_t r = 0; r < NR; ++r) {
+        uint32_t r_begin = 0, r_end = NR;
+        if constexpr (kSplit) {
+            r_begin = uniform(cur.r0);
+            r_end = uniform(cur.r1);
+            if (uniform(static_cast<uint32_t>(cur.half)) == kSecondHalf) {
+                // The first half's state: where round r_begin starts, the
+                // symbols placed before it and the carried ones. Without it
+                // (the first half did not hand over in time), the chunk is
+                // decoded whole from round 0.
+                if (tid == 0) take_handoff(args, cur.slot, kGroup, cur.lim, lds.hand);
+                __syncthreads();
+                if (lds.hand[0] != 0u) {
+                    p0 = lds.hand[1];
+                    ob = lds.hand[2];
+                    lead = lds.hand[3];
+                    if (tid < lead) stage[tid] = static_cast<uint8_t>(lds.hand[4 + (tid >> 2)] >> (8 * (tid & 3u)));
+                } else {
+                    r_begin = 0;
+                    fetch_issue<kMode, kTiny>(F, args, cur, 0, tid);
+                    fetch_commit<kTiny>(F, args, cur, 0, tid, s_tile);
+                }
+                __syncthreads();
+            }
+        }
+        for (uint32_t r = r_begin; r < r_end; ++r) {
             // Offsets derived from the thread index are cheap to recompute;
             // keeping them live across the round costs registers.
             uint32_t i = i_item;
             asm volatile("" : "+v"(i));
-            // Next words: this item's round r + 1, or the next item's round 0.
-            const bool last = r + 1 == NR;
+            // Next words: this item's round r + 1, or the next item's first.
+            const bool last = r + 1 == r_end;
             const Job& fj = last ? nxt : cur;
-            const uint32_t fr = last ? 0u : r + 1;
+            const uint32_t fr = last ? uniform(nxt.r0) : r + 1;
             // Wave priorities by phase: the two workgroups of a CU overlap best
             // when issuing loads comes first, stores and compaction next, the
             // agreement check and scan after, and the decode loops last (each
@@ -1952,20 +2120,31 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             lead = rem;
             if (g_active) p0 = e_last - RB;
         }
-        if (NR == 0) {
-            fetch_issue<kMode, kTiny>(F, args, nxt, 0, tid);
-            fetch_commit<kTiny>(F, args, nxt, 0, tid, s_tile);
+        if (r_begin == r_end) {
+            fetch_issue<kMode, kTiny>(F, args, nxt, nxt.r0, tid);
+            fetch_commit<kTiny>(F, args, nxt, nxt.r0, tid, s_tile);
         }
 
         // Symbols carried out of the last round, then positions no codeword
         // of the chunk reached: those decode from zero bits, i.e. to sym_lut[0].
+        // A first half hands them over instead; a chunk's empty second half
+        // has none.
         __syncthreads();
+        [[maybe_unused]] bool tail = true;
+        if constexpr (kSplit) {
+            const uint32_t half = uniform(static_cast<uint32_t>(cur.half));
+            if (half == kFirstHalf && tid == 0)
+                give_handoff(args, cur.slot, p0, static_cast<uint32_t>(ob), lead, stage);
+            tail = half == kWholeChunk || half == kSecondHalf;
+        }
         if constexpr (kMode != kModeIndex) {
+            if (tail) {
             const int64_t t0 = chunk_base + ob - lead;
             const int64_t n_tail = lim - (ob - lead);
             for (int64_t k = i_item; k < n_tail; k += tpc) {
                 const uint32_t ex = k < lead ? stage[k] : tb.sym0;
                 store_one<kMode>(T, args.gemv, t0 + k, ex);
+            }
             }
         }
         cur = nxt;
@@ -3265,6 +3444,42 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void spec_kernel(const Lau
     }
 }
 
+// The handoff records of split chunks, one array per GPU (zero when the
+// library loads; every launch leaves its records empty). Kernels take its
+// device address, found once per device with that device current.
+__device__ __attribute__((aligned(256))) uint64_t scratch[kHandoffSlots * kHandoffWords];
+
+int handoff_records(uint64_t** out) {
+    static std::mutex mu;
+    static uint64_t* ptr[64] = {};
+    int dev = 0;
+    const hipError_t ge = hipGetDevice(&dev);
+    if (ge != hipSuccess) return fail(AIMG_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(ge));
+    if (dev < 0 || dev >= 64) {
+        *out = nullptr;  // no records: chunks are not split
+        return AIMG_OK;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return fail(AIMG_ERR_HIP, std::string("hipGetSymbolAddress (chunk handoff records): ") +
+                                          hipGetErrorString(e));
+        ptr[dev] = static_cast<uint64_t*>(p);
+    }
+    *out = ptr[dev];
+    return AIMG_OK;
+}
+
+// A launch's record tag: never 0, so that a written record is never 0.
+uint32_t next_tag() {
+    static std::atomic<uint32_t> n{0};
+    uint32_t t = 0;
+    while (t == 0) t = n.fetch_add(1, std::memory_order_relaxed) + 1;
+    return t;
+}
+
 int cu_count() {
     static std::once_flag once;
     static int n = 0;
@@ -3295,13 +3510,70 @@ struct Batch {
     bool full = true;  // every tensor has kThreads threads per chunk
 };
 
+// Whole-workgroup chunks of bf16 and exponent-byte launches: when the grid's
+// last pass over the chunks has more of them than half the grid (1360 chunks
+// on 512 workgroups: 336), the CUs that decode two of the last chunks finish
+// a chunk's rounds later than the rest. Those chunks are split in two halves
+// of their rounds: the first halves go first in the grid, the second halves
+// last, so that every workgroup has 5 or 6 rounds and every CU 10 or 11
+// (instead of 10 or 12), and a second half finds its record long written.
+// Each first half hands its state (where the next round starts, the symbols
+// placed, the carried partial group) to its second half through a record.
+// AIMG_CHUNK_SPLIT=0 turns this off.
+// The most rounds any CU decodes (2 a chunk, 1 a half; the grid's
+// workgroups w and w + slots / 2 share a CU) when the last `rest` of n chunks
+// are split (rest 0: none).
+int64_t max_cu_rounds(int64_t n, int64_t rest, int64_t slots) {
+    const int64_t items = n + rest;
+    auto wg = [&](int64_t w) {
+        int64_t r = 0;
+        for (int64_t i = w; i < items; i += slots) r += i < rest || i >= n ? 1 : 2;
+        return r;
+    };
+    int64_t m = 0;
+    for (int64_t c = 0; c < slots / 2; ++c) {
+        const int64_t r = wg(c) + wg(c + slots / 2);
+        m = r > m ? r : m;
+    }
+    return m;
+}
+
+int plan_split(LaunchArgs& a, int64_t n, int64_t slots) {
+    a.n_split = 0;
+    a.split_first = n;
+    const char* e = std::getenv("AIMG_CHUNK_SPLIT");
+    if (e != nullptr && e[0] == '0') return AIMG_OK;
+    if (n <= slots || slots % 2 != 0) return AIMG_OK;
+    const int64_t rest = n % slots;
+    if (2 * rest <= slots || rest > static_cast<int64_t>(kHandoffSlots)) return AIMG_OK;
+    // Only where it lowers the busiest CU's rounds (the 14B block's 5042
+    // chunks already spread to 40 or 38 rounds a CU: no split).
+    if (max_cu_rounds(n, rest, slots) >= max_cu_rounds(n, 0, slots)) return AIMG_OK;
+    uint64_t* rec = nullptr;
+    const int rc = handoff_records(&rec);
+    if (rc != AIMG_OK || rec == nullptr) return rc;
+    a.n_split = rest;
+    a.split_first = n - rest;
+    a.total_items = n + rest;
+    a.handoff = rec;
+    a.tag = next_tag();
+    return AIMG_OK;
+}
+
 template <int kMode>
 int launch_batch(Batch& B, hipStream_t s, bool tiny) {
     B.args.n_tensors = B.m;
     B.args.total_items = B.items;
+    B.args.n_split = 0;
     if (B.items == 0) return AIMG_OK;
     const int64_t slots = static_cast<int64_t>(cu_count()) * kBlocksPerCu;
-    const int64_t grid = B.items < slots ? B.items : slots;
+    if constexpr (kMode == kModeBf16 || kMode == kModeU8) {
+        if (!tiny && B.vec && B.full) {
+            const int rc = plan_split(B.args, B.items, slots);
+            if (rc != AIMG_OK) return rc;
+        }
+    }
+    const int64_t grid = B.args.total_items < slots ? B.args.total_items : slots;
     const dim3 gdim(static_cast<uint32_t>(grid)), bdim(kThreads);
     constexpr int kVecGroup = kMode == kModeU8 ? 16 : 8;
     if constexpr (kMode == kModeIndex) {

@@ -21,7 +21,10 @@
  *   - Pointers named "device" are HIP device pointers. Streams are hipStream_t
  *     passed as void* (NULL = the null stream). Launches are asynchronous and
  *     ordered on the given stream. Nothing here synchronises the device.
- *   - No entry point allocates device memory.
+ *   - No entry point allocates device memory. bf16 and exponent-byte decodes of
+ *     chunks of 65536 symbols or more may split the launch's last chunks in two
+ *     halves that hand over through a static 64 KiB device array (one per GPU,
+ *     held until the process ends); launches that overlap on one GPU stay exact.
  *   - Functions are re-entrant.
  */
 #ifndef AFTERIMAGE_DECODE_H

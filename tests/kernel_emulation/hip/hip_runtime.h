@@ -248,6 +248,19 @@ inline float atomicAdd(float* p, float v) {
 inline int __ffs(int x) { return __builtin_ffs(x); }
 inline uint32_t __umulhi(uint32_t a, uint32_t b) { return (uint32_t)(((uint64_t)a * b) >> 32); }
 inline void __builtin_amdgcn_s_setprio(int) {}  // wave issue priority: no effect here
+// A wave's short sleep: blocks run one after another here, so a wait for a
+// later block only passes its poll count.
+inline void __builtin_amdgcn_s_sleep(int) { std::this_thread::yield(); }
+inline void __builtin_amdgcn_fence(int, const char*) { __atomic_thread_fence(__ATOMIC_SEQ_CST); }
+#ifndef __HIP_MEMORY_SCOPE_AGENT
+#define __HIP_MEMORY_SCOPE_AGENT 4
+#endif
+// Device globals are host globals here.
+#define HIP_SYMBOL(x) (&(x))
+inline hipError_t hipGetSymbolAddress(void** p, const void* sym) {
+    *p = const_cast<void*>(sym);
+    return hipSuccess;
+}
 // v_dot2c_f32_bf16: c + a.lo b.lo + a.hi b.hi in fp32 (bf16 products are exact
 // in fp32).
 typedef __bf16 emu_bf16x2 __attribute__((ext_vector_type(2)));

@@ -88,6 +88,7 @@ def _run(emu, name, mode, index="", runs=None, strided=None, cus=None, copies=No
     env.pop("AIMG_EMU_CUS", None)
     env.pop("AIMG_EMU_COPIES", None)
     env.pop("AIMG_SPEC_RUNS", None)
+    env.pop("AIMG_CHUNK_SPLIT", None)
     if spec is not None:
         # "0": tensors without an index decode chunk by chunk; "1": in
         # speculative runs whatever their chunk size
@@ -205,6 +206,29 @@ def test_bf16_whole_workgroup_chunks_several_per_workgroup(emu):
     # current one; a 1024-symbol tensor in the same launch (two tables).
     W = workloads.bf16_normal((27, 16384), 13, 0.02, outlier_frac=1e-3)
     _bf16(emu, "bf16_whole_items", W, 65536, cus=1, spec="0")
+
+
+def test_bf16_split_chunks_hand_over_or_decode_whole(emu):
+    # Seven 65536-symbol chunks on a grid of 4 workgroups: the last pass
+    # would hold 3 chunks, so those are split in halves (rounds 0 and 1). The
+    # emulator runs workgroups one after another: the second half of chunk 4
+    # (workgroup 3) takes the record its first half (workgroup 0) wrote; those
+    # of chunks 5 and 6 (workgroups 0 and 1) wait for first halves of later
+    # workgroups, give up and decode their chunks whole, and those first
+    # halves then find their records given up and empty them.
+    W = workloads.bf16_normal((27, 16384), 14, 0.02, outlier_frac=1e-3)
+    _bf16(emu, "bf16_split", W, 65536, cus=2, spec="0")
+
+
+def test_u8_split_chunks_across_tensors(emu):
+    # Three copies of a 7-chunk tensor (21 chunks) on a grid of 12: the last
+    # 9 chunks (two of the second tensor, seven of the third) are split.
+    # Exponent bytes carry partial 16-byte groups between the halves.
+    rng = np.random.default_rng(15)
+    exps = np.clip(np.rint(rng.normal(120, 2.0, 7 * 65536 - 3000)), 100, 140).astype(np.int64)
+    enc = encode_chunked(torch.as_tensor(exps), chunk_size=65536)
+    _write(emu[1] / "u8_split", enc, exps.astype(np.uint8))
+    _run(emu, "u8_split", "u8", cus=6, copies=3, spec="0")
 
 
 @full
