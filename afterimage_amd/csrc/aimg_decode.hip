@@ -404,8 +404,9 @@ __device__ __forceinline__ uint32_t advance(TileRef below, const Tables& tb, uin
         take<kGlobalEsc>(tb, s, &syms, &adv, &c);
         pn = s.p + adv;
     }
+    const uint32_t sp = pn - adv;  // s.p, from pn (see decode_run_il)
     uint32_t kept;
-    return cut_window(tb, s.p, s.p + adv, c > 1 ? tb.syms[s.idx] : 0u, c, x, &kept);
+    return cut_window(tb, sp, pn, c > 1 ? tb.syms[s.idx] : 0u, c, x, &kept);
 }
 
 // Before a segment is decoded into a slot, its first word is zero.
@@ -510,12 +511,20 @@ __device__ __forceinline__ void decode_placed(TileRef below, const Tables& tb, u
         lds_or(reinterpret_cast<uint32_t*>((q - (reinterpret_cast<uintptr_t>(q) & 3u)) + 4), spill);
 }
 
-// One lookup's symbols into an interleaved slot (`lane` points at the lane's
-// word 0; word j is lane[64 j]) at byte q, as slot_put does it.
-__device__ __forceinline__ void slot_put_il(uint32_t* lane, uint32_t q, uint32_t syms) {
-    const uint32_t b = q & 3u;
-    const uint64_t v = static_cast<uint64_t>(syms) << (8 * b);
-    uint32_t* w = lane + (q >> 2) * 64;
+// A lane's interleaved slot: word j of lane l of wave w at byte
+// wblk + 256 j + 4 l of `slots` (wblk = w * kSlotRows * 256, a multiple of 256).
+struct IlSlot {
+    uint8_t* slots;
+    uint32_t wblk;
+    uint32_t lane4;  // 4 l
+};
+
+// One lookup's symbols into an interleaved slot at qa = wblk + 64 q, for
+// slot byte q, as slot_put does it: word q / 4 is at (qa & ~255) | lane4
+// and the byte within it is (qa >> 6) & 3 (one AND-OR for the address).
+__device__ __forceinline__ void slot_put_il(const IlSlot& sl, uint32_t qa, uint32_t syms) {
+    const uint64_t v = static_cast<uint64_t>(syms) << ((qa >> 3) & 24u);
+    uint32_t* w = reinterpret_cast<uint32_t*>(sl.slots + ((qa & ~255u) | sl.lane4));
     lds_or(w, static_cast<uint32_t>(v));
     w[64] = static_cast<uint32_t>(v >> 32);
 }
@@ -529,10 +538,10 @@ __device__ __forceinline__ void slot_put_il(uint32_t* lane, uint32_t q, uint32_t
 // reaches past cend.
 template <bool kGlobalEsc>
 __device__ __forceinline__ Adv decode_run_il(TileRef below, const Tables& tb, uint32_t p,
-                                             uint32_t x, uint32_t cend, uint32_t* lane) {
-    lane[0] = 0u;
+                                             uint32_t x, uint32_t cend, const IlSlot& sl) {
+    *reinterpret_cast<uint32_t*>(sl.slots + (sl.wblk | sl.lane4)) = 0u;
     if (p >= x) return {p, 0u};
-    uint32_t q = 0;
+    uint32_t qa = sl.wblk;
     const Reader rd = reader_at(below, p);
     Step s = lookup<true>(below, tb, rd.p, rd.sh, rd.pair);
     uint32_t syms, adv, c;
@@ -540,15 +549,20 @@ __device__ __forceinline__ Adv decode_run_il(TileRef below, const Tables& tb, ui
     uint32_t pn = s.p + adv;
     while (pn < x) {
         Step t = lookup<false>(below, tb, pn, pn - s.m, s.next);
-        slot_put_il(lane, q, syms);
-        q += c;
+        slot_put_il(sl, qa, syms);
+        qa += c << 6;
+        // c's last use in this step: the next step's c can take its register.
+        asm volatile("" : "+v"(qa), "+v"(c));
         t.syms = tb.syms[t.idx];
         s = t;
         take<kGlobalEsc>(tb, s, &syms, &adv, &c);
         pn = s.p + adv;
     }
-    if (cend - s.p < 16u) {
-        const uint32_t w = s.w & ~(0xFFFFFFFFu >> (cend - s.p));
+    // The last window's start, from pn (s.p itself is then not needed past
+    // the loop, and pn and s.p share a register in it).
+    const uint32_t sp = pn - adv;
+    if (cend - sp < 16u) {
+        const uint32_t w = s.w & ~(0xFFFFFFFFu >> (cend - sp));
         const uint32_t idx = w >> (32 - kWinBits);
         const uint32_t meta = tb.meta[idx];
         syms = tb.syms[idx];
@@ -560,9 +574,9 @@ __device__ __forceinline__ Adv decode_run_il(TileRef below, const Tables& tb, ui
         }
     }
     uint32_t kept;  // 1..4
-    const uint32_t e = cut_window(tb, s.p, s.p + adv, syms, c, x, &kept);
-    slot_put_il(lane, q, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
-    return {e, q + kept};
+    const uint32_t e = cut_window(tb, sp, sp + adv, syms, c, x, &kept);
+    slot_put_il(sl, qa, syms & (0xFFFFFFFFu >> (32u - 8u * kept)));
+    return {e, ((qa - sl.wblk) >> 6) + kept};
 }
 
 // Where to load the 4 bytes from packed-buffer byte A (A below the buffer
@@ -1890,15 +1904,16 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 const uint32_t w = uniform(tid >> 6);
                 uint32_t* const slot_il =
                     reinterpret_cast<uint32_t*>(stage + kLeadBytes) + w * kSlotRows * 64 + lane;
+                const IlSlot sl{stage + kLeadBytes, w * kSlotRows * 256u, lane * 4u};
                 __builtin_amdgcn_s_setprio(0);
                 if (active) {
                     Adv a;
                     if (global_esc) {
                         f = i == 0 ? p0 : advance<true>(below, tb, seg_lo - kOverlapBits, seg_lo);
-                        a = decode_run_il<true>(below, tb, f, seg_hi, 0xFFFFFFFFu, slot_il);
+                        a = decode_run_il<true>(below, tb, f, seg_hi, 0xFFFFFFFFu, sl);
                     } else {
                         f = i == 0 ? p0 : advance<false>(below, tb, seg_lo - kOverlapBits, seg_lo);
-                        a = decode_run_il<false>(below, tb, f, seg_hi, 0xFFFFFFFFu, slot_il);
+                        a = decode_run_il<false>(below, tb, f, seg_hi, 0xFFFFFFFFu, sl);
                     }
                     e = a.p;
                     cnt = a.n;
@@ -1936,8 +1951,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                     if (redo) {
                         f = ep;
                         const Adv a = global_esc
-                                          ? decode_run_il<true>(below, tb, f, seg_hi, 0xFFFFFFFFu, slot_il)
-                                          : decode_run_il<false>(below, tb, f, seg_hi, 0xFFFFFFFFu, slot_il);
+                                          ? decode_run_il<true>(below, tb, f, seg_hi, 0xFFFFFFFFu, sl)
+                                          : decode_run_il<false>(below, tb, f, seg_hi, 0xFFFFFFFFu, sl);
                         e = a.p;
                         cnt = a.n;
                     }
@@ -3172,6 +3187,7 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
     asm volatile("" : "+v"(below));
     uint8_t* const stage = lds.stage;
     uint32_t* const slot = reinterpret_cast<uint32_t*>(lds.stage + kLeadBytes) + w * kSlotRows * 64 + lane;
+    const IlSlot sl{lds.stage + kLeadBytes, w * kSlotRows * 256u, lane * 4u};
     const int64_t piece_end = static_cast<int64_t>(cb) * cs < T.n_symbols ? static_cast<int64_t>(cb) * cs
                                                                          : T.n_symbols;
     while (fall_from < 0) {
@@ -3209,10 +3225,10 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
             Adv a;
             if (global_esc) {
                 f = kseg == 0 ? lo : tid == 0 ? rel + p0 : advance<true>(below, tb, lo - kOverlapBits, lo);
-                a = decode_run_il<true>(below, tb, f, hi, cend, slot);
+                a = decode_run_il<true>(below, tb, f, hi, cend, sl);
             } else {
                 f = kseg == 0 ? lo : tid == 0 ? rel + p0 : advance<false>(below, tb, lo - kOverlapBits, lo);
-                a = decode_run_il<false>(below, tb, f, hi, cend, slot);
+                a = decode_run_il<false>(below, tb, f, hi, cend, sl);
             }
             e = a.p;
             cnt = a.n;
@@ -3251,8 +3267,8 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
             __syncthreads();  // the records are read before they are written again
             if (redo) {
                 f = ep;
-                const Adv a = global_esc ? decode_run_il<true>(below, tb, f, hi, cend, slot)
-                                         : decode_run_il<false>(below, tb, f, hi, cend, slot);
+                const Adv a = global_esc ? decode_run_il<true>(below, tb, f, hi, cend, sl)
+                                         : decode_run_il<false>(below, tb, f, hi, cend, sl);
                 e = a.p;
                 cnt = a.n;
             }
