@@ -102,6 +102,10 @@ constexpr uint32_t kSmAhead = kStoreBatch;
 // faster on the 5120x17408 layer than the default policy, while the same
 // policy on the stream-word or sign/mantissa loads was 2.5% slower.
 constexpr int kCachePolicyNT = 2;
+// s_sleep argument (units of 64 clocks) of each of the two sleeps that delay
+// the second workgroup of a CU in the chunk kernel: 2 x 80 x 64 = 10240
+// clocks, about 4.3 us at 2.4 GHz.
+constexpr int kStaggerSleep = 80;
 static_assert(kSmAhead <= kStoreBatch, "kSmAhead");
 
 struct DevTensor {
@@ -174,6 +178,9 @@ struct LaunchArgs {
     int64_t n_split;
     uint64_t* handoff;
     uint32_t tag;
+    // Chunk by chunk on a full grid (two workgroups per CU, workgroups w and
+    // w + grid / 2 sharing one): the second half of the grid starts later.
+    int32_t stagger;
 };
 
 // Read-only launch data that every thread of a workgroup reads at the same
@@ -1777,6 +1784,17 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     uint32_t* const s_chk0 = lds.gpre + kWaves;
 
     const uint32_t tid = threadIdx.x;
+    // A CU's two workgroups start together and would go through their rounds
+    // in step, decoding at the same time and loading and storing at the same
+    // time. The second starts two sleeps of kStaggerSleep later (about 4 us,
+    // near a workgroup's start-up), so that their phases alternate from the
+    // first round on: 5120x17408 layer 71.4 -> 68.4 us (2 x 60: 68.6, 2 x
+    // 120: 69.0, 2 x 40: 70.2; the 14B block unchanged). AIMG_STAGGER=0
+    // turns it off.
+    if (args.stagger != 0 && blockIdx.x >= gridDim.x / 2) {
+        __builtin_amdgcn_s_sleep(kStaggerSleep);
+        __builtin_amdgcn_s_sleep(kStaggerSleep);
+    }
     const uint8_t* loaded = nullptr;
     Tables tb;
     tb.syms = s_wsyms;
@@ -3590,6 +3608,8 @@ int launch_batch(Batch& B, hipStream_t s, bool tiny) {
         }
     }
     const int64_t grid = B.args.total_items < slots ? B.args.total_items : slots;
+    const char* stag = std::getenv("AIMG_STAGGER");
+    B.args.stagger = grid == slots && slots % 2 == 0 && !(stag != nullptr && stag[0] == '0') ? 1 : 0;
     const dim3 gdim(static_cast<uint32_t>(grid)), bdim(kThreads);
     constexpr int kVecGroup = kMode == kModeU8 ? 16 : 8;
     if constexpr (kMode == kModeIndex) {
