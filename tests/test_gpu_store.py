@@ -167,11 +167,14 @@ def test_unaligned_output_view_uses_elementwise_stores():
 
 
 @pytest.mark.parametrize("shape,chunk,tiny", [((3,), 3, True), ((7, 5), 16, False),
-                                              ((64, 1000), 4096, False)])
+                                              ((64, 1000), 4096, False), ((40, 4096), 65536, False),
+                                              ((30,), 65536, False), ((23,), 65536, False),
+                                              ((20,), 65536, False)])
 def test_packed_buffer_without_slack_bytes(shape, chunk, tiny):
     """A packed buffer that ends at the last chunk's last byte: the final
     words come from the buffer's last whole word, or byte by byte when the
-    whole buffer is shorter than 4 bytes."""
+    whole buffer is shorter than 4 bytes. At 65536-symbol chunks (whole
+    workgroups) (30,) packs into 10 bytes, (23,) into 8 and (20,) into 7."""
     W = workloads.bf16_normal(shape, 123, 0.02)
     layer = compress_layer(W, chunk_size=chunk)
     enc = layer.encoded

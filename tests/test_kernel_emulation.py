@@ -220,6 +220,21 @@ def test_bf16_split_chunks_hand_over_or_decode_whole(emu):
     _bf16(emu, "bf16_split", W, 65536, cus=2, spec="0")
 
 
+@pytest.mark.parametrize("shape", [(40, 4096), (30,)])
+def test_bf16_whole_workgroup_chunks_without_slack_bytes(emu, shape):
+    # The packed buffer ends at the last chunk's last byte: the last words
+    # are loaded from the buffer's last whole word and shifted back.
+    import dataclasses
+    W = workloads.bf16_normal(shape, 123, 0.02)
+    layer = compress_layer(W, chunk_size=65536)
+    enc = layer.encoded
+    used = int(enc.chunk_offsets[-1]) + int(enc.chunk_nbytes[-1])
+    trimmed = dataclasses.replace(enc, packed=np.asarray(enc.packed)[:used].copy())
+    name = "bf16_noslack_%d" % W.numel()
+    _write(emu[1] / name, trimmed, W.reshape(-1).view(torch.int16).numpy(), layer.sign_mantissa.numpy())
+    _run(emu, name, "bf16", spec="0")
+
+
 def test_u8_split_chunks_across_tensors(emu):
     # Three copies of a 7-chunk tensor (21 chunks) on a grid of 12: the last
     # 9 chunks (two of the second tensor, seven of the third) are split.
