@@ -1903,7 +1903,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             // output starts at a known element; its length is known only
             // after decoding), requested now so the store never waits.
             SmBatch<kMode> smb;
-            sm_issue<kMode, kGroup>(smb, T, chunk_base + ob - lead, i, tpc);
+            // (A whole-workgroup chunk's: none past the chunk's last element.)
+            sm_issue<kMode, kGroup>(smb, T, chunk_base + ob - lead, i, tpc,
+                                    kWhole ? uniform(static_cast<uint32_t>(chunk_base + lim)) : 0xFFFFFFFFu);
             const uint32_t RB = round_len(cur, r);
             const bool g_active = RB != 0;
 
