@@ -104,3 +104,23 @@ def test_ragged_split_layers(rows):
     (o,) = decode_bf16([dt])
     torch.cuda.synchronize()
     assert torch.equal(_bits(o), _bits(W))
+
+
+def test_records_reused_by_a_smaller_launch_next(layers, monkeypatch):
+    # Two split launches in a row through the C-ABI, the second smaller (771
+    # chunks: the last 259 split): the records the first leaves empty serve
+    # the second, and both equal the same launches with splitting off.
+    W1, _, dt1 = layers[0]
+    W2 = workloads.bf16_normal((3081, 16384), 31, 0.02, outlier_frac=1e-3)
+    l2 = compress_layer(W2, chunk_size=65536)
+    assert l2.encoded.n_chunks == 771
+    dt2 = DeviceTensor.from_encoded(l2.encoded, l2.sign_mantissa, "cuda")
+    (a1,) = decode_bf16([dt1])
+    (a2,) = decode_bf16([dt2])
+    monkeypatch.setenv("AIMG_CHUNK_SPLIT", "0")
+    (b1,) = decode_bf16([dt1])
+    (b2,) = decode_bf16([dt2])
+    monkeypatch.delenv("AIMG_CHUNK_SPLIT")
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(a1), _bits(b1)) and torch.equal(_bits(a1), _bits(W1))
+    assert torch.equal(_bits(a2), _bits(b2)) and torch.equal(_bits(a2), _bits(W2))
