@@ -3171,16 +3171,25 @@ __device__ __forceinline__ void spec_tile_commit(const uint32_t (&raw)[kTileBatc
 // Chunks [ca, cb) of tensor T (all of them below n_jobs).
 template <int kMode, int kGroup>
 __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, const LaunchArgs& args,
-                           const DevTensor& T, uint32_t ca, uint32_t cb, const uint8_t* table) {
+                           const DevTensor& T, uint32_t ca, uint32_t cb, const uint8_t* table,
+                           uint32_t pre_c0 = 0xFFFFFFFFu) {
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, w = uniform(tid >> 6);
     const uint32_t S = segment_bits(tb.min_len);
     const uint32_t smagic = static_cast<uint32_t>(((uint64_t{1} << 32) + S / 8 - 1) / (S / 8));
     const int64_t cs = T.chunk_size;
     // The piece's first table and words; the decode table (when it changes)
-    // loads while they arrive.
+    // loads while they arrive. Chunks from pre_c0 on, when set: their offsets
+    // and lengths are in the stage already (those of the piece's chunks).
     SpecTabFetch TF;
-    spec_tab_issue(TF, T, ca, lane);
+    if (pre_c0 != 0xFFFFFFFFu) {
+        const uint32_t* const pre = reinterpret_cast<const uint32_t*>(lds.stage);
+        const uint32_t j = ca - pre_c0 + lane;
+        TF.co = j < kThreads ? pre[j] : 0u;
+        TF.cn = j < kThreads ? pre[kThreads + j] : 0u;
+    } else {
+        spec_tab_issue(TF, T, ca, lane);
+    }
     if (table != nullptr) {
         __syncthreads();  // every thread is done with the previous table
         load_table(table, tid, lds.wsyms, lds.wmeta, lds.len, lds.esc);
@@ -3438,10 +3447,89 @@ __device__ void spec_piece(SpecLds& lds, const Tables& tb, bool global_esc, cons
     __syncthreads();  // LDS is free for the next piece
 }
 
+// floor(a b / c) for a < 2^31, b < 2^16 and c >= 1: the products stay below
+// 2^47, where the rounded double quotient is within one of the true one.
+__device__ __forceinline__ uint32_t mul_div(uint32_t a, uint32_t b, uint32_t c) {
+    const uint64_t x = static_cast<uint64_t>(a) * b;
+    uint64_t q = static_cast<uint64_t>(static_cast<double>(x) / static_cast<double>(c));
+    if (q * c > x)
+        --q;
+    else if ((q + 1) * c <= x)
+        ++q;
+    return static_cast<uint32_t>(q);
+}
+
+// How a CU's chunks [ca, cb) of one tensor split between its two
+// workgroups: the first takes the first k of them (returned), the second the
+// rest. Rounds hold 512 segments (a chunk's may straddle two), so at the
+// middle both workgroups would often end in a partial round, R + 1 rounds for
+// the CU where R would do. The second workgroup takes instead the last chunks
+// that fit in floor(R / 2) whole rounds, the first the rest (its last round
+// partial). Shares of at most kThreads chunks (the 5120x17408 layer at
+// 1024-symbol chunks: 340 a CU); larger ones split at the middle. Every
+// thread of both workgroups finds the same k.
+// The chunks' offsets and lengths, loaded here, stay in the stage
+// (pre[0 .. kThreads) and pre[kThreads ..), chunk *pre_c0 first) for the
+// piece's first round table, and the tensor's decode table is loaded into
+// LDS while they arrive (*pre_c0 = 0xFFFFFFFF: neither was done).
+// Every wave of both workgroups runs this once, before the rounds: its
+// instructions count (a thousand a wave: about 2 us on the layer's grid).
+__device__ uint32_t spec_split(const DevTensor& T, uint32_t ca, uint32_t cb, SpecLds& lds,
+                               uint32_t* pre_c0) {
+    *pre_c0 = 0xFFFFFFFFu;
+    const uint32_t n = cb - ca;
+    if (n < 2 || n > static_cast<uint32_t>(kThreads)) return n / 2;
+    const uint32_t tid = threadIdx.x;
+    SpecTabFetch F;  // chunk ca + tid (0 past the chunk count)
+    {
+        const uint64_t n4 = 4 * static_cast<uint64_t>(T.n_chunks);
+        const uint32_t lim = n4 < 0xFFFFFFFFull ? static_cast<uint32_t>(n4) : 0xFFFFFFFCu;
+        F.co = __builtin_amdgcn_raw_buffer_load_b32(buffer_of(T.offsets, lim), 4 * (ca + tid), 0, 0);
+        F.cn = __builtin_amdgcn_raw_buffer_load_b32(buffer_of(T.nbytes, lim), 4 * (ca + tid), 0, 0);
+    }
+    const uint8_t* const table = uniform(T.table);
+    load_table(table, tid, lds.wsyms, lds.wmeta, lds.len, lds.esc);
+    consume(F.co);
+    consume(F.cn);
+    uint32_t* const pre = reinterpret_cast<uint32_t*>(lds.stage);
+    pre[tid] = F.co;
+    pre[kThreads + tid] = F.cn;
+    // Segments of the chunk, as the round table counts them.
+    const uint32_t S = segment_bits(header_of(table)->min_len);
+    const uint32_t smagic = static_cast<uint32_t>(((uint64_t{1} << 32) + S / 8 - 1) / (S / 8));
+    int64_t off = static_cast<int32_t>(F.co), nb = static_cast<int32_t>(F.cn);
+    off = off < 0 ? 0 : (off > T.packed_nbytes ? T.packed_nbytes : off);
+    nb = nb < 0 ? 0 : (nb > T.packed_nbytes - off ? T.packed_nbytes - off : nb);
+    const uint32_t nseg = tid < n && nb < kSpecMaxChunkBytes
+                              ? div_ceil_seg(static_cast<uint32_t>(nb), S / 8, smagic)
+                              : 0u;
+    uint32_t* const s_wsum = &lds.rec[0][0];  // free until the first round
+    if (tid == 0) lds.last[0] = 0u;
+    const uint32_t excl = block_scan_excl(nseg, s_wsum);
+    uint32_t total = 0;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) total += s_wsum[k];
+    const uint32_t rounds = (total + kThreads - 1) / kThreads;
+    // The first workgroup's chunks: those that start before its share ends,
+    // a prefix of the share (its segment counts only grow); the thread of
+    // its last chunk writes their number (an atomic maximum over all of them
+    // took 2.5 us: the LDS serialises updates of one word).
+    const uint32_t first_share = total - rounds / 2 * kThreads;
+    const bool mine = tid < n && excl < first_share;
+    const bool next = tid + 1 < n && excl + nseg < first_share;
+    if (mine && !next) lds.last[0] = tid + 1;
+    __syncthreads();
+    const uint32_t k = uniform(lds.last[0]);
+    __syncthreads();  // read before the rounds use these words
+    *pre_c0 = ca;
+    return k;
+}
+
 // The launch's tensors in one sequence of elements; each workgroup takes the
 // chunks whose first element lies in its share. On a full grid (args.strided
 // set) workgroups b and b + grid / 2 are taken to share a CU and split one
-// CU's share.
+// CU's share; a launch of one tensor there shares out chunks instead
+// (n_jobs b / (grid / 2) on), split by spec_split.
 template <int kMode, int kGroup>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void spec_kernel(const LaunchArgs args) {
     __shared__ SpecLds lds;
@@ -3450,21 +3538,39 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void spec_kernel(const Lau
     tb.meta = lds.wmeta;
     tb.len = lds.len;
     tb.esc = lds.esc;
-    const uint8_t* loaded = nullptr;
-    const int64_t N = args.total_items;
     const uint32_t G = gridDim.x;
     const uint32_t P = args.strided != 0 && G % 2 == 0 ? G / 2 : G;
     const uint32_t s = blockIdx.x % P, h = blockIdx.x / P;
-    const int64_t lo_cu = N * s / P, hi_cu = N * (s + 1) / P;
-    const int64_t mid = (lo_cu + hi_cu) / 2;
-    const int64_t L = P == G ? lo_cu : (h == 0 ? lo_cu : mid);
-    const int64_t R = P == G ? hi_cu : (h == 0 ? mid : hi_cu);
+    if (P != G && args.n_tensors == 1) {
+        const DevTensor& T = args.t[0];
+        const uint32_t nj = static_cast<uint32_t>(T.n_jobs);
+        const uint32_t ca_cu = mul_div(nj, s, P), cb_cu = mul_div(nj, s + 1, P);
+        uint32_t pre_c0;
+        const uint32_t k = spec_split(T, ca_cu, cb_cu, lds, &pre_c0);
+        const uint32_t ca = h == 0 ? ca_cu : ca_cu + k, cb = h == 0 ? ca_cu + k : cb_cu;
+        if (ca >= cb) return;
+        const uint8_t* const table = uniform(T.table);
+        const auto* hdr = header_of(table);
+        tb.sym0 = hdr->sym0;
+        tb.min_len = hdr->min_len >= 1 ? hdr->min_len : 1u;
+        tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(table + kEscOffset);
+        const bool global_esc = hdr->n_esc_blocks > static_cast<uint32_t>(kLdsEscBlocks);
+        spec_piece<kMode, kGroup>(lds, tb, global_esc, args, T, ca, cb,
+                                  pre_c0 != 0xFFFFFFFFu ? nullptr : table, pre_c0);
+        return;
+    }
+    const uint8_t* loaded = nullptr;
+    const int64_t N = args.total_items;
+    const int64_t L = N * s / P, R = N * (s + 1) / P;
+    const int64_t mid = (L + R) / 2;
+    const int64_t lo = P == G ? L : (h == 0 ? L : mid);
+    const int64_t hi = P == G ? R : (h == 0 ? mid : R);
     int64_t O = 0;  // first element of tensor d in the sequence
     for (int d = 0; d < args.n_tensors; ++d) {
         const DevTensor& T = args.t[d];
         const int64_t cs = T.chunk_size;
-        int64_t ca = L - O <= 0 ? 0 : (L - O + cs - 1) / cs;
-        int64_t cb = R - O <= 0 ? 0 : (R - O + cs - 1) / cs;
+        int64_t ca = lo - O <= 0 ? 0 : (lo - O + cs - 1) / cs;
+        int64_t cb = hi - O <= 0 ? 0 : (hi - O + cs - 1) / cs;
         ca = ca < T.n_jobs ? ca : T.n_jobs;
         cb = cb < T.n_jobs ? cb : T.n_jobs;
         O += T.n_symbols;

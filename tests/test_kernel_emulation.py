@@ -423,6 +423,24 @@ def test_spec_runs_bf16_1024_chunks_many_rounds(emu, spec):
     _bf16(emu, "sp1024_%s" % spec, W, 1024, cus=2, spec=spec)
 
 
+@full
+def test_spec_runs_u8_share_above_a_round_table(emu):
+    # One tensor of 1100 1024-symbol chunks on one CU: the share is more
+    # chunks than a workgroup has threads, so the two workgroups split it at
+    # its middle chunk instead of by segment counts.
+    rng = np.random.default_rng(27)
+    _u8(emu, "sp_wide", rng.integers(90, 135, 1024 * 1100), 1024, cus=1)
+
+
+def test_spec_runs_shares_of_two_or_three_chunks(emu):
+    # 16 and 17 chunks on 8 CUs (a full grid of 16 workgroups): CU shares of
+    # two chunks and of three, the smallest a full grid has.
+    W = workloads.bf16_normal((16, 1024), 28, 0.02, outlier_frac=1e-2)
+    _bf16(emu, "sp_two", W, 1024, cus=8)
+    W = workloads.bf16_normal((17, 1024), 29, 0.02, outlier_frac=1e-2)
+    _bf16(emu, "sp_three", W, 1024, cus=8)
+
+
 def test_spec_runs_bf16_64k_chunks_across_chunk_boundaries(emu):
     # 6 chunks of 65536 on a 2-CU grid, forced into speculative runs (such
     # chunks decode chunk by chunk unless forced): rounds of a workgroup
