@@ -3541,38 +3541,38 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void spec_kernel(const Lau
     const uint32_t G = gridDim.x;
     const uint32_t P = args.strided != 0 && G % 2 == 0 ? G / 2 : G;
     const uint32_t s = blockIdx.x % P, h = blockIdx.x / P;
-    if (P != G && args.n_tensors == 1) {
+    // (One call of spec_piece below: a second copy of it made the batch-4
+    // GEMV's registers spill to scratch memory, 4x slower.)
+    const bool by_chunks = P != G && args.n_tensors == 1;
+    uint32_t pre_c0 = 0xFFFFFFFFu;
+    uint32_t ca_w = 0, cb_w = 0;  // by_chunks: this workgroup's chunks
+    int64_t lo = 0, hi = 0;       // otherwise: its share of the elements
+    if (by_chunks) {
         const DevTensor& T = args.t[0];
         const uint32_t nj = static_cast<uint32_t>(T.n_jobs);
         const uint32_t ca_cu = mul_div(nj, s, P), cb_cu = mul_div(nj, s + 1, P);
-        uint32_t pre_c0;
         const uint32_t k = spec_split(T, ca_cu, cb_cu, lds, &pre_c0);
-        const uint32_t ca = h == 0 ? ca_cu : ca_cu + k, cb = h == 0 ? ca_cu + k : cb_cu;
-        if (ca >= cb) return;
-        const uint8_t* const table = uniform(T.table);
-        const auto* hdr = header_of(table);
-        tb.sym0 = hdr->sym0;
-        tb.min_len = hdr->min_len >= 1 ? hdr->min_len : 1u;
-        tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(table + kEscOffset);
-        const bool global_esc = hdr->n_esc_blocks > static_cast<uint32_t>(kLdsEscBlocks);
-        spec_piece<kMode, kGroup>(lds, tb, global_esc, args, T, ca, cb,
-                                  pre_c0 != 0xFFFFFFFFu ? nullptr : table, pre_c0);
-        return;
+        ca_w = h == 0 ? ca_cu : ca_cu + k;
+        cb_w = h == 0 ? ca_cu + k : cb_cu;
+    } else {
+        const int64_t N = args.total_items;
+        const int64_t L = N * s / P, R = N * (s + 1) / P;
+        const int64_t mid = (L + R) / 2;
+        lo = P == G ? L : (h == 0 ? L : mid);
+        hi = P == G ? R : (h == 0 ? mid : R);
     }
-    const uint8_t* loaded = nullptr;
-    const int64_t N = args.total_items;
-    const int64_t L = N * s / P, R = N * (s + 1) / P;
-    const int64_t mid = (L + R) / 2;
-    const int64_t lo = P == G ? L : (h == 0 ? L : mid);
-    const int64_t hi = P == G ? R : (h == 0 ? mid : R);
+    const uint8_t* loaded = pre_c0 != 0xFFFFFFFFu ? uniform(args.t[0].table) : nullptr;
     int64_t O = 0;  // first element of tensor d in the sequence
     for (int d = 0; d < args.n_tensors; ++d) {
         const DevTensor& T = args.t[d];
         const int64_t cs = T.chunk_size;
-        int64_t ca = lo - O <= 0 ? 0 : (lo - O + cs - 1) / cs;
-        int64_t cb = hi - O <= 0 ? 0 : (hi - O + cs - 1) / cs;
-        ca = ca < T.n_jobs ? ca : T.n_jobs;
-        cb = cb < T.n_jobs ? cb : T.n_jobs;
+        int64_t ca = ca_w, cb = cb_w;
+        if (!by_chunks) {
+            ca = lo - O <= 0 ? 0 : (lo - O + cs - 1) / cs;
+            cb = hi - O <= 0 ? 0 : (hi - O + cs - 1) / cs;
+            ca = ca < T.n_jobs ? ca : T.n_jobs;
+            cb = cb < T.n_jobs ? cb : T.n_jobs;
+        }
         O += T.n_symbols;
         if (ca >= cb) continue;
         const uint8_t* const table = uniform(T.table);
@@ -3582,7 +3582,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void spec_kernel(const Lau
         tb.gesc = (const __attribute__((address_space(1))) uint16_t*)(table + kEscOffset);
         const bool global_esc = hdr->n_esc_blocks > static_cast<uint32_t>(kLdsEscBlocks);
         spec_piece<kMode, kGroup>(lds, tb, global_esc, args, T, static_cast<uint32_t>(ca),
-                                  static_cast<uint32_t>(cb), table != loaded ? table : nullptr);
+                                  static_cast<uint32_t>(cb), table != loaded ? table : nullptr,
+                                  d == 0 ? pre_c0 : 0xFFFFFFFFu);
         loaded = table;
     }
 }
