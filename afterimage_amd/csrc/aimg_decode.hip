@@ -898,14 +898,17 @@ __device__ __forceinline__ uint32_t block_scan_excl(uint32_t v, uint32_t* s_wsum
 }
 
 // bf16 bits ((sm & 0x80) << 8) | (e << 7) | (sm & 0x7F), the closed form of
-// _recombine (compressed_store.py:94-114), for the two elements whose
-// sign/mantissa and exponent bytes sit at byte `lane2` and lane2+1 of `sm4`
-// and `e4`: sm|sm<<8 supplies bit 15 and bits 6..0, e<<7 bits 14..7.
-template <uint32_t kSmSel, uint32_t kExpSel>
-__device__ __forceinline__ uint32_t bf16_pair(uint32_t sm4, uint32_t e4) {
-    const uint32_t a = __builtin_amdgcn_perm(sm4, sm4, kSmSel);   // s0 s0 s1 s1
-    const uint32_t b = __builtin_amdgcn_perm(e4, e4, kExpSel) >> 1; // e0<<7, e1<<7
-    return (a & 0x807F807Fu) | (b & 0x7F807F80u);
+// _recombine (compressed_store.py:94-114), for the four elements whose
+// sign/mantissa and exponent bytes are the bytes of `sm4` and `e4`: elements
+// 0 and 1 in .x, 2 and 3 in .y. A bf16's low byte is e's bit 0 over sm's bits
+// 6..0, its high byte sm's bit 7 over e's bits 7..1: both for all four
+// elements with one shift and one bit select each, then one byte permutation
+// per pair interleaves them (six instructions; a pair at a time took eight).
+__device__ __forceinline__ uint2 bf16_quad(uint32_t sm4, uint32_t e4) {
+    const uint32_t lo = ((e4 << 7) & 0x80808080u) | (sm4 & 0x7F7F7F7Fu);  // low bytes
+    const uint32_t hi = (sm4 & 0x80808080u) | ((e4 >> 1) & 0x7F7F7F7Fu);  // high bytes
+    // {hi, lo} as bytes 7..0: element j's low byte is byte j, its high byte j + 4.
+    return make_uint2(__builtin_amdgcn_perm(hi, lo, 0x05010400u), __builtin_amdgcn_perm(hi, lo, 0x07030602u));
 }
 
 __device__ __forceinline__ uint16_t bf16_one(uint32_t sm, uint32_t e) {
@@ -1108,10 +1111,12 @@ __device__ __forceinline__ void gemv_round_whole(const uint2 (&sm)[kStoreBatch],
         const bool live = v < nfull && v >= v_lo;
         const uint2 e = *reinterpret_cast<const uint2*>(stage + v * kGroup);
         uint4 w;
-        w.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, e.x);
-        w.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, e.x);
-        w.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, e.y);
-        w.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, e.y);
+        const uint2 pa = bf16_quad(sm[k].x, e.x);
+        const uint2 pb = bf16_quad(sm[k].y, e.y);
+        w.x = pa.x;
+        w.y = pa.y;
+        w.z = pb.x;
+        w.w = pb.y;
         if (ec + kSpan <= cols) {
             if (er != acc_row) {
                 if (acc_row != 0xFFFFFFFFu) {
@@ -1305,10 +1310,12 @@ __device__ __forceinline__ void gemm_round_pieces(const uint2 (&sm)[kStoreBatch]
             const uint32_t v = k * kThreads + tid;
             if (v < ve) {
                 uint4 wv;
-                wv.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, ev[k].x);
-                wv.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, ev[k].x);
-                wv.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, ev[k].y);
-                wv.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, ev[k].y);
+                const uint2 pa = bf16_quad(sm[k].x, ev[k].x);
+                const uint2 pb = bf16_quad(sm[k].y, ev[k].y);
+                wv.x = pa.x;
+                wv.y = pa.y;
+                wv.z = pb.x;
+                wv.w = pb.y;
                 const uint32_t row = (g0 + v) / cg;
                 *reinterpret_cast<uint4*>(stage + 16 * (v - vb + pad * (row - rb))) = wv;
             }
@@ -1416,10 +1423,12 @@ __device__ __forceinline__ void gemm_round_rows(const DevTensor& T, const GemvAr
 #pragma unroll
                 for (uint32_t u = 0; u < kGemmUnroll; ++u) {
                     uint4 wb;
-                    wb.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[u].x, ex[u].x);
-                    wb.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[u].x, ex[u].x);
-                    wb.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[u].y, ex[u].y);
-                    wb.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[u].y, ex[u].y);
+                    const uint2 pa = bf16_quad(sm[u].x, ex[u].x);
+                    const uint2 pb = bf16_quad(sm[u].y, ex[u].y);
+                    wb.x = pa.x;
+                    wb.y = pa.y;
+                    wb.z = pb.x;
+                    wb.w = pb.y;
                     A.d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[u]),
                                                                   __builtin_bit_cast(bf16x8_t, wb),
                                                                   A.d, 0, 0, 0);
@@ -1537,10 +1546,12 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
             const uint32_t v = k * tpc + i;
             if (v >= nfull || v < v_lo) continue;
             v4u32 o4;
-            o4[0] = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, ev[k].x);
-            o4[1] = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, ev[k].x);
-            o4[2] = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, ev[k].y);
-            o4[3] = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, ev[k].y);
+            const uint2 pa = bf16_quad(sm[k].x, ev[k].x);
+            const uint2 pb = bf16_quad(sm[k].y, ev[k].y);
+            o4[0] = pa.x;
+            o4[1] = pa.y;
+            o4[2] = pb.x;
+            o4[3] = pb.y;
             __builtin_amdgcn_raw_buffer_store_b128(o4, rs, vo, 16u * k * tpc, kCachePolicyNT);
         }
         return;
@@ -1600,10 +1611,12 @@ __device__ __forceinline__ void store_round(const SmBatch<kMode>& B, const DevTe
         // Staged exponents read here rather than all at once: registers.
         const uint2 e = *reinterpret_cast<const uint2*>(stage + (kWhole || live ? v : 0u) * kGroup);
         uint4 w;
-        w.x = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].x, e.x);
-        w.y = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].x, e.x);
-        w.z = bf16_pair<0x01010000u, 0x010C000Cu>(sm[k].y, e.y);
-        w.w = bf16_pair<0x03030202u, 0x030C020Cu>(sm[k].y, e.y);
+        const uint2 pa = bf16_quad(sm[k].x, e.x);
+        const uint2 pb = bf16_quad(sm[k].y, e.y);
+        w.x = pa.x;
+        w.y = pa.y;
+        w.z = pb.x;
+        w.w = pb.y;
         const uint32_t r0 = __builtin_amdgcn_readlane(row, __builtin_ctzll(lm));
         if (__ballot(live && row != r0) == 0) {
             if (r0 != acc_row) {
@@ -3968,8 +3981,9 @@ __global__ __launch_bounds__(256) void recombine_kernel(const uint8_t* e, const 
             v4u32 o[2];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                o[q / 2][2 * (q % 2)] = bf16_pair<0x01010000u, 0x010C000Cu>(sw[q], ew[q]);
-                o[q / 2][2 * (q % 2) + 1] = bf16_pair<0x03030202u, 0x030C020Cu>(sw[q], ew[q]);
+                const uint2 qq = bf16_quad(sw[q], ew[q]);
+                o[q / 2][2 * (q % 2)] = qq.x;
+                o[q / 2][2 * (q % 2) + 1] = qq.y;
             }
             v4u32* dst = reinterpret_cast<v4u32*>(out + 16 * v);
             __builtin_nontemporal_store(o[0], dst);
