@@ -2011,8 +2011,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 avail = lead + want;
                 nfull = avail / kGroup;
                 a0 = chunk_base + ob - lead;
-                const uint32_t n_active = g_active ? (RB + S - 1) / S : 1u;
-                if (i == n_active - 1) s_glast[0] = e;
+                // The last active thread (its segment ends the round), or
+                // thread 0 of an empty round, leaves its end.
+                if (g_active ? active && seg_hi == RB : i == 0) s_glast[0] = e;
                 __builtin_amdgcn_s_setprio(2);
                 // Compaction: the slot into registers (the dense area overlaps
                 // the slots), a barrier, then the symbols to their place.
@@ -2093,8 +2094,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                     cnt = a.n;
                 }
             }
-            const uint32_t n_active = g_active ? (RB + S - 1) / S : 1u;
-            if (i == n_active - 1) s_glast[g] = e;
+            if (g_active ? active && seg_hi == RB : i == 0) s_glast[g] = e;
             if constexpr (kMode == kModeIndex) {
                 // Index build: each segment's first boundary (0..15 bits
                 // past its start) and codeword count; no output.
