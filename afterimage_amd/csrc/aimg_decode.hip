@@ -787,13 +787,15 @@ __device__ __forceinline__ uint32_t last_word(const DevTensor& T) {
 // kTiny: the packed buffer has fewer than 4 bytes, so its words are read
 // byte by byte. Such tensors go to a kernel of their own, which keeps these
 // loads and their waits out of every other kernel's round loop.
-template <int kMode, bool kTiny>
+// kLg: threads per chunk as the kernel's (0: the job's own).
+template <int kMode, bool kTiny, uint32_t kLg>
 __device__ __forceinline__ void fetch_issue(Fetch& F, const LaunchArgs& args, const Job& J,
                                             uint32_t r, uint32_t tid) {
     if (round_len(J, r) == 0) return;
     const DevTensor& T = args.t[J.d];
-    const uint32_t tpc = 1u << J.lg;
-    const uint32_t b0 = ((r * J.S) << J.lg) / 8 + 4 * (tid & (tpc - 1));
+    const uint32_t lg = kLg > 0 ? kLg : J.lg;
+    const uint32_t tpc = 1u << lg;
+    const uint32_t b0 = ((r * J.S) << lg) / 8 + 4 * (tid & (tpc - 1));
     // All words are requested before any is used; words past the chunk read
     // an in-buffer word and are zeroed when written.
     if (!kTiny) {
@@ -816,7 +818,7 @@ __device__ __forceinline__ void fetch_issue(Fetch& F, const LaunchArgs& args, co
 // for every store issued in between.
 __device__ __forceinline__ void consume(uint32_t v) { asm volatile("" ::"v"(v)); }
 
-template <bool kTiny>
+template <bool kTiny, uint32_t kLg>
 __device__ __forceinline__ void fetch_commit(const Fetch& F, const LaunchArgs& args, const Job& J,
                                              uint32_t r, uint32_t tid, uint32_t* s_tile) {
 #pragma unroll
@@ -824,12 +826,15 @@ __device__ __forceinline__ void fetch_commit(const Fetch& F, const LaunchArgs& a
     const uint32_t RB = round_len(J, r);
     if (RB == 0) return;
     const DevTensor& T = args.t[J.d];
-    const uint32_t tpc = 1u << J.lg;
+    const uint32_t lg = kLg > 0 ? kLg : J.lg;
+    const uint32_t tpc = 1u << lg;
     const uint32_t i = tid & (tpc - 1);
-    uint32_t* top = tile_top(s_tile, tid >> J.lg, J.lg);
+    uint32_t* top = tile_top(s_tile, tid >> lg, lg);
     const uint32_t last = last_word(T);
-    const uint32_t b0 = ((r * J.S) << J.lg) / 8;
+    const uint32_t b0 = ((r * J.S) << lg) / 8;
     const uint32_t nw = (RB + 31) / 32 + 3;
+    // Words below nin lie wholly inside the chunk (b0 + 4 j + 4 <= nb).
+    const uint32_t nin = J.nb > b0 ? (J.nb - b0) / 4 : 0u;
 #pragma unroll
     for (uint32_t k = 0; k < kTileBatch; ++k) {
         const uint32_t j = k * tpc + i;
@@ -838,7 +843,7 @@ __device__ __forceinline__ void fetch_commit(const Fetch& F, const LaunchArgs& a
         uint32_t v = F.raw[k];
         // A word wholly inside the chunk was loaded from its own address
         // (A + 4 <= off + nb <= buffer size): only its byte order changes.
-        if (b + 4 <= J.nb) {
+        if (j < nin) {
             *(top - j) = __builtin_bswap32(v);
             continue;
         }
@@ -1828,10 +1833,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
     // The first item's words and table load together.
     Job cur = make_job<kMode, kLg>(args, blockIdx.x, tid);
     Fetch F;
-    fetch_issue<kMode, kTiny>(F, args, cur, cur.r0, tid);
+    fetch_issue<kMode, kTiny, kLg>(F, args, cur, cur.r0, tid);
     loaded = uniform(args.t[uniform(static_cast<uint32_t>(cur.d))].table);
     load_table(loaded, tid, s_wsyms, s_wmeta, s_len, s_esc);
-    fetch_commit<kTiny>(F, args, cur, cur.r0, tid, s_tile);
+    fetch_commit<kTiny, kLg>(F, args, cur, cur.r0, tid, s_tile);
 
     for (int64_t item = blockIdx.x; item < args.total_items; item += gridDim.x) {
         const DevTensor& T = args.t[uniform(static_cast<uint32_t>(cur.d))];
@@ -1899,8 +1904,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                     if (tid < lead) stage[tid] = static_cast<uint8_t>(lds.hand[4 + (tid >> 2)] >> (8 * (tid & 3u)));
                 } else {
                     r_begin = 0;
-                    fetch_issue<kMode, kTiny>(F, args, cur, 0, tid);
-                    fetch_commit<kTiny>(F, args, cur, 0, tid, s_tile);
+                    fetch_issue<kMode, kTiny, kLg>(F, args, cur, 0, tid);
+                    fetch_commit<kTiny, kLg>(F, args, cur, 0, tid, s_tile);
                 }
                 __syncthreads();
             }
@@ -1919,7 +1924,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             // agreement check and scan after, and the decode loops last (each
             // setting measured; 6.5% faster than equal priorities).
             __builtin_amdgcn_s_setprio(3);
-            fetch_issue<kMode, kTiny>(F, args, fj, fr, tid);
+            fetch_issue<kMode, kTiny, kLg>(F, args, fj, fr, tid);
             // Sign/mantissa bytes of every group this round can fill (its
             // output starts at a known element; its length is known only
             // after decoding), requested now so the store never waits.
@@ -2047,7 +2052,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                 if (ntail >= 2) *reinterpret_cast<uint16_t*>(tl) = static_cast<uint16_t>(tv);
                 if (ntail & 1u) tl[ntail - 1] = static_cast<uint8_t>(tv >> (8 * (ntail - 1)));
                 // Every thread is past its decode, so the tile takes the next words.
-                fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
+                fetch_commit<kTiny, kLg>(F, args, fj, fr, tid, s_tile);
                 __syncthreads();
             } else {
             __builtin_amdgcn_s_setprio(0);
@@ -2104,7 +2109,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
                         (cnt << 4) | (f - seg_lo), index_part(T, L.entries, 4 * L.capacity),
                         4u * (cur.ib + r * tpc + i), 0, 0);
                 }
-                fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
+                fetch_commit<kTiny, kLg>(F, args, fj, fr, tid, s_tile);
                 __syncthreads();
                 if (g_active) p0 = s_glast[g] - RB;
                 continue;
@@ -2158,7 +2163,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             for (uint32_t k = 0; k < 3; ++k)
                 if (k < ntail) tl[k] = static_cast<uint8_t>(tv >> (8 * k));
             // Every thread is past its decode, so the tile takes the next words.
-            fetch_commit<kTiny>(F, args, fj, fr, tid, s_tile);
+            fetch_commit<kTiny, kLg>(F, args, fj, fr, tid, s_tile);
             __syncthreads();
             }
 
@@ -2173,8 +2178,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void decode_kernel(const L
             if (g_active) p0 = e_last - RB;
         }
         if (r_begin == r_end) {
-            fetch_issue<kMode, kTiny>(F, args, nxt, nxt.r0, tid);
-            fetch_commit<kTiny>(F, args, nxt, nxt.r0, tid, s_tile);
+            fetch_issue<kMode, kTiny, kLg>(F, args, nxt, nxt.r0, tid);
+            fetch_commit<kTiny, kLg>(F, args, nxt, nxt.r0, tid, s_tile);
         }
 
         // Symbols carried out of the last round, then positions no codeword
